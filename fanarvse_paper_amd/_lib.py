@@ -1,0 +1,272 @@
+"""ctypes binding of libfvs.so (include/fvs.h) with host-side shape checks.
+
+Every wrapper takes torch tensors, checks device, dtype, contiguity and shapes before anything is
+launched, passes raw pointers plus torch's current stream, and raises RuntimeError on a non-zero
+return code. There is no fallback: if libfvs.so is missing or a tensor is not on the GPU, the call
+fails.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfvs.so")
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+U32 = ctypes.c_uint32
+
+# name -> argument types (return type is int for all but fvs_error_string)
+SIGNATURES = {
+    "fvs_abi_version": [],
+    "fvs_error_string": [ctypes.c_int],
+    "fvs_fill_u32": [P, I64, U32, P],
+    "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
+    "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
+    "fvs_route_topk": [P, I64, I32, I32, P, P],
+    "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, P, P, P],
+    "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
+    "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P],
+    "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
+    "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
+    "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
+    "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
+}
+
+_lib = None
+
+
+def lib():
+    """Load libfvs.so once; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               "(or python fanarvse_paper_amd/build.py)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name == "fvs_error_string" else ctypes.c_int
+        if L.fvs_abi_version() != 1:
+            raise RuntimeError("libfvs.so ABI version mismatch")
+        _lib = L
+    return _lib
+
+
+def _check(rc, name):
+    if rc != 0:
+        msg = lib().fvs_error_string(rc).decode()
+        raise RuntimeError(f"{name} failed: {msg} (code {rc})")
+
+
+def _stream():
+    return P(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t, dtype, name, shape=None, host_ok=False):
+    """Pointer of a contiguous tensor of the given dtype on the GPU (or pinned host if host_ok)."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    if not t.is_cuda and not (host_ok and t.is_pinned()):
+        raise ValueError(f"{name}: tensor must be on the GPU" + (" or in pinned host memory" if host_ok else ""))
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    return P(t.data_ptr())
+
+
+def _opt(t, dtype, name, shape=None):
+    return P(None) if t is None else _dev(t, dtype, name, shape)
+
+
+def _empty(shape, dtype, device):
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
+# ------------------------------------------------------------------------------------------- ops
+def fill_u32(t, value):
+    if t.element_size() != 4:
+        raise TypeError("fill_u32: 32-bit tensor expected")
+    _check(lib().fvs_fill_u32(_dev(t, t.dtype, "dst"), t.numel(), U32(value), _stream()), "fvs_fill_u32")
+
+
+def query_prep(Q, Vr, c):
+    """q8 [B,R] int8, qs [B], qc [B], qh [B,d] fp16 (throughput/enginei8.py:38, :62)."""
+    B, d = Q.shape
+    R = Vr.shape[1]
+    dev = Q.device
+    q8 = _empty((B, R), torch.int8, dev)
+    qs = _empty((B,), torch.float32, dev)
+    qc = _empty((B,), torch.float32, dev)
+    qh = _empty((B, d), torch.float16, dev)
+    _check(lib().fvs_query_prep(_dev(Q, torch.float32, "Q"), B, d, _dev(Vr, torch.float32, "Vr", (d, R)), R,
+                                _dev(c, torch.float32, "c", (d,)), _dev(q8, torch.int8, "q8"), _dev(qs, torch.float32, "qs"),
+                                _dev(qc, torch.float32, "qc"), _dev(qh, torch.float16, "qh"), _stream()),
+           "fvs_query_prep")
+    return q8, qs, qc, qh
+
+
+def build_codes(X16, order, cell, means16, Vr):
+    """Z [N,R] int8 and zs [N] of the cell residuals in sorted order (throughput/enginei8.py:19-27)."""
+    N = order.shape[0]
+    d = X16.shape[1]
+    NC = means16.shape[0]
+    R = Vr.shape[1]
+    if int(order.max()) >= X16.shape[0] or int(order.min()) < 0:
+        raise ValueError("build_codes: order out of range")
+    if int(cell.max()) >= NC or int(cell.min()) < 0:
+        raise ValueError("build_codes: cell out of range")
+    Z = _empty((N, R), torch.int8, X16.device)
+    zs = _empty((N,), torch.float32, X16.device)
+    _check(lib().fvs_build_codes(_dev(X16, torch.float16, "X16"), _dev(order, torch.int32, "order", (N,)),
+                                 _dev(cell, torch.int32, "cell", (N,)), N, d,
+                                 _dev(means16, torch.float16, "means16", (NC, d)), _dev(Vr, torch.float32, "Vr", (d, R)),
+                                 R, _dev(Z, torch.int8, "Z"), _dev(zs, torch.float32, "zs"), _stream()),
+           "fvs_build_codes")
+    return Z, zs
+
+
+def route_topk(QM, nprobe):
+    B, NC = QM.shape
+    probe = _empty((B, nprobe), torch.int32, QM.device)
+    _check(lib().fvs_route_topk(_dev(QM, torch.float16, "QM"), B, NC, nprobe, _dev(probe, torch.int32, "probe"),
+                                _stream()), "fvs_route_topk")
+    return probe
+
+
+def pairs(probe, n, NC, QM, mnorm):
+    """(qid, qrank, coff, ccnt, qcp) of the first n probe columns (throughput/enginei8.py:11-16)."""
+    B, npr = probe.shape
+    dev = probe.device
+    if QM.shape != (B, NC):
+        raise ValueError("pairs: QM shape")
+    ccnt = _empty((NC,), torch.int32, dev)
+    coff = _empty((NC,), torch.int32, dev)
+    fill = _empty((NC,), torch.int32, dev)
+    qid = _empty((B * n,), torch.int32, dev)
+    qrank = _empty((B * n,), torch.int32, dev)
+    qcp = _empty((B * n,), torch.float32, dev)
+    _check(lib().fvs_pairs(_dev(probe, torch.int32, "probe"), B, npr, n, NC, _dev(QM, torch.float16, "QM"),
+                           _opt(mnorm, torch.float32, "mnorm", (NC,)), _dev(ccnt, torch.int32, "ccnt"),
+                           _dev(coff, torch.int32, "coff"), _dev(fill, torch.int32, "fill"),
+                           _dev(qid, torch.int32, "qid"), _dev(qrank, torch.int32, "qrank"),
+                           _dev(qcp, torch.float32, "qcp"), _stream()), "fvs_pairs")
+    return qid, qrank, coff, ccnt, qcp
+
+
+def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1, MB=1, n1=1):
+    """First pass (mode 0) or emit (mode 1) over the static (cell, block) items (throughput/civf8.py:89-91).
+
+    `blocks` must come from index.static_blocks over the same index as Z (its rows lie inside Z);
+    no host synchronisation happens here, so the call can be captured in a graph."""
+    pcell, pblk, ps, pe = blocks
+    qid, qrank, coff, ccnt, qcp = pr
+    P_ = pcell.shape[0]
+    N, R = Z.shape
+    if q8.shape[1] != R:
+        raise ValueError("i8_scan: code width mismatch")
+    B = q8.shape[0]
+    if mode == 0 and (bm is None or bm.numel() != B * n1 * MB):
+        raise ValueError("i8_scan: bm must hold B*n1*MB values")
+    if mode == 1 and (bval is None or bval.shape != (B, CAP) or bpos.shape != (B, CAP) or cnt.shape != (B,)):
+        raise ValueError("i8_scan: emit buffers must be [B, CAP]")
+    f32, i32 = torch.float32, torch.int32
+    _check(lib().fvs_i8_scan(mode, P_, _dev(q8, torch.int8, "q8"), _dev(qs, f32, "qs", (B,)), _dev(qid, i32, "qid"),
+                             _dev(qrank, i32, "qrank"), _dev(coff, i32, "coff"), _dev(ccnt, i32, "ccnt"),
+                             _dev(pcell, i32, "pcell"), _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"),
+                             _dev(pe, i32, "pe"), _dev(Z, torch.int8, "Z"), _dev(zs, f32, "zs", (N,)), N, R,
+                             _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"),
+                             _opt(bval, f32, "bval"), _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1,
+                             _stream()), "fvs_i8_scan")
+
+
+def threshold(bm, probe, off, n1, MB, r):
+    B, npr = probe.shape
+    t0 = _empty((B,), torch.float32, probe.device)
+    _check(lib().fvs_threshold(_dev(bm, torch.float32, "bm"), _dev(probe, torch.int32, "probe"), npr,
+                               _dev(off, torch.int32, "off"), B, n1, MB, r, _dev(t0, torch.float32, "t0"), _stream()),
+           "fvs_threshold")
+    return t0
+
+
+def select(bval, bpos, cnt, K, kd, delta):
+    B, M = bval.shape
+    dev = bval.device
+    pos = _empty((B, K), torch.int32, dev)
+    est1 = _empty((B, K), torch.float32, dev)
+    ok = _empty((B,), torch.uint8, dev)
+    ncnt = _empty((B,), torch.int32, dev)
+    _check(lib().fvs_select(_dev(bval, torch.float32, "bval"), _dev(bpos, torch.int32, "bpos", (B, M)),
+                            _dev(cnt, torch.int32, "cnt", (B,)), B, M, K, kd, F32(-1.0 if delta is None else delta),
+                            _dev(pos, torch.int32, "pos"), _dev(est1, torch.float32, "est1"),
+                            _dev(ok, torch.uint8, "ok"), _dev(ncnt, torch.int32, "ncnt"), _stream()), "fvs_select")
+    return pos, est1, ok, ncnt
+
+
+def _tiers_arr(TS):
+    arr = (ctypes.c_int32 * (3 * len(TS)))()
+    for t, (s, e, b) in enumerate(TS):
+        arr[3 * t], arr[3 * t + 1], arr[3 * t + 2] = int(s), int(e), int(b)
+    return arr
+
+
+def lut_build(Zq, TS, half):
+    """L [B, D/4*16] (fp16 if half), qsum, qn2 [T, B] (throughput/s2lut.py:118-126)."""
+    B, D = Zq.shape
+    dev = Zq.device
+    L = _empty((B, D // 4 * 16), torch.float16 if half else torch.float32, dev)
+    qsum = _empty((len(TS), B), torch.float32, dev)
+    qn2 = _empty((len(TS), B), torch.float32, dev)
+    _check(lib().fvs_lut_build(_dev(Zq, torch.float16, "Zq"), B, D, len(TS), _tiers_arr(TS), int(bool(half)),
+                               _dev(L, L.dtype, "L"), _dev(qsum, torch.float32, "qsum"),
+                               _dev(qn2, torch.float32, "qn2"), _stream()), "fvs_lut_build")
+    return L, qsum, qn2
+
+
+def lut_score(pos, qc, pre, code, ncnt=None):
+    """(est, sd) [B, K] of the candidates (throughput/s2lut.py:92-106), from the packed records."""
+    L, qsum, qn2 = pre
+    B, K = pos.shape
+    TS = code["TS"]
+    T = len(TS)
+    rec = code["rec"]
+    N, RB = rec.shape
+    half = L.dtype == torch.float16
+    deltas = (ctypes.c_float * T)(*[float(code["deltas"][b]) for _, _, b in TS])
+    toff = (ctypes.c_int32 * T)(*[int(x) for x in code["toff"]])
+    est = _empty((B, K), torch.float32, pos.device)
+    sd = _empty((B, K), torch.float32, pos.device)
+    _check(lib().fvs_lut_score(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
+                               _dev(L, L.dtype, "L"), int(half), L.shape[1], _dev(qsum, torch.float32, "qsum", (T, B)),
+                               _dev(qn2, torch.float32, "qn2", (T, B)), _dev(rec, torch.uint8, "rec"), N, RB,
+                               int(code["soff"]), T, _tiers_arr(TS), deltas, toff,
+                               _opt(ncnt, torch.int32, "ncnt", (B,)), B, K, _dev(est, torch.float32, "est"),
+                               _dev(sd, torch.float32, "sd"), _stream()), "fvs_lut_score")
+    return est, sd
+
+
+def refine(est, sd, pos, order, H, Q, z, k):
+    """(ids [B,K], I [B,k], scores [B,k], reads [B]) (throughput/enginei8.py:92-95, src/stage3_zc.py)."""
+    B, K = est.shape
+    d = Q.shape[1]
+    if H.shape[1] != d:
+        raise ValueError("refine: H width")
+    dev = est.device
+    ids = _empty((B, K), torch.int32, dev)
+    I = _empty((B, k), torch.int32, dev)
+    scores = _empty((B, k), torch.float32, dev)
+    reads = _empty((B,), torch.int32, dev)
+    _check(lib().fvs_refine(_dev(est, torch.float32, "est"), _dev(sd, torch.float32, "sd", (B, K)),
+                            _dev(pos, torch.int32, "pos", (B, K)), _dev(order, torch.int32, "order"),
+                            _dev(H, torch.float16, "H", host_ok=True), _dev(Q, torch.float32, "Q", (B, d)), B, K, d,
+                            F32(z), k, _dev(ids, torch.int32, "ids"), _dev(I, torch.int32, "I"),
+                            _dev(scores, torch.float32, "scores"), _dev(reads, torch.int32, "reads"), _stream()),
+           "fvs_refine")
+    return ids, I, scores, reads

@@ -1,0 +1,140 @@
+// Device helpers shared by the libfvs kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fvs.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+#define FVS_WAVE 64
+
+// Return the launch status of the kernel just enqueued (0 on success).
+static inline int fvs_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+__device__ __forceinline__ float fvs_h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t fvs_f2h(float f) {  // round to nearest even
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Order-preserving maps to unsigned keys (larger float -> larger key); -0 is mapped like +0.
+__device__ __forceinline__ uint32_t fvs_ord32(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fvs_unord32(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ uint32_t fvs_ord16(uint16_t u) {
+  if (u == 0x8000u) u = 0u;
+  return (u & 0x8000u) ? (uint32_t)((~u) & 0xffffu) : (uint32_t)(u | 0x8000u);
+}
+
+__device__ __forceinline__ float fvs_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, FVS_WAVE));
+  return v;
+}
+
+// Inclusive prefix sum over threadIdx.x for a 256-thread block. tmp: 4 ints of LDS.
+__device__ __forceinline__ int fvs_block_scan256(int v, int *tmp) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(v, o, FVS_WAVE);
+    if (lane >= o) v += t;
+  }
+  if (lane == 63) tmp[w] = v;
+  __syncthreads();
+  int add = 0;
+  for (int i = 0; i < w; i++) add += tmp[i];
+  __syncthreads();
+  return v + add;
+}
+
+// k-th largest (1-based, counted with multiplicity) of n keys key(i), 1 <= k <= n, by an MSD radix
+// select of 8 bits per pass. Block of 256 threads; hist: 256 ints of LDS, sh: 8 ints of LDS.
+// Every thread returns the same key.
+template <typename KT, typename F>
+__device__ KT fvs_block_kth(F key, int n, int k, int *hist, int *sh) {
+  KT prefix = 0, pmask = 0;
+  for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
+    hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+      KT x = key(i);
+      if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
+    }
+    __syncthreads();
+    const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
+    const int h = hist[b];
+    const int inc = fvs_block_scan256(h, sh);
+    const int exc = inc - h;
+    if (exc < k && k <= inc) {
+      sh[4] = b;
+      sh[5] = k - exc;
+    }
+    __syncthreads();
+    prefix |= (KT)sh[4] << shift;
+    pmask |= (KT)0xff << shift;
+    k = sh[5];
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// In-place bitonic sort of n (a power of two) keys in LDS, descending when DESC. Any block size.
+template <typename KT, bool DESC>
+__device__ void fvs_block_bitonic(KT *s, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const KT a = s[i], b = s[ixj];
+          const bool first = (i & k) == 0;  // this pair is ordered like the final order
+          const bool swap = DESC ? (first ? a < b : a > b) : (first ? a > b : a < b);
+          if (swap) {
+            s[i] = b;
+            s[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__host__ __device__ __forceinline__ int fvs_pow2_ceil(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
+// Requires kk <= n. Block of 256 threads; cnt: 1 int of LDS.
+template <typename F>
+__device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
+  const int P = fvs_pow2_ceil(kk);
+  const uint64_t kth = fvs_block_kth<uint64_t>(key, n, kk, hist, sh);
+  if (threadIdx.x == 0) *cnt = 0;
+  for (int i = threadIdx.x; i < P; i += 256) s[i] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const uint64_t x = key(i);
+    if (x >= kth) {
+      const int slot = atomicAdd(cnt, 1);
+      if (slot < P) s[slot] = x;  // keys are unique, so exactly kk of them pass
+    }
+  }
+  __syncthreads();
+  fvs_block_bitonic<uint64_t, true>(s, P);
+}

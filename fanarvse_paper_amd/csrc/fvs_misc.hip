@@ -1,0 +1,33 @@
+// Version, error strings and a graph-capturable fill.
+#include "fvs_common.h"
+
+namespace {
+
+__global__ void k_fill_u32(uint32_t *__restrict__ dst, int64_t n, uint32_t value) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = value;
+}
+
+}  // namespace
+
+extern "C" int fvs_abi_version(void) { return FVS_ABI_VERSION; }
+
+extern "C" const char *fvs_error_string(int code) {
+  switch (code) {
+    case FVS_OK: return "ok";
+    case FVS_E_ARG: return "argument out of range";
+    case FVS_E_SHAPE: return "unsupported shape";
+    case FVS_E_CAPACITY: return "per-workgroup capacity exceeded";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}
+
+extern "C" int fvs_fill_u32(void *dst, int64_t n, uint32_t value, void *stream) {
+  if (n < 0) return FVS_E_ARG;
+  if (n == 0) return FVS_OK;
+  if (!dst) return FVS_E_ARG;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (uint32_t *)dst, n, value);
+  return fvs_launch_status();
+}

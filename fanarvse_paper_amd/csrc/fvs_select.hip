@@ -1,0 +1,122 @@
+// Threshold t0 from the first-pass block maxima, and the final stage-1 top-K selection.
+#include "fvs_common.h"
+
+namespace {
+
+constexpr int kMaxK = 4096;     // LDS capacity of the sorted top-K
+constexpr int kMaxN1 = 4096;
+
+__device__ __forceinline__ int cell_blocks(const int32_t *off, int c) {
+  const int s = off[c], e = off[c + 1];
+  return e > s ? (e - 1) / 32 - s / 32 + 1 : 0;
+}
+
+// One block per query. Valid values: bm[q][j][b], j < n1, b < blocks(probe[q][j]).
+__global__ __launch_bounds__(256) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
+                                                   int npr, const int32_t *__restrict__ off, int n1, int MB, int r,
+                                                   float *__restrict__ t0) {
+  __shared__ int nb[kMaxN1];
+  __shared__ int hist[256];
+  __shared__ int sh[8];
+  const int64_t q = blockIdx.x;
+  int mine = 0;
+  for (int j = threadIdx.x; j < n1; j += 256) {
+    nb[j] = cell_blocks(off, probe[q * npr + j]);
+    mine += nb[j];
+  }
+  // block sum of the valid counts
+  const int tot = fvs_block_scan256(mine, sh);
+  if (threadIdx.x == 255) sh[6] = tot;
+  __syncthreads();
+  const int nv = sh[6];
+  __syncthreads();
+  const int n = n1 * MB;
+  const float *row = bm + q * (int64_t)n;
+  auto key = [&](int i) -> uint32_t {
+    const int j = i / MB, b = i - j * MB;
+    return b < nb[j] ? fvs_ord32(row[i]) : 0u;
+  };
+  const int kk = min(min(r, n), nv);
+  float out = 1e30f;
+  if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t>(key, n, kk, hist, sh));
+  if (threadIdx.x == 0) t0[q] = out;
+}
+
+// One block per query: top-K of the first min(cnt, M) buffer entries by (est desc, pos asc).
+__global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, const int32_t *__restrict__ bpos,
+                                                const int32_t *__restrict__ cntp, int M, int K, int kd, float delta,
+                                                int32_t *__restrict__ pos, float *__restrict__ est1,
+                                                uint8_t *__restrict__ ok, int32_t *__restrict__ ncnt) {
+  __shared__ uint64_t s[kMaxK];
+  __shared__ int hist[256];
+  __shared__ int sh[8];
+  __shared__ int gcnt;
+  const int64_t q = blockIdx.x;
+  const int cq = cntp[q];
+  const int n = min(cq, M);
+  const float *bv = bval + q * (int64_t)M;
+  const int32_t *bp = bpos + q * (int64_t)M;
+  auto key = [&](int i) -> uint64_t {
+    return ((uint64_t)fvs_ord32(bv[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)bp[i]);
+  };
+  int have;
+  if (n >= K) {
+    fvs_block_topk_u64(key, n, K, s, hist, sh, &gcnt);
+    have = K;
+  } else {
+    const int P = fvs_pow2_ceil(n > 0 ? n : 1);
+    for (int i = threadIdx.x; i < P; i += 256) s[i] = i < n ? key(i) : 0ull;
+    __syncthreads();
+    fvs_block_bitonic<uint64_t, true>(s, P);
+    have = n;
+  }
+  float *e1 = est1 + q * (int64_t)K;
+  int32_t *po = pos + q * (int64_t)K;
+  for (int i = threadIdx.x; i < K; i += 256) {
+    if (i < have) {
+      const uint64_t x = s[i];
+      e1[i] = fvs_unord32((uint32_t)(x >> 32));
+      po[i] = (int32_t)(0xffffffffu - (uint32_t)(x & 0xffffffffu));
+    } else {
+      e1[i] = -1e30f;
+      po[i] = 0;
+    }
+  }
+  if (threadIdx.x == 0) ok[q] = (uint8_t)(cq >= K && cq <= M);
+  if (delta >= 0.f) {
+    auto est_at = [&](int i) -> float { return i < have ? fvs_unord32((uint32_t)(s[i] >> 32)) : -1e30f; };
+    const float thr = est_at(kd) - delta;
+    int mine = 0;
+    for (int i = threadIdx.x; i < K; i += 256) mine += (est_at(i) >= thr) ? 1 : 0;
+    const int tot = fvs_block_scan256(mine, sh);
+    if (threadIdx.x == 255) ncnt[q] = tot;
+  } else if (threadIdx.x == 0) {
+    ncnt[q] = K;
+  }
+}
+
+}  // namespace
+
+extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
+                             int32_t n1, int32_t MB, int32_t r, float *t0, void *stream) {
+  if (B < 0 || n1 <= 0 || n1 > npr || MB <= 0 || r <= 0) return FVS_E_ARG;
+  if (n1 > kMaxN1) return FVS_E_CAPACITY;
+  if ((int64_t)n1 * MB > (int64_t)1 << 30) return FVS_E_ARG;
+  if (B == 0) return FVS_OK;
+  if (!bm || !probe || !off || !t0) return FVS_E_ARG;
+  hipLaunchKernelGGL(k_threshold, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, n1, MB, r,
+                     t0);
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64_t B, int32_t M, int32_t K,
+                          int32_t kd, float delta, int32_t *pos, float *est1, uint8_t *ok, int32_t *ncnt,
+                          void *stream) {
+  if (B < 0 || M <= 0 || K <= 0 || kd < 0 || kd >= K) return FVS_E_ARG;
+  if (K > kMaxK) return FVS_E_CAPACITY;
+  if (B == 0) return FVS_OK;
+  if (!bval || !bpos || !cnt || !pos || !est1 || !ok || !ncnt) return FVS_E_ARG;
+  hipLaunchKernelGGL(k_select, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bval, bpos, cnt, M, K, kd, delta,
+                     pos, est1, ok, ncnt);
+  return fvs_launch_status();
+}

@@ -1,0 +1,213 @@
+"""EngineI8 on MI355X: the throughput-mode batched search of FanarVSE (FanarVSE-T).
+
+Same entry points and knobs as the reference (throughput/enginei8.py:29-122):
+    E = EngineI8(s1, code, Z, zs, Vr); E.H = <fp16 vectors in id order>
+    I, reads, cand_ids = E.search(Qb, K, z, nprobe, k)
+The search is one hipGraph replay per (B, K, z, nprobe, k) followed by one host synchronisation on
+the exactness flags; flagged queries are recomputed by _fallback (rho = 1, beta = 1.5, a 65,536-entry
+buffer, an fp32 LUT and no delta rule), as in the reference. Every stage runs in libfvs kernels; the
+two plain fp16 GEMMs (routing scores and the rotated tier queries) use torch's BLAS.
+
+The class attributes default to the final operating point of throughput/e_v3final.py:16,28-30
+(NROUTE, LUTF, LUTH, DELTA = 0.07, RHO = 0.6, MSZ = 3072). Variants this build does not implement
+(PROJ, K2, routing without NROUTE) raise NotImplementedError instead of silently changing results.
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import _lib, index, s2lut
+
+
+def pairs_fast(probe, NC, QM, scale=None):
+    """(qid, coff, ccnt, qc, qrank) of the (query, cell) pairs, grouped by cell with queries ascending
+    (throughput/enginei8.py:11-16). `qrank` replaces the permutation `o`: it is the rank of the cell in
+    the query's probe row, which is all the first pass needs to place its block maxima."""
+    qid, qrank, coff, ccnt, qcp = _lib.pairs(probe, probe.shape[1], NC, QM, scale)
+    return qid, coff, ccnt, qcp, qrank
+
+
+class EngineI8:
+    BQ, BN = 32, 32
+    PROJ = False
+    UNSORTED = False
+    CUDA = False
+    FASTPAIRS = True
+    NW = 2
+    SORTROUTE = False
+    MSZ = 3072
+    ROUTE16 = True
+    LUTF = True
+    K2 = None
+    NT = 3
+    BETA = None
+    RHO = 0.6
+    NROUTE = True
+    DELTA = 0.07
+    LUTH = True
+
+    def __init__(self, s1, code, Z, zs, Vr, H=None):
+        if self.BN != 32:
+            raise NotImplementedError("the MFMA scan uses 32-row blocks")
+        self.s1, self.code, self.Z, self.zs, self.Vr = s1, code, Z, zs, Vr.contiguous()
+        self.H = H
+        s2lut.prepare_u(code)
+        self.blocks, self.MB = index.static_blocks(s1["off_t"], self.BN)
+        N = Z.shape[0]
+        if int(s1["off_t"][-1]) != N or int(self.blocks[3].max()) > N:
+            raise ValueError("EngineI8: cell offsets do not match the code rows")
+        self.meansN = (s1["means16"].float() * s1["inv_mnorm"][:, None]).half().contiguous()
+        self.mnorm = (1.0 / s1["inv_mnorm"]).float().contiguous()
+        self.graphs = {}
+        self.nbad = 0
+        self.nbad2 = 0
+
+    # ------------------------------------------------------------------ stages
+    def _check_knobs(self):
+        if self.PROJ:
+            raise NotImplementedError("PROJ routing is not implemented")
+        if self.K2 is not None:
+            raise NotImplementedError("progressive stage 2 (K2) is not implemented")
+        if not self.NROUTE:
+            raise NotImplementedError("only NROUTE routing (normalised cell means) is implemented")
+
+    def _params(self, K, nprobe, rho_override=None, M_override=None):
+        NC = len(self.s1["off"]) - 1
+        N = self.Z.shape[0]
+        M = M_override or self.MSZ or max(4096, 16 * K)
+        beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
+        if self.BETA:
+            beta = self.BETA
+        if self.RHO:
+            rho = self.RHO
+        if rho_override:
+            beta, rho = 1.5, rho_override
+        n1 = min(max(int(np.ceil(beta * K / (N / NC / self.BN + 1))), 1), nprobe)
+        r = int(np.ceil(rho * K))
+        return M, n1, r
+
+    def stage1_i8(self, Qb, QM, probe, K, rho_override=None, M_override=None, qp=None, delta=None, kd=9):
+        """Threshold-and-emit stage 1 (throughput/enginei8.py:36-60). Returns (pos [B,K] int32, ok bool);
+        sets self._est1 and self._ncnt (the delta-rule count, K when delta is None)."""
+        s1 = self.s1
+        NC = len(s1["off"]) - 1
+        B = Qb.shape[0]
+        q8, qs, _, _ = qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"])
+        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
+        pr = _lib.pairs(probe, n1, NC, QM, self.mnorm)
+        bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=Qb.device)
+        _lib.i8_scan(0, self.blocks, q8, qs, pr, self.Z, self.zs, bm=bm, MB=self.MB, n1=n1)
+        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
+        cnt = torch.empty((B,), dtype=torch.int32, device=Qb.device)
+        _lib.fill_u32(cnt, 0)
+        bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
+        bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
+        pr = _lib.pairs(probe, probe.shape[1], NC, QM, self.mnorm)
+        _lib.i8_scan(1, self.blocks, q8, qs, pr, self.Z, self.zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
+        pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, min(kd, K - 1), delta)
+        self._est1, self._ncnt, self._t0, self._cnt = est1, ncnt, t0, cnt
+        self._bm, self._bval, self._bpos, self._n1, self._M = bm, bval, bpos, n1, M
+        return pos, ok.bool()
+
+    def _route(self, Qh, nprobe):
+        QM = Qh @ self.meansN.T
+        return QM, _lib.route_topk(QM, nprobe)
+
+    def _gpu(self, Qb, K, z, nprobe, k):
+        """One batch on the GPU without host synchronisation: (ok, I, reads, ids, scores, QM, Zq); the two
+        BLAS products are returned so that the fallback reuses their rows."""
+        self._check_knobs()
+        if self.H is None:
+            raise RuntimeError("EngineI8.H (fp16 vectors in id order) must be set before searching")
+        s1 = self.s1
+        qp = _lib.query_prep(Qb, self.Vr, s1["c"])
+        q8, qs, QC, Qh = qp
+        QM, probe = self._route(Qh, nprobe)
+        pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
+        Zq = s2lut.rotate(self.code, Qh)
+        ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=self.LUTF and self.LUTH,
+                                                 ncnt=self._ncnt if self.DELTA is not None else None)
+        return ok, I, reads, ids, scores, QM, Zq
+
+    def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt):
+        """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95)."""
+        pre = _lib.lut_build(Zq, self.code["TS"], half)
+        est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
+        self._est, self._sd = est, sd
+        ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
+        return ok, I, reads, ids, scores
+
+    # ------------------------------------------------------------------ entry point
+    def search(self, Qb, K, z, nprobe, k, ret_est=False, ret_scores=False):
+        """(I [B,k] ids, reads [B], cand_ids [B,K]) (+ scores [B,k] when ret_scores): the exact scores of
+        the picks read in full precision, the stage-2 estimates of the surely-in ones."""
+        Qb = Qb.float().contiguous()
+        B = len(Qb)
+        key = (B, K, float(z), nprobe, k)
+        if key not in self.graphs:
+            qs = Qb.clone()
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                for _ in range(3):
+                    self._gpu(qs, K, z, nprobe, k)
+            torch.cuda.current_stream().wait_stream(st)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs = self._gpu(qs, K, z, nprobe, k)
+            self.graphs[key] = (g, qs, outs)
+        g, qs, (ok, I, nr, ids, sc, QM, Zq) = self.graphs[key]
+        qs.copy_(Qb)
+        g.replay()
+        I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
+        if not bool(ok.all()):
+            bad = torch.nonzero(~ok).flatten()
+            self.nbad += len(bad)
+            a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, QM[bad].contiguous(), Zq[bad].contiguous())
+            I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
+        return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
+
+    def _fallback(self, Qb, K, z, nprobe, k, QM=None, Zq=None):
+        """Flagged queries again with r = K, n1 over 1.5K blocks, M = 65,536, an fp32 LUT and every
+        candidate scored (throughput/enginei8.py:112-120). QM / Zq: the rows of the main pass's BLAS
+        products for these queries (recomputed when not given)."""
+        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
+        q8, qs, QC, Qh = qp
+        if QM is None:
+            QM = Qh @ self.meansN.T
+        probe = _lib.route_topk(QM, nprobe)
+        if Zq is None:
+            Zq = s2lut.rotate(self.code, Qh)
+        pos, ok = self.stage1_i8(Qb, QM, probe, K, rho_override=1.0, M_override=65536, qp=qp, delta=None)
+        ok2, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=False, ncnt=None)
+        self.nbad2 += int((~ok).sum())
+        return I, reads, ids, scores
+
+    def trace(self, Qb, K, z, nprobe, k):
+        """Eager run of one batch that returns every intermediate (for parity tests and profiling)."""
+        self._check_knobs()
+        Qb = Qb.float().contiguous()
+        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
+        q8, qs, QC, Qh = qp
+        QM, probe = self._route(Qh, nprobe)
+        pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
+        half = self.LUTF and self.LUTH
+        ncnt = self._ncnt if self.DELTA is not None else None
+        Zq = s2lut.rotate(self.code, Qh)
+        pre = _lib.lut_build(Zq, self.code["TS"], half)
+        est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
+        ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
+        return dict(q8=q8, qs=qs, QC=QC, Qh=Qh, QM=QM, probe=probe, bm=self._bm, n1=self._n1, M=self._M,
+                    t0=self._t0, cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, est1=self._est1, ok=ok,
+                    ncnt=self._ncnt, Zq=Zq, L=pre[0], qsum=pre[1], qn2=pre[2], est=est, sd=sd, ids=ids, I=I,
+                    scores=scores, reads=reads)
+
+    def gpu_bytes(self):
+        """Bytes per vector kept on the GPU by the search tables (int8 code + scale, record, id), as the
+        reference's memory accounting (throughput/enginei8.py:121-122)."""
+        N = self.Z.shape[0]
+        per = self.Z.shape[1] + 4 + self.code["RB"] + 4
+        tables = (self.meansN.numel() * 2 + self.mnorm.numel() * 4 + self.Vr.numel() * 4 +
+                  self.code["VP16"].numel() * 2)
+        return per + tables / N

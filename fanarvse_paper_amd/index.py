@@ -1,0 +1,102 @@
+"""Index build for the throughput-mode search path (runs once; its outputs are the tables the kernels read).
+
+Mirrors, in order:
+  * global centre c = mean of the first 50k vectors (src/rev_fanardb.py:37);
+  * 4,096-cell spherical k-means over a 200k sample, 15 iterations, then every vector assigned to its
+    best cell and the index sorted by cell (src/ideas_engine2.py:27-40);
+  * cell means of the members (src/engine_cell.py:8-15) and their norms (src/engine_cell.py:26-32);
+  * the tiered refinement code with uniform codebooks (throughput/s2lut.py:18-29, src/tiered.py);
+  * the 256-direction PCA basis of the int8 code (throughput/e_brute.py:71-73) and the int8
+    cell-residual codes (throughput/enginei8.py:19-27, on the GPU through libfvs);
+  * the static (cell, block) work list (src/s1cell.py:157-168).
+Random draws use numpy PCG64 seeds (the reference draws some from a CUDA generator, which cannot be
+reproduced on another device).
+"""
+import numpy as np
+import torch
+
+from . import _lib, s2lut
+
+
+def spherical_kmeans(X16, nlist, seed=0, iters=15, sample=200000, chunk=50000):
+    """Spherical k-means centroids (unit rows) fitted on a random sample (src/ideas_engine2.py:27-33)."""
+    g = np.random.default_rng(seed)
+    N = X16.shape[0]
+    idx = torch.from_numpy(g.permutation(N)[:sample]).to(X16.device)
+    samp = X16[idx].float()
+    cen = samp[torch.from_numpy(g.permutation(len(samp))[:nlist]).to(X16.device)].clone()
+    for _ in range(iters):
+        a = torch.cat([(samp[j:j + chunk] @ cen.T).argmax(1) for j in range(0, len(samp), chunk)])
+        cen = torch.nn.functional.normalize(torch.zeros_like(cen).index_add_(0, a, samp) + 1e-9, dim=1)
+    return cen
+
+
+def assign(X16, cen, chunk=100000):
+    return torch.cat([(X16[j:j + chunk].float() @ cen.T).argmax(1) for j in range(0, X16.shape[0], chunk)])
+
+
+def build_stage1_cells(X16, nlist=4096, seed=0):
+    """Stage-1 tables: c, order (sorted position -> id, int32), off (numpy int64 [NC+1]), off_t (int32
+    tensor), cell (cell of each sorted position), means16 (fp16 cell means), inv_mnorm."""
+    dev = X16.device
+    N = X16.shape[0]
+    c = X16[:50000].float().mean(0)
+    cen = spherical_kmeans(X16, nlist, seed)
+    A = assign(X16, cen)
+    order = torch.argsort(A, stable=True)
+    off = torch.searchsorted(A[order].contiguous(), torch.arange(nlist + 1, device=dev))
+    cell = A[order]
+    means = torch.zeros(nlist, X16.shape[1], device=dev)
+    for j in range(0, N, 65536):
+        means.index_add_(0, cell[j:j + 65536], X16[order[j:j + 65536]].float())
+    cnt = (off[1:] - off[:-1]).clamp(min=1).float()
+    means /= cnt[:, None]
+    means16 = means.half().contiguous()
+    inv_mnorm = (1.0 / means16.float().norm(dim=1).clamp(min=1e-12)).contiguous()
+    return dict(c=c.contiguous(), order=order.to(torch.int32).contiguous(), off=off.cpu().numpy().astype(np.int64),
+                off_t=off.to(torch.int32).contiguous(), cell=cell.to(torch.int32).contiguous(), means16=means16,
+                inv_mnorm=inv_mnorm)
+
+
+def pca_int8_basis(X16, R=256, nmean=200000, step=10):
+    """Top-R principal directions of x - mu, mu = mean of the first 200k vectors, covariance of every
+    10th vector (throughput/e_brute.py:71-73). The eigendecomposition runs in float64 on the host."""
+    mu = X16[:nmean].float().mean(0)
+    S = X16[::step].float() - mu
+    cov = torch.cov(S.T).double().cpu().numpy()
+    ev, V = np.linalg.eigh(cov)
+    V = V[:, ::-1][:, :R].copy()
+    return torch.from_numpy(V).float().to(X16.device).contiguous()
+
+
+def build_codes(s1, X16, Vr):
+    """int8 codes of the cell residuals in sorted order and their scales (throughput/enginei8.py:19-27)."""
+    return _lib.build_codes(X16, s1["order"], s1["cell"], s1["means16"], Vr.contiguous())
+
+
+def static_blocks(off_t, BN=32):
+    """All (cell, block) items of the index: cell, global block id, cell start and end, and MB = max blocks
+    per cell + 1 (src/s1cell.py:161-168)."""
+    off = off_t.long()
+    s, e = off[:-1], off[1:]
+    nb = torch.where(e > s, (e - 1) // BN - s // BN + 1, torch.zeros_like(s))
+    cell = torch.repeat_interleave(torch.arange(len(s), device=off.device), nb)
+    first = torch.cumsum(nb, 0) - nb
+    blk = s[cell] // BN + torch.arange(len(cell), device=off.device) - first[cell]
+    MB = int((int((e - s).max()) + BN - 1) // BN + 1)
+    i32 = lambda x: x.to(torch.int32).contiguous()
+    return (i32(cell), i32(blk), i32(s[cell]), i32(e[cell])), MB
+
+
+def build_index(X16, nlist=4096, R=256, bits_per_dim=2.5, seed=0, with_codes=True):
+    """Everything EngineI8 needs: (s1, code, Z, zs, Vr). X16: fp16 [N, d] in id order."""
+    s1 = build_stage1_cells(X16, nlist, seed)
+    lam, V = s2lut.pca_basis(X16, s1["c"])
+    TS = s2lut.allocate(lam, int(bits_per_dim * X16.shape[1]))
+    code = s2lut.encode_uniform(X16, s1["order"], s1["c"], V, TS, seed)
+    s2lut.prepare_u(code)
+    Vr = pca_int8_basis(X16, R)
+    Z = zs = None
+    if with_codes:
+        Z, zs = build_codes(s1, X16, Vr)
+    return s1, code, Z, zs, Vr

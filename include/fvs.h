@@ -1,0 +1,188 @@
+/*
+ * fvs.h - C ABI of libfvs.so, the MI355X (gfx950) kernels of the FanarVSE batched search path
+ * (route -> int8 cell-residual stage 1 with threshold-and-emit -> LUT stage 2 with error bars
+ * -> exact fp16 refinement of the ambiguous candidates).
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers unless a comment says otherwise (the refine entry point also
+ *     accepts a pinned, device-mapped host pointer for the fp16 rows).
+ *   - Sizes are plain integers; `stream` is a hipStream_t passed as void* (torch's
+ *     torch.cuda.current_stream().cuda_stream), the way the reference hands torch's stream to
+ *     its CUDA twin (throughput/civf8.py:89-91).
+ *   - Every call returns 0 on success, a positive hipError_t if a launch failed, or a negative
+ *     FVS_E_* code when an argument is out of range (nothing is launched then).
+ *   - The library never allocates, frees or synchronises: every buffer, scratch included, is
+ *     owned by the caller, so a whole search can be captured in one hipGraph. Calls are reentrant
+ *     (no mutable global state); calls that share an output buffer must be ordered by the caller.
+ *   - fp16 data is passed as uint16_t (IEEE binary16 bit patterns).
+ *
+ * Determinism: every floating-point result has one canonical operation order, written next to
+ * each entry point; the CPU checker under oracle/ follows the same order, so results are
+ * bit-identical for identical inputs. The order in which the emit pass appends candidates is
+ * not deterministic (atomics), as in the reference; everything read back from the buffer is.
+ */
+#ifndef FVS_H
+#define FVS_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FVS_ABI_VERSION 1
+
+#define FVS_OK 0
+#define FVS_E_ARG (-1)      /* an argument is out of its documented range            */
+#define FVS_E_SHAPE (-2)    /* a shape the kernels do not support (R, d, tiers, ...) */
+#define FVS_E_CAPACITY (-3) /* a per-workgroup capacity is exceeded (K, n_p, cell)   */
+
+/* Maximum tiers of the refinement code (the reference asserts <= 6: src/tiered_fused.py:55). */
+#define FVS_MAX_TIERS 8
+
+/* ABI version (FVS_ABI_VERSION) and a static description of an error code. */
+int fvs_abi_version(void);
+const char *fvs_error_string(int code);
+
+/* Fill n 32-bit words with `value` (graph-capturable replacement for hipMemsetAsync). */
+int fvs_fill_u32(void *dst, int64_t n, uint32_t value, void *stream);
+
+/*
+ * Query code (a6) plus the global-centre term and the fp16 copy of the queries.
+ * Replaces throughput/enginei8.py:38 (z = Qb @ Vr; qs = max|z|/127; q8 = round(z/qs)),
+ * throughput/enginei8.py:62 (QC = Qb @ c) and the Qb.half() casts at :67 and s2lut.py:122.
+ *   Q  f32 [B, d] row-major; Vr f32 [d, R]; c f32 [d]
+ *   q8 i8 [B, R]; qs f32 [B]; qc f32 [B]; qh fp16 [B, d]
+ * Canonical order: z[j] = fmaf(Q[k], Vr[k][j], z[j]) for k = 0..d-1 from +0;
+ *   qs = max(max_j |z[j]|, 1e-12f) / 127.0f; q8[j] = clamp(rintf(z[j] / qs), -127, 127);
+ *   qc = (float) sum_k (double)Q[k]*(double)c[k], summed in k order in double.
+ * R must be 256; d must be a multiple of 8.
+ */
+int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *Vr, int32_t R, const float *c,
+                   int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream);
+
+/*
+ * int8 cell-residual codes of the base set (a3). Replaces build_codes, throughput/enginei8.py:19-27.
+ *   X16 fp16 [n_ids, d] in id order; order i32 [N] (sorted position -> id);
+ *   cell i32 [N] (cell of each sorted position); means16 fp16 [NC, d]; Vr f32 [d, R]
+ *   Z i8 [N, R] in sorted order; zs f32 [N]
+ * Canonical order: x[k] = (float)X16[order[n]][k] - (float)means16[cell[n]][k] (one f32 subtraction),
+ *   then the projection and quantisation of fvs_query_prep.
+ */
+int fvs_build_codes(const uint16_t *X16, const int32_t *order, const int32_t *cell, int64_t N, int32_t d,
+                    const uint16_t *means16, const float *Vr, int32_t R, int8_t *Z, float *zs, void *stream);
+
+/*
+ * Routing top-n_p (a7). Replaces `probe = QM.topk(nprobe, 1).indices` (throughput/enginei8.py:68).
+ *   QM fp16 [B, NC]; probe i32 [B, nprobe], each row sorted by (QM value descending, cell ascending);
+ *   -0 and +0 compare equal. nprobe <= min(NC, 4096).
+ */
+int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t nprobe, int32_t *probe, void *stream);
+
+/*
+ * (query, cell) pairs grouped by cell (a8). Replaces pairs_fast (throughput/enginei8.py:11-16) with
+ * scale = |m_c| (the NROUTE branch, :47).
+ *   probe i32 [B, npr] (only the first n columns are used); QM fp16 [B, NC]; mnorm f32 [NC] or NULL (scale 1)
+ *   ccnt i32 [NC]  number of pairs of each cell      coff i32 [NC]  exclusive prefix of ccnt
+ *   fill i32 [NC]  scratch                            qid i32 [B*n]  query of each pair, cell-major,
+ *                                                     queries ascending inside a cell (the stable-sort order)
+ *   qrank i32 [B*n] rank of the cell in the query's probe row     qcp f32 [B*n] = (float)QM[q][c] * mnorm[c]
+ * At most 16384 pairs per cell.
+ */
+int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
+              const float *mnorm, int32_t *ccnt, int32_t *coff, int32_t *fill, int32_t *qid, int32_t *qrank,
+              float *qcp, void *stream);
+
+/*
+ * int8 stage-1 scan on MFMA (a9, a11). Same inputs and outputs as the reference's CUDA twin
+ * civf8.launch(mode, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, t0, cnt, bval,
+ * bpos, bmc, CAP, MB) (throughput/civf8.py:89-91), which the Triton pair _first8c/_emit8c
+ * (throughput/ivf8c_kern.py:2-36) also implements; plus qrank/n1 so that the first pass writes each
+ * query's block maxima straight into its own row.
+ *   One program per static (cell, 32-row block) item p < P (pcell, pblk, ps, pe: the cell, the global
+ *   block index, and the cell's first and end row). For every query q of the cell's pair list:
+ *     acc = sum_j q8[q][j] * Z[n][j] (int32, exact), est = fmaf((float)acc * qs[q], zs[n], qcp[pair]).
+ *   mode 0 (first pass): bm[(q*n1 + qrank[pair])*MB + blk - cs/32] = max over the block's rows in the
+ *     cell; entries of blocks a cell does not have are left untouched.
+ *   mode 1 (emit): every (q, n) with est >= t0[q] increments cnt[q]; the first CAP of them are stored in
+ *     bval[q*CAP + idx] = est, bpos[q*CAP + idx] = n. cnt must be zero before the call.
+ * R must be 256. Z must have at least max(pe) rows; N is its row count.
+ */
+int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
+                const int32_t *qrank, const int32_t *coff, const int32_t *ccnt, const int32_t *pcell,
+                const int32_t *pblk, const int32_t *ps, const int32_t *pe, const int8_t *Z, const float *zs,
+                int64_t N, int32_t R, const float *qcp, const float *t0, int32_t *cnt, float *bval,
+                int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
+
+/*
+ * Threshold t0 (a10). Replaces throughput/enginei8.py:53-55
+ *   (v = bmc[inv]; top = v.topk(min(r, n1*MB)); t0 = min(top where top > -1e29 else 1e30)).
+ *   bm f32 [B, n1, MB] written by fvs_i8_scan mode 0; probe i32 [B, npr]; off i32 [NC+1] cell offsets.
+ *   Valid values of query q: bm[q][j][b] for j < n1 and b < blocks(cell probe[q][j]).
+ *   t0[q] = the min(r, n1*MB, #valid)-th largest valid value, or 1e30 if none is valid.
+ */
+int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
+                  int32_t n1, int32_t MB, int32_t r, float *t0, void *stream);
+
+/*
+ * Final stage-1 selection (a12) and the delta rule (a14). Replaces throughput/enginei8.py:60
+ * (t = bval.topk(K); pos = bpos[t]; ok = K <= cnt <= M) and :87-88 (ncnt).
+ *   bval f32 [B, M], bpos i32 [B, M], cnt i32 [B]: the emit buffers (only the first min(cnt, M)
+ *   entries of a row are read). pos i32 [B, K], est1 f32 [B, K] sorted by (est descending, pos
+ *   ascending); rows with fewer than K entries are completed with (est -1e30, pos 0).
+ *   ok u8 [B] = (K <= cnt <= M). ncnt i32 [B] = #{j < K : est1[j] >= est1[kd] - delta} when
+ *   delta >= 0 (f32 subtraction), K otherwise. K <= 4096, 0 <= kd < K.
+ */
+int fvs_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64_t B, int32_t M, int32_t K,
+               int32_t kd, float delta, int32_t *pos, float *est1, uint8_t *ok, int32_t *ncnt, void *stream);
+
+/*
+ * Nibble lookup tables of the uniform tiered code (a13). Replaces luts_fused/_lut_kernel
+ * (throughput/s2lut.py:108-126).
+ *   Zq fp16 [B, D] (the rotated queries, Qb.half() @ VP16[:, :D]); tiers i32 [T][3] = (start, end, bits)
+ *   is a HOST array. L [B, D/4*16] is fp16 when half != 0, else f32:
+ *     L[q][n*16 + v] = sum_{i<4} Zq[q][4n+i] * ((v >> (3-i)) & 1), as fmaf in i order from +0.
+ *   qsum, qn2 f32 [T, B]: (float) of the sums over the tier's coordinates of Zq and Zq^2, in double,
+ *   in coordinate order.
+ */
+int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int32_t *tiers, int32_t half,
+                  void *L, float *qsum, float *qn2, void *stream);
+
+/*
+ * LUT stage 2 with error bars (a15). Replaces score_lut/_score_lut/_tier_lut (throughput/s2lut.py:48-106)
+ * over the packed 512-byte-class records of src/tiered_fused.py:112-125.
+ *   pos i32 [B, K] sorted positions; qc f32 [B]; L (fp16 if half else f32) [B, LW];
+ *   qsum, qn2 f32 [T, B]; rec u8 [N, RB]: tier t plane p at toff[t] + p*(d_t/8), then (scale, sigma)
+ *   fp16 pairs per tier at soff + 4t; tiers i32 [T][3], deltas f32 [T], toff i32 [T] are HOST arrays.
+ *   ncnt i32 [B] or NULL (score all K). est, sd f32 [B, K]; slots m >= ncnt[q] get (-1e30, 0).
+ * Canonical arithmetic: each LUT entry is turned into the integer fx = rint(L * 2^(24-s)), with
+ * s = max(0, E - 3) where max|L| of the query = f * 2^E, f in [0.5, 1) (frexp); the tier sums
+ *   A_t = sum_p 2^(b-1-p) sum_j (fx[hi nibble] + fx[lo nibble]) are exact integers. Then, in f32:
+ *   a = ldexpf((float)A_t, s - 24); a = delta_t * (a - mid_t * qsum[t]); est += a * scale_t;
+ *   var += (qn2[t] * sig_t) * sig_t, for t = 0..T-1, from est = qc[q], var = 0; sd = sqrtf(var).
+ */
+int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
+                  const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB, int32_t soff,
+                  int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff, const int32_t *ncnt,
+                  int64_t B, int32_t K, float *est, float *sd, void *stream);
+
+/*
+ * Error-bar classification, exact refinement and final top-k (a16, a17, a18). Replaces
+ * throughput/enginei8.py:92-95, src/engine3.py:143-146 and src/stage3_zc.py:11-27.
+ *   est, sd f32 [B, K]; pos i32 [B, K]; order i32 [N]; H fp16 [n_ids, d] in id order (device memory or a
+ *   pinned device-mapped host buffer); Q f32 [B, d].
+ *   lo = est - z*sd, hi = est + z*sd; sure = lo > (k+1)-th largest hi; amb = hi >= k-th largest lo and not sure.
+ *   score = est + 10 (sure), exact <H[id], Q> (amb), -1e9 (other).
+ *   ids i32 [B, K] = order[pos]; I i32 [B, k] = ids of the top-k scores (score descending, slot ascending);
+ *   scores f32 [B, k]: the exact score of an ambiguous pick, the estimate of a sure one;
+ *   reads i32 [B] = #amb. Exact dot canonical order: lane l (0..63) sums elements 8g..8g+7 of groups
+ *   g = l, l+64, ... with fmaf in element order, then acc += shfl_xor(acc, o) for o = 32, 16, 8, 4, 2, 1.
+ * k < K <= 4096; d a multiple of 8.
+ */
+int fvs_refine(const float *est, const float *sd, const int32_t *pos, const int32_t *order, const uint16_t *H,
+               const float *Q, int64_t B, int32_t K, int32_t d, float z, int32_t k, int32_t *ids, int32_t *I,
+               float *scores, int32_t *reads, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FVS_H */

@@ -1,0 +1,338 @@
+"""CPU oracle of the FanarVSE throughput-mode search path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py may import this module; the
+product (fanarvse_paper_amd) never does. Integer bookkeeping is restated here in numpy; every
+floating-point stage calls oracle.c (built by oracle/Makefile into liboracle.so), which follows the
+reference's arithmetic with the canonical operation order of include/fvs.h.
+
+References (under /root/reference):
+    static_blocks      src/s1cell.py:161-168
+    pairs              throughput/enginei8.py:11-16
+    params             throughput/enginei8.py:40-47
+    pipeline           throughput/enginei8.py:36-120 (stage1_i8, _gpu NROUTE branch, _finish, _fallback)
+    recall             src/rev_fanardb.py:134-136
+Pinned by tests/test_oracle_*.py (closed forms, brute force, the paper's lemmas, planted mistakes).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+I64, I32, F32 = ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+
+# ------------------------------------------------------------------------------------ numpy parts
+def static_blocks(off, BN=32):
+    """(pcell, pblk, ps, pe, MB): every (cell, BN-row block) of a cell-sorted index (src/s1cell.py:161-168)."""
+    off = np.asarray(off, dtype=np.int64)
+    s, e = off[:-1], off[1:]
+    nb = np.where(e > s, (e - 1) // BN - s // BN + 1, 0)
+    cell = np.repeat(np.arange(len(s)), nb)
+    first = np.cumsum(nb) - nb
+    blk = s[cell] // BN + np.arange(len(cell)) - first[cell]
+    MB = int((int((e - s).max()) + BN - 1) // BN + 1)
+    return cell.astype(np.int32), blk.astype(np.int32), s[cell].astype(np.int32), e[cell].astype(np.int32), MB
+
+
+def pairs(probe, NC, QM16, mnorm=None):
+    """(qid, coff, ccnt, qcp, o) of the (query, cell) pairs (throughput/enginei8.py:11-16): a stable sort of
+    the flattened cell ids, per-cell counts and offsets, qcp = f32(QM[q, c]) * |m_c|."""
+    B, npr = probe.shape
+    flat = probe.reshape(-1).astype(np.int64)
+    o = np.argsort(flat, kind="stable")
+    qid = (o // npr).astype(np.int32)
+    ccnt = np.bincount(flat, minlength=NC).astype(np.int32)
+    coff = (np.cumsum(ccnt) - ccnt).astype(np.int32)
+    fo = flat[o]
+    qcp = np.asarray(QM16).view(np.float16)[qid, fo].astype(np.float32)
+    if mnorm is not None:
+        qcp = qcp * np.asarray(mnorm, np.float32)[fo]
+    return qid, coff, ccnt, qcp.astype(np.float32), o
+
+
+def params(K, nprobe, N, NC, BN=32, MSZ=3072, BETA=None, RHO=0.6, rho_override=None, M_override=None):
+    """(M, n1, r) of throughput/enginei8.py:40-47,53."""
+    M = M_override or MSZ or max(4096, 16 * K)
+    beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
+    if BETA:
+        beta = BETA
+    if RHO:
+        rho = RHO
+    if rho_override:
+        beta, rho = 1.5, rho_override
+    n1 = min(max(int(np.ceil(beta * K / (N / NC / BN + 1))), 1), nprobe)
+    return M, n1, int(np.ceil(rho * K))
+
+
+def recall(I, GT, k=10):
+    I, GT = np.asarray(I), np.asarray(GT)
+    return round(float(np.mean([len(set(I[i, :k].tolist()) & set(GT[i, :k].tolist())) / k for i in range(len(I))])), 4)
+
+
+# ------------------------------------------------------------------------------------ C stages
+def query_prep(Q, Vr, c):
+    Q = _c(Q, np.float32)
+    Vr = _c(Vr, np.float32)
+    c = _c(c, np.float32)
+    B, d = Q.shape
+    R = Vr.shape[1]
+    q8 = np.empty((B, R), np.int8)
+    qs = np.empty(B, np.float32)
+    qc = np.empty(B, np.float32)
+    qh = np.empty((B, d), np.uint16)
+    lib().or_query_prep(_p(Q), I64(B), I32(d), _p(Vr), I32(R), _p(c), _p(q8), _p(qs), _p(qc), _p(qh))
+    return q8, qs, qc, qh
+
+
+def build_codes(X16, order, cell, means16, Vr):
+    X16 = _c(np.asarray(X16).view(np.uint16), np.uint16)
+    means16 = _c(np.asarray(means16).view(np.uint16), np.uint16)
+    order = _c(order, np.int32)
+    cell = _c(cell, np.int32)
+    Vr = _c(Vr, np.float32)
+    N = len(order)
+    d = X16.shape[1]
+    R = Vr.shape[1]
+    Z = np.empty((N, R), np.int8)
+    zs = np.empty(N, np.float32)
+    lib().or_build_codes(_p(X16), _p(order), _p(cell), I64(N), I32(d), _p(means16), _p(Vr), I32(R), _p(Z), _p(zs))
+    return Z, zs
+
+
+def fp16_gemm_nt(A16, Bt16):
+    A16 = _c(np.asarray(A16).view(np.uint16), np.uint16)
+    Bt16 = _c(np.asarray(Bt16).view(np.uint16), np.uint16)
+    M, K = A16.shape
+    Nn = Bt16.shape[0]
+    out = np.empty((M, Nn), np.uint16)
+    lib().or_fp16_gemm_nt(_p(A16), _p(Bt16), I64(M), I64(Nn), I32(K), _p(out))
+    return out
+
+
+def fp16_gemm_nn(A16, Bm16):
+    A16 = _c(np.asarray(A16).view(np.uint16), np.uint16)
+    Bm16 = _c(np.asarray(Bm16).view(np.uint16), np.uint16)
+    M, K = A16.shape
+    Nn = Bm16.shape[1]
+    out = np.empty((M, Nn), np.uint16)
+    lib().or_fp16_gemm_nn(_p(A16), _p(Bm16), I64(M), I64(Nn), I32(K), I32(Bm16.shape[1]), _p(out))
+    return out
+
+
+def route_topk(QM16, nprobe):
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    B, NC = QM16.shape
+    probe = np.empty((B, nprobe), np.int32)
+    lib().or_route_topk(_p(QM16), I64(B), I32(NC), I32(nprobe), _p(probe))
+    return probe
+
+
+def first_pass(q8, qs, probe, n1, off, Z, zs, QM16, mnorm, MB):
+    q8 = _c(q8, np.int8)
+    qs = _c(qs, np.float32)
+    probe = _c(probe, np.int32)
+    off = _c(off, np.int32)
+    Z = _c(Z, np.int8)
+    zs = _c(zs, np.float32)
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    B, npr = probe.shape
+    NC = QM16.shape[1]
+    mn = None if mnorm is None else _c(mnorm, np.float32)
+    bm = np.full((B, n1, MB), -1e30, np.float32)
+    lib().or_first_pass(_p(q8), _p(qs), _p(probe), I32(npr), I32(n1), _p(off), _p(Z), _p(zs), I32(Z.shape[1]),
+                        _p(QM16), I32(NC), _p(mn) if mn is not None else None, I64(B), I32(MB), _p(bm))
+    return bm
+
+
+def threshold(bm, probe, off, n1, MB, r):
+    bm = _c(bm, np.float32)
+    probe = _c(probe, np.int32)
+    off = _c(off, np.int32)
+    B, npr = probe.shape
+    t0 = np.empty(B, np.float32)
+    lib().or_threshold(_p(bm), _p(probe), I32(npr), _p(off), I64(B), I32(n1), I32(MB), I32(r), _p(t0))
+    return t0
+
+
+def emit(q8, qs, probe, off, Z, zs, QM16, mnorm, t0, M):
+    """(cnt, bval, bpos): every probed row with est >= t0, canonical order, first M kept."""
+    q8 = _c(q8, np.int8)
+    qs = _c(qs, np.float32)
+    probe = _c(probe, np.int32)
+    off = _c(off, np.int32)
+    Z = _c(Z, np.int8)
+    zs = _c(zs, np.float32)
+    t0 = _c(t0, np.float32)
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    B, npr = probe.shape
+    NC = QM16.shape[1]
+    mn = None if mnorm is None else _c(mnorm, np.float32)
+    cnt = np.empty(B, np.int32)
+    bval = np.empty((B, M), np.float32)
+    bpos = np.empty((B, M), np.int32)
+    lib().or_emit(_p(q8), _p(qs), _p(probe), I32(npr), I32(npr), _p(off), _p(Z), _p(zs), I32(Z.shape[1]), _p(QM16),
+                  I32(NC), _p(mn) if mn is not None else None, _p(t0), I64(B), I32(M), _p(cnt), _p(bval), _p(bpos))
+    return cnt, bval, bpos
+
+
+def select(bval, bpos, cnt, K, kd, delta):
+    bval = _c(bval, np.float32)
+    bpos = _c(bpos, np.int32)
+    cnt = _c(cnt, np.int32)
+    B, M = bval.shape
+    pos = np.empty((B, K), np.int32)
+    est1 = np.empty((B, K), np.float32)
+    ok = np.empty(B, np.uint8)
+    ncnt = np.empty(B, np.int32)
+    lib().or_select(_p(bval), _p(bpos), _p(cnt), I64(B), I32(M), I32(K), I32(kd), F32(-1.0 if delta is None else delta),
+                    _p(pos), _p(est1), _p(ok), _p(ncnt))
+    return pos, est1, ok, ncnt
+
+
+def _tiers(TS):
+    return np.asarray([[s, e, b] for s, e, b in TS], dtype=np.int32).reshape(-1)
+
+
+def lut_build(Zq16, TS, half):
+    Zq16 = _c(np.asarray(Zq16).view(np.uint16), np.uint16)
+    B, D = Zq16.shape
+    T = len(TS)
+    L = np.empty((B, D // 4 * 16), np.uint16 if half else np.float32)
+    qsum = np.empty((T, B), np.float32)
+    qn2 = np.empty((T, B), np.float32)
+    tiers = _tiers(TS)
+    lib().or_lut_build(_p(Zq16), I64(B), I32(D), I32(T), _p(tiers), I32(int(half)), _p(L), _p(qsum), _p(qn2))
+    return L, qsum, qn2
+
+
+def lut_score(pos, qc, L, half, qsum, qn2, rec, soff, TS, deltas, toff, ncnt=None):
+    pos = _c(pos, np.int32)
+    qc = _c(qc, np.float32)
+    L = _c(L, np.uint16 if half else np.float32)
+    qsum = _c(qsum, np.float32)
+    qn2 = _c(qn2, np.float32)
+    rec = _c(rec, np.uint8)
+    tiers = _tiers(TS)
+    dl = _c(deltas, np.float32)
+    to = _c(toff, np.int32)
+    B, K = pos.shape
+    est = np.empty((B, K), np.float32)
+    sd = np.empty((B, K), np.float32)
+    nc = None if ncnt is None else _c(ncnt, np.int32)
+    lib().or_lut_score(_p(pos), _p(qc), _p(L), I32(int(half)), I32(L.shape[1]), _p(qsum), _p(qn2), _p(rec),
+                       I32(rec.shape[1]), I32(soff), I32(len(TS)), _p(tiers), _p(dl), _p(to),
+                       _p(nc) if nc is not None else None, I64(B), I32(K), _p(est), _p(sd))
+    return est, sd
+
+
+def refine(est, sd, pos, order, H16, Q, z, k):
+    est = _c(est, np.float32)
+    sd = _c(sd, np.float32)
+    pos = _c(pos, np.int32)
+    order = _c(order, np.int32)
+    H16 = _c(np.asarray(H16).view(np.uint16), np.uint16)
+    Q = _c(Q, np.float32)
+    B, K = est.shape
+    d = Q.shape[1]
+    ids = np.empty((B, K), np.int32)
+    I = np.empty((B, k), np.int32)
+    scores = np.empty((B, k), np.float32)
+    reads = np.empty(B, np.int32)
+    lib().or_refine(_p(est), _p(sd), _p(pos), _p(order), _p(H16), _p(Q), I64(B), I32(K), I32(d), F32(z), I32(k),
+                    _p(ids), _p(I), _p(scores), _p(reads))
+    return ids, I, scores, reads
+
+
+# ------------------------------------------------------------------------------------ whole path
+def index_from_tables(s1, code, Z, zs, Vr, H):
+    """Host copies (numpy) of the tables an EngineI8 searches, in the oracle's layout."""
+    import torch
+
+    t = lambda x: x.detach().cpu().numpy() if torch.is_tensor(x) else np.asarray(x)
+    TS = code["TS"]
+    meansN = (s1["means16"].float() * s1["inv_mnorm"][:, None]).half()
+    mnorm = (1.0 / s1["inv_mnorm"]).float()
+    return dict(order=t(s1["order"]).astype(np.int32), off=np.asarray(s1["off"]).astype(np.int32),
+                meansN=t(meansN).view(np.uint16), mnorm=t(mnorm), c=t(s1["c"]).astype(np.float32),
+                Vr=t(Vr).astype(np.float32), Z=t(Z), zs=t(zs), TS=list(TS),
+                deltas=np.array([code["deltas"][b] for _, _, b in TS], np.float32),
+                toff=np.array(code["toff"], np.int32), soff=int(code["soff"]), rec=t(code["rec"]),
+                VP16=t(code["VP16"]).view(np.uint16), H=t(H).view(np.uint16))
+
+
+def stage1(idx, q8, qs, QM16, probe, K, knobs, rho_override=None, M_override=None, delta=None, kd=9):
+    N = idx["Z"].shape[0]
+    NC = len(idx["off"]) - 1
+    M, n1, r = params(K, probe.shape[1], N, NC, MSZ=knobs.get("MSZ", 3072), BETA=knobs.get("BETA"),
+                      RHO=knobs.get("RHO", 0.6), rho_override=rho_override, M_override=M_override)
+    MB = static_blocks(idx["off"])[4]
+    bm = first_pass(q8, qs, probe[:, :n1], n1, idx["off"], idx["Z"], idx["zs"], QM16, idx["mnorm"], MB)
+    t0 = threshold(bm, probe, idx["off"], n1, MB, r)
+    cnt, bval, bpos = emit(q8, qs, probe, idx["off"], idx["Z"], idx["zs"], QM16, idx["mnorm"], t0, M)
+    pos, est1, ok, ncnt = select(bval, bpos, cnt, K, min(kd, K - 1), delta)
+    return dict(n1=n1, r=r, M=M, MB=MB, bm=bm, t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos, est1=est1, ok=ok,
+                ncnt=ncnt)
+
+
+def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, fallback=True):
+    """Every intermediate of one batch (EngineI8._gpu + _fallback). QM16 / Zq16 (fp16 as uint16) are the
+    two BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs, otherwise
+    computed here with sequential fp32 accumulation."""
+    knobs = dict(knobs or {})
+    delta = knobs.get("DELTA", 0.07)
+    half = knobs.get("LUTF", True) and knobs.get("LUTH", True)
+    q8, qs, qc, qh = query_prep(Q, idx["Vr"], idx["c"])
+    D = idx["TS"][-1][1]
+    if QM16 is None:
+        QM16 = fp16_gemm_nt(qh, idx["meansN"])
+    if Zq16 is None:
+        Zq16 = fp16_gemm_nn(qh, np.ascontiguousarray(idx["VP16"][:, :D]))
+    probe = route_topk(QM16, nprobe)
+    s1 = stage1(idx, q8, qs, QM16, probe, K, knobs, delta=delta, kd=k - 1)
+    L, qsum, qn2 = lut_build(Zq16, idx["TS"], half)
+    est, sd = lut_score(s1["pos"], qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
+                        idx["toff"], s1["ncnt"] if delta is not None else None)
+    ids, I, scores, reads = refine(est, sd, s1["pos"], idx["order"], idx["H"], Q, z, k)
+    out = dict(q8=q8, qs=qs, qc=qc, qh=qh, QM=QM16, Zq=Zq16, probe=probe, L=L, qsum=qsum, qn2=qn2, est=est, sd=sd,
+               ids=ids, I=I.copy(), scores=scores.copy(), reads=reads.copy(), cand=ids.copy(), **s1)
+    bad = np.nonzero(s1["ok"] == 0)[0]
+    out["bad"] = bad
+    if fallback and len(bad):
+        f1 = stage1(idx, q8[bad], qs[bad], QM16[bad], probe[bad], K, knobs, rho_override=1.0, M_override=65536,
+                    delta=None)
+        Lf, qsf, qnf = lut_build(Zq16[bad], idx["TS"], False)
+        estf, sdf = lut_score(f1["pos"], qc[bad], Lf, False, qsf, qnf, idx["rec"], idx["soff"], idx["TS"],
+                              idx["deltas"], idx["toff"], None)
+        idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], idx["order"], idx["H"], np.asarray(Q)[bad], z, k)
+        out["I"][bad], out["scores"][bad], out["reads"][bad], out["cand"][bad] = If, scf, rf_, idsf
+        out["fallback_ok"] = f1["ok"]
+    return out
