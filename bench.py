@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=2000)
     ap.add_argument("--k", type=int, default=10)
     ap.add_argument("--z", type=float, default=1.25)
-    ap.add_argument("--points", default="256:150,352:175,512:300,768:400")
+    ap.add_argument("--points", default="352:175:3072,512:300:4096,768:400:4096,1024:400:4096",
+                    help="n_p:K:M operating points (the reference's grid, throughput/e_v3final.py:31)")
     ap.add_argument("--target", type=float, default=0.99)
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -83,7 +84,9 @@ def main():
     # ---- operating point: fastest point reaching the recall target
     pts = [tuple(int(v) for v in p.split(":")) for p in args.points.split(",")]
     best, rows = None, []
-    for nprobe, K in pts:
+    for nprobe, K, M in pts:
+        E.MSZ = M
+        E.nbad = 0
         I, reads, ids = E.search(Q, K, args.z, nprobe, args.k)
         rec = metrics.recall(I.cpu().numpy(), GT, args.k)
         torch.cuda.synchronize()
@@ -92,7 +95,7 @@ def main():
             E.search(Q, K, args.z, nprobe, args.k)
         torch.cuda.synchronize()
         qps = 3 * args.batch / (time.perf_counter() - t0)
-        row = dict(nprobe=nprobe, K=K, recall=rec, qps=round(qps), reads=round(float(reads.float().mean()), 2),
+        row = dict(nprobe=nprobe, K=K, M=M, recall=rec, qps=round(qps), reads=round(float(reads.float().mean()), 2),
                    fallback=E.nbad)
         rows.append(row)
         log(f"point {row}")
@@ -102,6 +105,7 @@ def main():
         best = max(rows, key=lambda r: (r["recall"], r["qps"]))
         log(f"no point reached recall {args.target}; reporting the best recall {best}")
     nprobe, K = best["nprobe"], best["K"]
+    E.MSZ = best["M"]
 
     # ---- timed region
     for _ in range(args.warmup):
@@ -133,7 +137,7 @@ def main():
         "config": {"workload": f"throughput mode, {args.n}x{args.d} fp16 synthetic (1024-cluster power-law), "
                                f"batch {args.batch}, k={args.k}",
                    "n": args.n, "d": args.d, "nlist": args.nlist, "batch": args.batch, "k": args.k,
-                   "nprobe": nprobe, "K": K, "z": args.z, "recall@10": recall,
+                   "nprobe": nprobe, "K": K, "M": E.MSZ, "z": args.z, "recall@10": recall,
                    "reads_per_query": round(float(reads.float().mean()), 2), "fallback_queries": E.nbad,
                    "parallelism": "single GPU", "points": rows},
         "roofline": kern["roofline"],

@@ -27,7 +27,8 @@ SIGNATURES = {
     "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
-    "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, P, P, P],
+    "fvs_pairs_scratch_bytes": [I64, I32],
+    "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
@@ -50,7 +51,8 @@ def lib():
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name == "fvs_error_string" else ctypes.c_int
+            fn.restype = {"fvs_error_string": ctypes.c_char_p, "fvs_pairs_scratch_bytes": ctypes.c_int64}.get(
+                name, ctypes.c_int)
         if L.fvs_abi_version() != 1:
             raise RuntimeError("libfvs.so ABI version mismatch")
         _lib = L
@@ -97,20 +99,23 @@ def fill_u32(t, value):
     _check(lib().fvs_fill_u32(_dev(t, t.dtype, "dst"), t.numel(), U32(value), _stream()), "fvs_fill_u32")
 
 
-def query_prep(Q, Vr, c):
-    """q8 [B,R] int8, qs [B], qc [B], qh [B,d] fp16 (throughput/enginei8.py:38, :62)."""
+def query_prep(Q, Vr, c, z=None):
+    """q8 [B,R] int8, qs [B], qc [B], qh [B,d] fp16 and the projection z [B,R] (throughput/enginei8.py:38, :62).
+    z = Q @ Vr is an fp32 BLAS product, as in the reference (pass it to reuse rows of an earlier product);
+    the rest runs in one kernel."""
     B, d = Q.shape
     R = Vr.shape[1]
     dev = Q.device
+    z = (Q @ Vr).contiguous() if z is None else z.contiguous()
     q8 = _empty((B, R), torch.int8, dev)
     qs = _empty((B,), torch.float32, dev)
     qc = _empty((B,), torch.float32, dev)
     qh = _empty((B, d), torch.float16, dev)
-    _check(lib().fvs_query_prep(_dev(Q, torch.float32, "Q"), B, d, _dev(Vr, torch.float32, "Vr", (d, R)), R,
+    _check(lib().fvs_query_prep(_dev(Q, torch.float32, "Q"), B, d, _dev(z, torch.float32, "z", (B, R)), R,
                                 _dev(c, torch.float32, "c", (d,)), _dev(q8, torch.int8, "q8"), _dev(qs, torch.float32, "qs"),
                                 _dev(qc, torch.float32, "qc"), _dev(qh, torch.float16, "qh"), _stream()),
            "fvs_query_prep")
-    return q8, qs, qc, qh
+    return q8, qs, qc, qh, z
 
 
 def build_codes(X16, order, cell, means16, Vr):
@@ -141,21 +146,28 @@ def route_topk(QM, nprobe):
     return probe
 
 
-def pairs(probe, n, NC, QM, mnorm):
+def pairs_scratch(B, NC, device):
+    """Scratch buffer for pairs() (a cell-major probe-rank matrix); reusable across calls on a stream."""
+    nbytes = lib().fvs_pairs_scratch_bytes(B, NC)
+    return torch.empty((nbytes,), dtype=torch.uint8, device=device)
+
+
+def pairs(probe, n, NC, QM, mnorm, scratch=None):
     """(qid, qrank, coff, ccnt, qcp) of the first n probe columns (throughput/enginei8.py:11-16)."""
     B, npr = probe.shape
     dev = probe.device
     if QM.shape != (B, NC):
         raise ValueError("pairs: QM shape")
+    if scratch is None:
+        scratch = pairs_scratch(B, NC, dev)
     ccnt = _empty((NC,), torch.int32, dev)
     coff = _empty((NC,), torch.int32, dev)
-    fill = _empty((NC,), torch.int32, dev)
     qid = _empty((B * n,), torch.int32, dev)
     qrank = _empty((B * n,), torch.int32, dev)
     qcp = _empty((B * n,), torch.float32, dev)
     _check(lib().fvs_pairs(_dev(probe, torch.int32, "probe"), B, npr, n, NC, _dev(QM, torch.float16, "QM"),
                            _opt(mnorm, torch.float32, "mnorm", (NC,)), _dev(ccnt, torch.int32, "ccnt"),
-                           _dev(coff, torch.int32, "coff"), _dev(fill, torch.int32, "fill"),
+                           _dev(coff, torch.int32, "coff"), _dev(scratch, torch.uint8, "scratch"), scratch.numel(),
                            _dev(qid, torch.int32, "qid"), _dev(qrank, torch.int32, "qrank"),
                            _dev(qcp, torch.float32, "qcp"), _stream()), "fvs_pairs")
     return qid, qrank, coff, ccnt, qcp

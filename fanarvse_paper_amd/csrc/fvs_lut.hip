@@ -56,24 +56,50 @@ __global__ __launch_bounds__(256) void k_lut_build(const uint16_t *__restrict__ 
       for (int v = 0; v < 4; v++) L4[v] = make_float4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
     }
   }
-  // per-tier sums, one thread per tier (the unrolled loop keeps the argument-struct index uniform)
+  // per-tier sums, one wave per tier: lane l sums coordinates start+l, start+l+64, ... in double,
+  // then a fixed xor butterfly (the unrolled tier loop keeps the argument-struct index uniform)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
   for (int t = 0; t < FVS_MAX_TIERS; t++) {
-    if (t < ta.T && (int)threadIdx.x == t) {
+    if (t < ta.T && (t & 3) == wv) {
       const int i0 = ta.loff[t] / 4, i1 = i0 + 8 * ta.kb[t];
       double s1 = 0.0, s2 = 0.0;
-      for (int i = i0; i < i1; i++) {
+      for (int i = i0 + lane; i < i1; i += 64) {
         const double x = (double)fvs_h2f(zr[i]);
         s1 += x;
         s2 += x * x;
       }
-      qsum[(int64_t)t * B + q] = (float)s1;
-      qn2[(int64_t)t * B + q] = (float)s2;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        s1 += __shfl_xor(s1, o, FVS_WAVE);
+        s2 += __shfl_xor(s2, o, FVS_WAVE);
+      }
+      if (lane == 0) {
+        qsum[(int64_t)t * B + q] = (float)s1;
+        qn2[(int64_t)t * B + q] = (float)s2;
+      }
     }
   }
 }
 
 constexpr int kScoreThreads = 128;
+constexpr int kUnit = 16;  // 16-byte chunks per pipeline unit (256 bytes of a record)
+
+// Per-dword descriptors (LDS): planes carry the LUT byte offset, the plane weight, an end-of-tier flag
+// and the tier; the dwords after the planes carry the (scale, sigma) pair of tier t.
+constexpr uint32_t kMetaLast = 1u << 24;
+constexpr uint32_t kMetaScale = 1u << 25;
+
+struct RecUnit {
+  uint4 c[kUnit];
+};
+
+__device__ __forceinline__ void load_unit(RecUnit &b, const uint8_t *__restrict__ rec, int64_t row, int RB, int u,
+                                          int nchunk, bool live) {
+  const uint4 *rp = reinterpret_cast<const uint4 *>(rec + row * RB) + u * kUnit;
+#pragma unroll
+  for (int c = 0; c < kUnit; c++) b.c[c] = (live && u * kUnit + c < nchunk) ? rp[c] : make_uint4(0, 0, 0, 0);
+}
 
 template <bool HALF>
 __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
@@ -82,28 +108,45 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     TierArgs ta, const int32_t *__restrict__ ncnt, int64_t N, int64_t B, int K, float *__restrict__ est,
     float *__restrict__ sdo) {
   extern __shared__ int32_t smem[];
-  int32_t *lut = smem;                                               // [LW]
-  uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW);          // [nw]
+  int32_t *lut = smem;                                                 // [LW] fixed-point table
   const int nw = soff / 4;
-  float *tf = reinterpret_cast<float *>(meta + nw);                  // [T][4]: delta, mid, qsum, qn2
-  uint32_t *ssw = reinterpret_cast<uint32_t *>(tf + 4 * FVS_MAX_TIERS);  // [threads][8]
+  uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW);            // [nw + T], padded to even
+  float *tf = reinterpret_cast<float *>(meta + ((nw + FVS_MAX_TIERS + 1) & ~1));  // [T][4]: delta, mid, qsum, qn2
+  uint32_t *ssw = reinterpret_cast<uint32_t *>(tf + 4 * FVS_MAX_TIERS);  // [threads][T] (scale, sigma)
+  int64_t *acct = reinterpret_cast<int64_t *>(ssw + kScoreThreads * FVS_MAX_TIERS);  // [threads][T]
+  int32_t *rows = reinterpret_cast<int32_t *>(acct + kScoreThreads * FVS_MAX_TIERS);  // [K]
   __shared__ float red[2];
   __shared__ int sexp;
 
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
+  const int T = ta.T;
 
-  // 1. fixed-point exponent of this query's table
+  // 1. fixed-point exponent of this query's table (vectorised passes over the table)
   float m = 0.f;
   if (HALF) {
-    const uint16_t *L = reinterpret_cast<const uint16_t *>(Lin) + q * LW;
-    for (int i = tid; i < LW; i += kScoreThreads) m = fmaxf(m, fabsf(fvs_h2f(L[i])));
+    const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
+#pragma unroll 8
+    for (int i = tid; i < LW / 8; i += kScoreThreads) {
+      const uint4 v = L4[i];
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        m = fmaxf(m, fmaxf(fabsf(fvs_h2f((uint16_t)(w4[u] & 0xffffu))), fabsf(fvs_h2f((uint16_t)(w4[u] >> 16)))));
+    }
   } else {
-    const float *L = reinterpret_cast<const float *>(Lin) + q * LW;
-    for (int i = tid; i < LW; i += kScoreThreads) m = fmaxf(m, fabsf(L[i]));
+    const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
+#pragma unroll 8
+    for (int i = tid; i < LW / 4; i += kScoreThreads) {
+      const float4 v = L4[i];
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
   }
   m = fvs_wave_max(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
+  // candidate rows of this query, staged while the reduction settles
+  const int lim = ncnt ? min(ncnt[q], K) : K;
+  for (int i = tid; i < K; i += kScoreThreads) rows[i] = (int32_t)min(max((int64_t)pos[q * (int64_t)K + i], (int64_t)0), N - 1);
   __syncthreads();
   if (tid == 0) {
     int E = 0;
@@ -115,32 +158,52 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
 
   // 2. integer LUT, per-dword descriptors, per-tier constants
   if (HALF) {
-    const uint16_t *L = reinterpret_cast<const uint16_t *>(Lin) + q * LW;
-    for (int i = tid; i < LW; i += kScoreThreads) lut[i] = (int32_t)rintf(ldexpf(fvs_h2f(L[i]), 24 - s));
+    const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
+#pragma unroll 8
+    for (int i = tid; i < LW / 8; i += kScoreThreads) {
+      const uint4 v = L4[i];
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        lut[8 * i + 2 * u] = (int32_t)rintf(ldexpf(fvs_h2f((uint16_t)(w4[u] & 0xffffu)), 24 - s));
+        lut[8 * i + 2 * u + 1] = (int32_t)rintf(ldexpf(fvs_h2f((uint16_t)(w4[u] >> 16)), 24 - s));
+      }
+    }
   } else {
-    const float *L = reinterpret_cast<const float *>(Lin) + q * LW;
-    for (int i = tid; i < LW; i += kScoreThreads) lut[i] = (int32_t)rintf(ldexpf(L[i], 24 - s));
+    const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
+#pragma unroll 8
+    for (int i = tid; i < LW / 4; i += kScoreThreads) {
+      const float4 v = L4[i];
+      lut[4 * i + 0] = (int32_t)rintf(ldexpf(v.x, 24 - s));
+      lut[4 * i + 1] = (int32_t)rintf(ldexpf(v.y, 24 - s));
+      lut[4 * i + 2] = (int32_t)rintf(ldexpf(v.z, 24 - s));
+      lut[4 * i + 3] = (int32_t)rintf(ldexpf(v.w, 24 - s));
+    }
   }
-  for (int w = tid; w < nw; w += kScoreThreads) {
-    const int byte = 4 * w;
+  for (int w = tid; w < nw + T; w += kScoreThreads) {
     uint32_t d = 0;
-    for (int t = 0; t < ta.T; t++) {
-      const int len = ta.bits[t] * ta.kb[t];
-      if (byte >= ta.toff[t] && byte < ta.toff[t] + len) {
-        const int rel = byte - ta.toff[t];
-        const int p = rel / ta.kb[t];
-        const int j0 = rel - p * ta.kb[t];
-        const uint32_t base = (uint32_t)(ta.loff[t] + 32 * j0);
-        const uint32_t shift = (uint32_t)(ta.bits[t] - 1 - p);
-        const uint32_t last = (byte + 4 == ta.toff[t] + len) ? 1u : 0u;
-        d = base | (shift << 16) | (last << 19) | ((uint32_t)t << 20);
+    if (w >= nw) {
+      d = kMetaScale | (uint32_t)(w - nw);
+    } else {
+      const int byte = 4 * w;
+      for (int t = 0; t < T; t++) {
+        const int len = ta.bits[t] * ta.kb[t];
+        if (byte >= ta.toff[t] && byte < ta.toff[t] + len) {
+          const int rel = byte - ta.toff[t];
+          const int p = rel / ta.kb[t];
+          const int j0 = rel - p * ta.kb[t];
+          const uint32_t base = (uint32_t)(ta.loff[t] + 32 * j0) * 4u;  // byte offset in the table
+          const uint32_t shift = (uint32_t)(ta.bits[t] - 1 - p);
+          const uint32_t last = (byte + 4 == ta.toff[t] + len) ? kMetaLast : 0u;
+          d = base | (shift << 17) | last | ((uint32_t)t << 20);
+        }
       }
     }
     meta[w] = d;
   }
 #pragma unroll
   for (int t = 0; t < FVS_MAX_TIERS; t++) {
-    if (t < ta.T && tid == t) {
+    if (t < T && tid == t) {
       tf[4 * t + 0] = ta.delta[t];
       tf[4 * t + 1] = ta.mid[t];
       tf[4 * t + 2] = qsum[(int64_t)t * B + q];
@@ -149,61 +212,79 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   }
   __syncthreads();
 
-  const int lim = ncnt ? min(ncnt[q], K) : K;
+  // 3. candidates: lane `tid` scores slots tid, tid + 128, ...; the record stream is cut into units of
+  //    256 bytes and double-buffered in registers, so the next unit is in flight while one is summed
+  const int nchunk = (soff + 4 * T + 15) / 16;  // chunks holding planes and (scale, sigma) pairs
+  const int U = (nchunk + kUnit - 1) / kUnit;
+  const int nround = (K + kScoreThreads - 1) / kScoreThreads;
+  const int S = nround * U;
+  const char *lutb = reinterpret_cast<const char *>(lut);
   const float qcq = qc[q];
-  const int nchunk = RB / 16;
-  for (int mm = tid; mm < K; mm += kScoreThreads) {
-    const int64_t o = q * (int64_t)K + mm;
-    if (mm >= lim) {
-      est[o] = -1e30f;
-      sdo[o] = 0.f;
-      continue;
+  RecUnit ub0, ub1;
+  int64_t acc = 0;
+  // one pipeline step: `cur` holds unit sq, `nxt` receives unit sq + 1
+  auto step = [&](int sq, const RecUnit &cur, RecUnit &nxt) {
+    const int i = sq / U, u = sq - i * U;
+    const int mm = tid + kScoreThreads * i;
+    const bool live = mm < lim;
+    if (sq + 1 < S) {
+      const int i1 = (sq + 1) / U, u1 = (sq + 1) - i1 * U;
+      const int m1 = tid + kScoreThreads * i1;
+      load_unit(nxt, rec, m1 < lim ? rows[m1] : 0, RB, u1, nchunk, m1 < lim);
     }
-    const int64_t row = min(max((int64_t)pos[o], (int64_t)0), N - 1);  // positions come from fvs_select
-    const uint8_t *rp = rec + row * RB;
-    const uint32_t *rp32 = reinterpret_cast<const uint32_t *>(rp);
-    const uint4 *rp16 = reinterpret_cast<const uint4 *>(rp);
-    for (int t = 0; t < ta.T; t++) ssw[tid * 8 + t] = rp32[soff / 4 + t];
-    int64_t acc = 0;
-    float e = qcq, var = 0.f;
-    for (int w0 = 0; w0 < nw; w0 += 32) {
-      uint4 ch[8];
+    if (live) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int ci = w0 / 4 + u;
-        ch[u] = ci < nchunk ? rp16[ci] : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const uint32_t xs[4] = {ch[u].x, ch[u].y, ch[u].z, ch[u].w};
+      for (int c = 0; c < kUnit; c++) {
+        const uint32_t xs[4] = {cur.c[c].x, cur.c[c].y, cur.c[c].z, cur.c[c].w};
 #pragma unroll
         for (int ee = 0; ee < 4; ee++) {
-          const int w = w0 + 4 * u + ee;
+          const int w = (u * kUnit + c) * 4 + ee;
           if (w < nw) {
             const uint32_t mt = meta[w];
-            const int base = (int)(mt & 0xffffu);
+            const char *lb = lutb + (mt & 0x1ffffu);
             const uint32_t x = xs[ee];
-            const int part = lut[base + ((x >> 4) & 15)] + lut[base + 16 + (x & 15)] +
-                             lut[base + 32 + ((x >> 12) & 15)] + lut[base + 48 + ((x >> 8) & 15)] +
-                             lut[base + 64 + ((x >> 20) & 15)] + lut[base + 80 + ((x >> 16) & 15)] +
-                             lut[base + 96 + (x >> 28)] + lut[base + 112 + ((x >> 24) & 15)];
-            acc += (int64_t)part << ((mt >> 16) & 7);
-            if (mt & (1u << 19)) {
-              const int t = (int)(mt >> 20);
-              float a = ldexpf((float)acc, s - 24);
-              a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
-              const uint32_t sw = ssw[tid * 8 + t];
-              const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
-              e = __builtin_fmaf(a, sc, e);
-              var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
+            const uint32_t xh = (x >> 2) & 0x3c3c3c3cu, xl = (x << 2) & 0x3c3c3c3cu;  // nibble * 4 per byte
+            int part = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              part += *reinterpret_cast<const int32_t *>(lb + 128 * j + ((xh >> (8 * j)) & 0xffu));
+              part += *reinterpret_cast<const int32_t *>(lb + 128 * j + 64 + ((xl >> (8 * j)) & 0xffu));
+            }
+            acc += (int64_t)part << ((mt >> 17) & 7u);
+            if (mt & kMetaLast) {
+              acct[tid * FVS_MAX_TIERS + ((mt >> 20) & 7u)] = acc;
               acc = 0;
             }
+          } else if (w < nw + T) {
+            ssw[tid * FVS_MAX_TIERS + (w - nw)] = xs[ee];
           }
         }
       }
     }
-    est[o] = e;
-    sdo[o] = sqrtf(var);
+    if (u == U - 1 && mm < K) {
+      const int64_t o = q * (int64_t)K + mm;
+      if (!live) {
+        est[o] = -1e30f;
+        sdo[o] = 0.f;
+      } else {
+        float e = qcq, var = 0.f;
+        for (int t = 0; t < T; t++) {
+          float a = ldexpf((float)acct[tid * FVS_MAX_TIERS + t], s - 24);
+          a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
+          const uint32_t sw = ssw[tid * FVS_MAX_TIERS + t];
+          const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
+          e = __builtin_fmaf(a, sc, e);
+          var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
+        }
+        est[o] = e;
+        sdo[o] = sqrtf(var);
+      }
+    }
+  };
+  load_unit(ub0, rec, tid < lim ? rows[tid] : 0, RB, 0, nchunk, tid < lim);
+  for (int sq = 0; sq < S; sq += 2) {
+    step(sq, ub0, ub1);
+    if (sq + 1 < S) step(sq + 1, ub1, ub0);
   }
 }
 
@@ -263,7 +344,9 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (at != soff || soff + 4 * T > RB) return FVS_E_SHAPE;
   if (B == 0) return FVS_OK;
   if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
-  const size_t shm = (size_t)LW * 4 + (size_t)(soff / 4) * 4 + 4 * FVS_MAX_TIERS * 4 + kScoreThreads * 8 * 4;
+  if (K > 4096) return FVS_E_CAPACITY;
+  const size_t shm = (size_t)LW * 4 + (size_t)((soff / 4 + FVS_MAX_TIERS + 1) & ~1) * 4 + 4 * FVS_MAX_TIERS * 4 +
+                     (size_t)kScoreThreads * FVS_MAX_TIERS * (4 + 8) + (size_t)K * 4;
   if (shm > 160 * 1024 - 64) return FVS_E_CAPACITY;
   hipStream_t st = (hipStream_t)stream;
   if (half)

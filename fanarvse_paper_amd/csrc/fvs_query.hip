@@ -10,7 +10,29 @@
 namespace {
 
 constexpr int kR = 256;
-constexpr int kKC = 64;  // k-chunk staged in LDS
+constexpr int kKC = 32;  // k-chunk staged in LDS (double-buffered)
+
+template <int QB, bool RESID>
+__device__ __forceinline__ void stage_rows(float (*xs)[QB], const float *__restrict__ Q, const uint16_t *__restrict__ X16,
+                                           const int32_t *__restrict__ order, const int32_t *__restrict__ cell,
+                                           const uint16_t *__restrict__ M16, int64_t r0, int64_t nrows, int d, int k0) {
+  for (int i = threadIdx.x; i < QB * kKC; i += 256) {
+    const int rr = i / kKC, kk = i % kKC;
+    const int64_t row = r0 + rr;
+    const int k = k0 + kk;
+    float x = 0.f;
+    if (row < nrows && k < d) {
+      if (RESID) {
+        const int64_t id = order[row];
+        const int64_t cc = cell[row];
+        x = fvs_h2f(X16[id * d + k]) - fvs_h2f(M16[cc * d + k]);
+      } else {
+        x = Q[row * d + k];
+      }
+    }
+    xs[kk][rr] = x;
+  }
+}
 
 template <int QB, bool RESID>
 __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, const uint16_t *__restrict__ X16,
@@ -18,7 +40,7 @@ __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, co
                                                  const uint16_t *__restrict__ M16, int64_t nrows, int d,
                                                  const float *__restrict__ Vr, int8_t *__restrict__ out8,
                                                  float *__restrict__ outs) {
-  __shared__ float xs[kKC][QB];
+  __shared__ float xs[2][kKC][QB];
   __shared__ float red[QB][4];
   const int j = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * QB;
@@ -26,31 +48,41 @@ __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, co
 #pragma unroll
   for (int rr = 0; rr < QB; rr++) acc[rr] = 0.f;
 
+  // software pipeline: chunk i+1 of the rows (LDS) and of Vr's column j (registers) is fetched while
+  // chunk i is consumed
+  float vcur[kKC], vnext[kKC];
+  stage_rows<QB, RESID>(xs[0], Q, X16, order, cell, M16, r0, nrows, d, 0);
+#pragma unroll
+  for (int kk = 0; kk < kKC; kk++) vcur[kk] = kk < d ? Vr[(int64_t)kk * kR + j] : 0.f;
+  __syncthreads();
+  int buf = 0;
   for (int k0 = 0; k0 < d; k0 += kKC) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < QB * kKC; i += 256) {
-      const int rr = i / kKC, kk = i % kKC;
-      const int64_t row = r0 + rr;
-      const int k = k0 + kk;
-      float x = 0.f;
-      if (row < nrows && k < d) {
-        if (RESID) {
-          const int64_t id = order[row];
-          const int64_t cc = cell[row];
-          x = fvs_h2f(X16[id * d + k]) - fvs_h2f(M16[cc * d + k]);
-        } else {
-          x = Q[row * d + k];
+    const int k1 = k0 + kKC;
+    if (k1 < d) {
+      stage_rows<QB, RESID>(xs[buf ^ 1], Q, X16, order, cell, M16, r0, nrows, d, k1);
+#pragma unroll
+      for (int kk = 0; kk < kKC; kk++) vnext[kk] = k1 + kk < d ? Vr[(int64_t)(k1 + kk) * kR + j] : 0.f;
+    }
+    const int kn = min(kKC, d - k0);
+    if (kn == kKC) {
+#pragma unroll
+      for (int kk = 0; kk < kKC; kk++) {
+#pragma unroll
+        for (int rr = 0; rr < QB; rr++) acc[rr] = __builtin_fmaf(xs[buf][kk][rr], vcur[kk], acc[rr]);
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < kKC; kk++) {
+        if (kk < kn) {
+#pragma unroll
+          for (int rr = 0; rr < QB; rr++) acc[rr] = __builtin_fmaf(xs[buf][kk][rr], vcur[kk], acc[rr]);
         }
       }
-      xs[kk][rr] = x;
     }
     __syncthreads();
-    const int kn = min(kKC, d - k0);
-    for (int kk = 0; kk < kn; kk++) {
-      const float v = Vr[(int64_t)(k0 + kk) * kR + j];
 #pragma unroll
-      for (int rr = 0; rr < QB; rr++) acc[rr] = __builtin_fmaf(xs[kk][rr], v, acc[rr]);
-    }
+    for (int kk = 0; kk < kKC; kk++) vcur[kk] = vnext[kk];
+    buf ^= 1;
   }
 
   // per-row max |z| over the 256 coordinates
@@ -74,35 +106,50 @@ __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, co
   }
 }
 
-// qc = <Q, c> (sequential double sum) and the fp16 copy of Q. One block per query.
-__global__ __launch_bounds__(256) void k_qc_cast(const float *__restrict__ Q, int d, const float *__restrict__ c,
-                                                 float *__restrict__ qc, uint16_t *__restrict__ qh) {
-  const int64_t q = blockIdx.x;
-  const float *qr = Q + q * d;
-  for (int k = threadIdx.x; k < d; k += 256) qh[q * d + k] = fvs_f2h(qr[k]);
-  if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int k = 0; k < d; k++) s += (double)qr[k] * (double)c[k];
-    qc[q] = (float)s;
+// Query code from the projected query z (R = 256: four coordinates per lane), plus qc = <Q, c> and
+// the fp16 copy of Q. One wave per query. qc: lane l sums the exact double products of coordinates
+// l, l+64, ... in order, then a fixed xor butterfly combines the 64 lane sums.
+__global__ __launch_bounds__(256) void k_query_code(const float *__restrict__ z, const float *__restrict__ Q, int64_t B,
+                                                    int d, const float *__restrict__ c, int8_t *__restrict__ q8,
+                                                    float *__restrict__ qs, float *__restrict__ qc,
+                                                    uint16_t *__restrict__ qh) {
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= B) return;
+  const int lane = threadIdx.x & 63;
+  const float4 zz = reinterpret_cast<const float4 *>(z + q * kR)[lane];
+  const float amax = fvs_wave_max(fmaxf(fmaxf(fabsf(zz.x), fabsf(zz.y)), fmaxf(fabsf(zz.z), fabsf(zz.w))));
+  const float a = fmaxf(amax, 1e-12f) / 127.0f;
+  const float zv[4] = {zz.x, zz.y, zz.z, zz.w};
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float qv = fminf(fmaxf(rintf(zv[i] / a), -127.0f), 127.0f);
+    packed |= ((uint32_t)(uint8_t)(int8_t)(int)qv) << (8 * i);
   }
+  reinterpret_cast<uint32_t *>(q8 + q * kR)[lane] = packed;
+  if (lane == 0) qs[q] = a;
+  const float *qr = Q + q * d;
+  double s = 0.0;
+  for (int k = lane; k < d; k += 64) {
+    const float x = qr[k];
+    qh[q * d + k] = fvs_f2h(x);
+    s += (double)x * (double)c[k];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, FVS_WAVE);
+  if (lane == 0) qc[q] = (float)s;
 }
 
 }  // namespace
 
-extern "C" int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *Vr, int32_t R, const float *c,
+extern "C" int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *z, int32_t R, const float *c,
                               int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream) {
   if (R != kR) return FVS_E_SHAPE;
   if (B < 0 || d <= 0 || d % 8 != 0) return FVS_E_ARG;
   if (B == 0) return FVS_OK;
-  if (!Q || !Vr || !c || !q8 || !qs || !qc || !qh) return FVS_E_ARG;
-  hipStream_t st = (hipStream_t)stream;
-  constexpr int QB = 8;
-  const int64_t nb = (B + QB - 1) / QB;
-  hipLaunchKernelGGL((k_project<QB, false>), dim3((unsigned)nb), dim3(256), 0, st, Q, nullptr, nullptr, nullptr,
-                     nullptr, B, d, Vr, q8, qs);
-  int e = fvs_launch_status();
-  if (e) return e;
-  hipLaunchKernelGGL(k_qc_cast, dim3((unsigned)B), dim3(256), 0, st, Q, d, c, qc, qh);
+  if (!Q || !z || !c || !q8 || !qs || !qc || !qh) return FVS_E_ARG;
+  hipLaunchKernelGGL(k_query_code, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, z, Q, B, d, c,
+                     q8, qs, qc, qh);
   return fvs_launch_status();
 }
 

@@ -1,86 +1,135 @@
 // Error-bar classification, exact scoring of the ambiguous candidates and the final top-k.
 //
-// One block (4 waves) per query. The two order statistics (k+1-th largest upper bound, k-th
-// largest lower bound) come from radix selects; the ambiguous slots are compacted in LDS and the
-// waves take them round-robin, each wave reading one fp16 row (coalesced 16-byte lane loads, from
-// HBM or from pinned host memory over PCIe) and reducing with a fixed butterfly.
+// One block (4 waves) per query. est/sd are staged once into LDS as the lower/upper interval keys;
+// the two order statistics (k+1-th largest upper bound, k-th largest lower bound) come from radix
+// selects over LDS. Ambiguous slots and their ids are compacted in LDS and the waves take them in
+// groups of four rows, so four fp16 rows (coalesced 16-byte lane loads, from HBM or pinned host
+// memory over PCIe) are in flight per wave; each lane keeps its slice of the query in registers,
+// and every row's partial sums are reduced with the same fixed butterfly.
 #include "fvs_common.h"
 
 namespace {
 
 constexpr int kMaxK = 4096;
 constexpr int kMaxk = 1024;
+constexpr int kRows = 4;       // rows in flight per wave
+constexpr int kMaxG = 8;       // 8-element groups per lane: d <= 8 * 64 * kMaxG = 4096
 
+struct RefineLds {  // fixed part; the per-slot arrays follow in dynamic LDS
+  uint64_t s[kMaxk];
+  int hist[256];
+  int sh[8];
+  int namb, gcnt;
+};
+
+template <int NG>
+__device__ __forceinline__ void dot_rows(const uint16_t *__restrict__ H, int d, const int32_t *ids, const int16_t *slots,
+                                         int a0, int na, const float (&qv)[NG][8], float *score, int lane) {
+  // rows a0 .. a0+kRows-1 of the ambiguous list (guarded), lane l covers groups l, l+64, ...
+  uint4 hv[kRows][NG];
+#pragma unroll
+  for (int r = 0; r < kRows; r++) {
+    const int a = a0 + r;
+    const int64_t id = a < na ? ids[a] : ids[a0];
+    const uint4 *hr = reinterpret_cast<const uint4 *>(H + id * d);
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      const int gi = lane + 64 * g;
+      hv[r][g] = gi * 8 < d ? hr[gi] : make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRows; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      if ((lane + 64 * g) * 8 < d) {
+        const uint32_t hw[4] = {hv[r][g].x, hv[r][g].y, hv[r][g].z, hv[r][g].w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          acc = __builtin_fmaf(fvs_h2f((uint16_t)(hw[u] & 0xffffu)), qv[g][2 * u], acc);
+          acc = __builtin_fmaf(fvs_h2f((uint16_t)(hw[u] >> 16)), qv[g][2 * u + 1], acc);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, FVS_WAVE);
+    if (lane == 0 && a0 + r < na) score[slots[a0 + r]] = acc;
+  }
+}
+
+template <int NG>
 __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, const float *__restrict__ sd,
                                                 const int32_t *__restrict__ pos, const int32_t *__restrict__ order,
                                                 const uint16_t *__restrict__ H, const float *__restrict__ Q, int K,
                                                 int d, float z, int k, int32_t *__restrict__ ids,
                                                 int32_t *__restrict__ Iout, float *__restrict__ scores,
                                                 int32_t *__restrict__ reads) {
-  __shared__ float score[kMaxK];
-  __shared__ uint8_t flag[kMaxK];  // 1 sure, 2 ambiguous
-  __shared__ int16_t amb[kMaxK];
-  __shared__ uint64_t s[kMaxk];
-  __shared__ int hist[256];
-  __shared__ int sh[8];
-  __shared__ int namb, gcnt;
+  __shared__ RefineLds L;
+  extern __shared__ uint8_t dyn[];
+  float *lo = reinterpret_cast<float *>(dyn);     // [K]
+  float *hi = lo + K;                            // [K]
+  float *score = hi + K;                         // [K]
+  int32_t *sid = reinterpret_cast<int32_t *>(score + K);  // [K] ids of the slots
+  int32_t *aid = sid + K;                        // [K] ids of the ambiguous slots
+  int16_t *amb = reinterpret_cast<int16_t *>(aid + K);    // [K]
+  uint8_t *flag = reinterpret_cast<uint8_t *>(amb + K);   // [K] 1 sure, 2 ambiguous
 
   const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x;
   const float *e = est + q * (int64_t)K;
   const float *g = sd + q * (int64_t)K;
-  auto lo = [&](int i) -> float { return e[i] - z * g[i]; };
-  auto hi = [&](int i) -> float { return e[i] + z * g[i]; };
-
-  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(hi(i)); }, K, k + 1, hist, sh));
-  const float lk = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(lo(i)); }, K, k, hist, sh));
-
-  if (threadIdx.x == 0) namb = 0;
+  const int32_t *pq = pos + q * (int64_t)K;
+  for (int i = tid; i < K; i += 256) {
+    const float t = z * g[i];
+    lo[i] = e[i] - t;
+    hi[i] = e[i] + t;
+    const int32_t id = order[pq[i]];
+    sid[i] = id;
+    ids[q * (int64_t)K + i] = id;
+  }
+  if (tid == 0) L.namb = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < K; i += 256) {
-    const float l = lo(i), h = hi(i);
-    const bool sure = l > hk1;
-    const bool am = (h >= lk) && !sure;
+  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(hi[i]); }, K, k + 1, L.hist, L.sh));
+  const float lk = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(lo[i]); }, K, k, L.hist, L.sh));
+  for (int i = tid; i < K; i += 256) {
+    const bool sure = lo[i] > hk1;
+    const bool am = (hi[i] >= lk) && !sure;
     flag[i] = sure ? 1 : (am ? 2 : 0);
     score[i] = sure ? e[i] + 10.0f : -1e9f;
-    ids[q * (int64_t)K + i] = order[pos[q * (int64_t)K + i]];
-    if (am) amb[atomicAdd(&namb, 1)] = (int16_t)i;
+    if (am) {
+      const int a = atomicAdd(&L.namb, 1);
+      amb[a] = (int16_t)i;
+      aid[a] = sid[i];
+    }
   }
   __syncthreads();
 
   // exact scores of the ambiguous candidates
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const float *qr = Q + q * (int64_t)d;
-  const int ng = d / 8;
-  for (int a = w; a < namb; a += 4) {
-    const int slot = amb[a];
-    const int64_t id = order[pos[q * (int64_t)K + slot]];
-    const uint4 *hr = reinterpret_cast<const uint4 *>(H + id * d);
-    float acc = 0.f;
-    for (int gi = lane; gi < ng; gi += 64) {
-      const uint4 hv = hr[gi];
-      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-      const float *qg = qr + 8 * gi;
+  const int lane = tid & 63, w = tid >> 6;
+  const int na = L.namb;
+  if (na > 0) {
+    float qv[NG][8];
+    const float *qr = Q + q * (int64_t)d;
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        acc = __builtin_fmaf(fvs_h2f((uint16_t)(hw[u] & 0xffffu)), qg[2 * u], acc);
-        acc = __builtin_fmaf(fvs_h2f((uint16_t)(hw[u] >> 16)), qg[2 * u + 1], acc);
-      }
+    for (int gg = 0; gg < NG; gg++) {
+      const int gi = lane + 64 * gg;
+#pragma unroll
+      for (int u = 0; u < 8; u++) qv[gg][u] = gi * 8 < d ? qr[gi * 8 + u] : 0.f;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, FVS_WAVE);
-    if (lane == 0) score[slot] = acc;
+    for (int a0 = w * kRows; a0 < na; a0 += 4 * kRows) dot_rows<NG>(H, d, aid, amb, a0, na, qv, score, lane);
   }
   __syncthreads();
-  if (threadIdx.x == 0) reads[q] = namb;
+  if (tid == 0) reads[q] = na;
 
   // final top-k by (score descending, slot ascending)
   auto key = [&](int i) -> uint64_t {
     return ((uint64_t)fvs_ord32(score[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   };
-  fvs_block_topk_u64(key, K, k, s, hist, sh, &gcnt);
-  for (int j = threadIdx.x; j < k; j += 256) {
-    const int slot = (int)(0xffffffffu - (uint32_t)(s[j] & 0xffffffffu));
-    Iout[q * (int64_t)k + j] = order[pos[q * (int64_t)K + slot]];
+  fvs_block_topk_u64(key, K, k, L.s, L.hist, L.sh, &L.gcnt);
+  for (int j = tid; j < k; j += 256) {
+    const int slot = (int)(0xffffffffu - (uint32_t)(L.s[j] & 0xffffffffu));
+    Iout[q * (int64_t)k + j] = sid[slot];
     scores[q * (int64_t)k + j] = flag[slot] == 1 ? e[slot] : score[slot];
   }
 }
@@ -91,10 +140,25 @@ extern "C" int fvs_refine(const float *est, const float *sd, const int32_t *pos,
                           const uint16_t *H, const float *Q, int64_t B, int32_t K, int32_t d, float z, int32_t k,
                           int32_t *ids, int32_t *I, float *scores, int32_t *reads, void *stream) {
   if (B < 0 || k <= 0 || K <= k || d <= 0 || d % 8 != 0 || !(z >= 0.f)) return FVS_E_ARG;
-  if (K > kMaxK || k > kMaxk) return FVS_E_CAPACITY;
+  if (K > kMaxK || k > kMaxk || d > 8 * 64 * kMaxG) return FVS_E_CAPACITY;
   if (B == 0) return FVS_OK;
   if (!est || !sd || !pos || !order || !H || !Q || !ids || !I || !scores || !reads) return FVS_E_ARG;
-  hipLaunchKernelGGL(k_refine, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, est, sd, pos, order, H, Q, K, d,
-                     z, k, ids, I, scores, reads);
+  const size_t shm = (size_t)K * (4 * 5 + 2 + 1);
+  hipStream_t st = (hipStream_t)stream;
+  const int ng = (d / 8 + 63) / 64;
+#define FVS_REFINE_LAUNCH(NG)                                                                                     \
+  hipLaunchKernelGGL(k_refine<NG>, dim3((unsigned)B), dim3(256), shm, st, est, sd, pos, order, H, Q, K, d, z, k, ids, \
+                     I, scores, reads)
+  if (ng <= 1)
+    FVS_REFINE_LAUNCH(1);
+  else if (ng <= 2)
+    FVS_REFINE_LAUNCH(2);
+  else if (ng <= 3)
+    FVS_REFINE_LAUNCH(3);
+  else if (ng <= 4)
+    FVS_REFINE_LAUNCH(4);
+  else
+    FVS_REFINE_LAUNCH(8);
+#undef FVS_REFINE_LAUNCH
   return fvs_launch_status();
 }

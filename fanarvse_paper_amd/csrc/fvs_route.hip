@@ -1,49 +1,117 @@
 // Routing (top-n_p cells per query) and the (query, cell) pair lists grouped by cell.
+//
+// Routing: one block per query. The query's NC fp16 scores are staged once in LDS as orderable
+// 16-bit keys; two 8-bit histogram passes (per-wave sub-histograms) find the n_p-th largest score
+// v*, every cell above v* plus the lowest-numbered cells equal to v* are gathered, and the n_p
+// selected keys (score << 16 | 0xffff - cell) are sorted in LDS.
+//
+// Pairs: instead of a global counting sort (atomics on popular cells serialise), the probe lists are
+// transposed into a cell-major rank matrix rank[c][q] (int16, -1 = not probed) in caller scratch.
+// Each cell's block then reads its row once to count and once to compact its queries in ascending
+// order -- the order of the reference's stable sort -- with no atomics and no per-cell sort.
 #include "fvs_common.h"
 
 namespace {
 
-constexpr int kMaxProbe = 4096;     // LDS capacity of the routing sort
-constexpr int kMaxCellPairs = 16384;  // LDS capacity of the per-cell pair sort
+constexpr int kMaxProbe = 4096;  // LDS capacity of the routing sort
+constexpr int kMaxNC = 16384;    // LDS capacity of the routing key row
 
-// One block per query: radix-select the n_p-th largest key, gather the n_p keys above it and sort
-// them. Key = (orderable fp16 score << 16) | (0xffff - cell): score descending, then cell ascending.
-__global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__ QM, int NC, int np,
-                                                    int32_t *__restrict__ probe) {
-  __shared__ uint64_t s[kMaxProbe];
-  __shared__ int hist[256];
-  __shared__ int sh[8];
-  __shared__ int cnt;
-  const int64_t q = blockIdx.x;
-  const uint16_t *row = QM + q * NC;
-  auto key = [&](int i) -> uint64_t {
-    return ((uint64_t)fvs_ord16(row[i]) << 16) | (uint64_t)(0xffffu - (uint32_t)i);
-  };
-  fvs_block_topk_u64(key, NC, np, s, hist, sh, &cnt);
-  for (int i = threadIdx.x; i < np; i += 256) probe[q * np + i] = (int32_t)(0xffffu - (uint32_t)(s[i] & 0xffffu));
+__device__ __forceinline__ int wave_hist_sum(int (*hist)[256], int b) {
+  return hist[0][b] + hist[1][b] + hist[2][b] + hist[3][b];
 }
 
-__global__ void k_pairs_count(const int32_t *__restrict__ probe, int64_t B, int npr, int n, int32_t *__restrict__ ccnt) {
+__global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__ QM, int NC, int np,
+                                                    int32_t *__restrict__ probe) {
+  __shared__ uint16_t v[kMaxNC];
+  __shared__ uint32_t s[kMaxProbe];
+  __shared__ int hist[4][256];
+  __shared__ int sh[16];
+  __shared__ int cnt;
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6;
+  const uint16_t *row = QM + q * NC;
+  for (int i = tid; i < NC; i += 256) v[i] = (uint16_t)fvs_ord16(row[i]);
+  int want = np;
+  uint32_t prefix = 0;
+  for (int pass = 0; pass < 2; pass++) {
+    for (int i = tid; i < 4 * 256; i += 256) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < NC; i += 256) {
+      const uint32_t x = v[i];
+      if (pass == 0)
+        atomicAdd(&hist[w][x >> 8], 1);
+      else if ((x >> 8) == prefix)
+        atomicAdd(&hist[w][x & 255], 1);
+    }
+    __syncthreads();
+    const int b = 255 - tid;
+    const int h = wave_hist_sum(hist, b);
+    const int inc = fvs_block_scan256(h, sh);
+    const int exc = inc - h;
+    if (exc < want && want <= inc) {
+      sh[8] = b;
+      sh[9] = want - exc;
+    }
+    __syncthreads();
+    prefix = pass == 0 ? (uint32_t)sh[8] : ((prefix << 8) | (uint32_t)sh[8]);
+    want = sh[9];
+    __syncthreads();
+  }
+  const uint32_t vstar = prefix;  // the n_p-th largest key; `want` of its ties are taken
+  if (tid == 0) cnt = 0;
+  __syncthreads();
+  int run = 0;  // ties already taken, in cell order
+  for (int base = 0; base < NC; base += 256) {
+    const int i = base + tid;
+    const uint32_t x = i < NC ? (uint32_t)v[i] : 0u;
+    const bool gt = i < NC && x > vstar;
+    const bool eq = i < NC && x == vstar;
+    if (gt) s[atomicAdd(&cnt, 1)] = (x << 16) | (0xffffu - (uint32_t)i);
+    const int neq = __syncthreads_count(eq);
+    if (neq > 0 && run < want) {
+      const int rk = fvs_block_scan256(eq ? 1 : 0, sh) - 1;
+      if (eq && run + rk < want) s[atomicAdd(&cnt, 1)] = (x << 16) | (0xffffu - (uint32_t)i);
+    }
+    run += neq;
+  }
+  __syncthreads();
+  const int P = fvs_pow2_ceil(np);
+  for (int i = np + tid; i < P; i += 256) s[i] = 0u;
+  __syncthreads();
+  fvs_block_bitonic<uint32_t, true>(s, P);
+  for (int i = tid; i < np; i += 256) probe[q * np + i] = (int32_t)(0xffffu - (s[i] & 0xffffu));
+}
+
+// rank[c][q] = r for the first n probe columns (the matrix is pre-filled with 0xffff).
+__global__ void k_rank_scatter(const int32_t *__restrict__ probe, int64_t B, int npr, int n, uint16_t *__restrict__ rank) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= B * n) return;
   const int64_t q = t / n;
   const int r = (int)(t % n);
-  atomicAdd(&ccnt[probe[q * npr + r]], 1);
+  rank[(int64_t)probe[q * npr + r] * B + q] = (uint16_t)r;
 }
 
-// Exclusive prefix sum of ccnt into coff; clears fill. One block of 256 threads.
-__global__ __launch_bounds__(256) void k_pairs_scan(const int32_t *__restrict__ ccnt, int NC, int32_t *__restrict__ coff,
-                                                    int32_t *__restrict__ fill) {
+// ccnt[c] = number of queries probing cell c.
+__global__ __launch_bounds__(256) void k_cell_count(const uint16_t *__restrict__ rank, int64_t B,
+                                                    int32_t *__restrict__ ccnt) {
+  __shared__ int sh[8];
+  const int c = blockIdx.x;
+  const uint16_t *rr = rank + (int64_t)c * B;
+  int m = 0;
+  for (int64_t q = threadIdx.x; q < B; q += 256) m += rr[q] != 0xffffu;
+  const int tot = fvs_block_scan256(m, sh);
+  if (threadIdx.x == 255) ccnt[c] = tot;
+}
+
+// Exclusive prefix sum of ccnt into coff. One block of 256 threads.
+__global__ __launch_bounds__(256) void k_cell_scan(const int32_t *__restrict__ ccnt, int NC, int32_t *__restrict__ coff) {
   __shared__ int tmp[8];
   int run = 0;
   for (int base = 0; base < NC; base += 256) {
     const int c = base + (int)threadIdx.x;
     const int v = c < NC ? ccnt[c] : 0;
     const int inc = fvs_block_scan256(v, tmp);
-    if (c < NC) {
-      coff[c] = run + inc - v;
-      fill[c] = 0;
-    }
+    if (c < NC) coff[c] = run + inc - v;
     if (threadIdx.x == 255) tmp[4] = inc;
     __syncthreads();
     run += tmp[4];
@@ -51,79 +119,69 @@ __global__ __launch_bounds__(256) void k_pairs_scan(const int32_t *__restrict__ 
   }
 }
 
-// Scatter each (q, r) pair into its cell's range; packs (q << 12 | r) into qid until the sort.
-__global__ void k_pairs_scatter(const int32_t *__restrict__ probe, int64_t B, int npr, int n,
-                                const int32_t *__restrict__ coff, int32_t *__restrict__ fill,
-                                int32_t *__restrict__ qid) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= B * n) return;
-  const int64_t q = t / n;
-  const int r = (int)(t % n);
-  const int c = probe[q * npr + r];
-  const int slot = coff[c] + atomicAdd(&fill[c], 1);
-  qid[slot] = (int32_t)(((uint32_t)q << 12) | (uint32_t)r);
-}
-
-// One block per cell: sort the cell's packed pairs by query (queries are unique within a cell, so
-// the order equals the stable-sort order), unpack, and gather the pair constants.
-__global__ __launch_bounds__(256) void k_pairs_sort(const int32_t *__restrict__ ccnt, const int32_t *__restrict__ coff,
-                                                    const uint16_t *__restrict__ QM, const float *__restrict__ mnorm,
-                                                    int NC, int32_t *__restrict__ qid, int32_t *__restrict__ qrank,
-                                                    float *__restrict__ qcp) {
-  __shared__ uint32_t s[kMaxCellPairs];
+// One block per cell: its queries in ascending order, their probe ranks and pair constants.
+__global__ __launch_bounds__(256) void k_cell_emit(const uint16_t *__restrict__ rank, int64_t B,
+                                                   const int32_t *__restrict__ coff, const uint16_t *__restrict__ QM,
+                                                   const float *__restrict__ mnorm, int NC, int32_t *__restrict__ qid,
+                                                   int32_t *__restrict__ qrank, float *__restrict__ qcp) {
+  __shared__ int sh[8];
   const int c = blockIdx.x;
-  const int cnt = ccnt[c];
-  // cnt <= B <= kMaxCellPairs when probe rows hold distinct cells (as fvs_route_topk writes them);
-  // a malformed probe with repeated cells is left unsorted rather than overrunning LDS.
-  if (cnt == 0 || cnt > kMaxCellPairs) return;
-  const int base = coff[c];
-  const int P = fvs_pow2_ceil(cnt);
-  for (int i = threadIdx.x; i < P; i += 256) s[i] = i < cnt ? (uint32_t)qid[base + i] : 0xffffffffu;
-  __syncthreads();
-  fvs_block_bitonic<uint32_t, false>(s, P);
+  const uint16_t *rr = rank + (int64_t)c * B;
   const float sc = mnorm ? mnorm[c] : 1.0f;
-  for (int i = threadIdx.x; i < cnt; i += 256) {
-    const uint32_t v = s[i];
-    const int64_t q = v >> 12;
-    qid[base + i] = (int32_t)q;
-    qrank[base + i] = (int32_t)(v & 0xfffu);
-    qcp[base + i] = fvs_h2f(QM[q * NC + c]) * sc;
+  int run = coff[c];
+  for (int64_t base = 0; base < B; base += 256) {
+    const int64_t q = base + threadIdx.x;
+    const uint16_t r = q < B ? rr[q] : (uint16_t)0xffffu;
+    const bool f = r != 0xffffu;
+    const int inc = fvs_block_scan256(f ? 1 : 0, sh);
+    if (f) {
+      const int o = run + inc - 1;
+      qid[o] = (int32_t)q;
+      qrank[o] = (int32_t)r;
+      qcp[o] = fvs_h2f(QM[q * NC + c]) * sc;
+    }
+    if (threadIdx.x == 255) sh[6] = inc;
+    __syncthreads();
+    run += sh[6];
+    __syncthreads();
   }
 }
 
 }  // namespace
 
 extern "C" int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t nprobe, int32_t *probe, void *stream) {
-  if (B < 0 || NC <= 0 || NC > 65536 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
-  if (nprobe > kMaxProbe) return FVS_E_CAPACITY;
+  if (B < 0 || NC <= 0 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
+  if (nprobe > kMaxProbe || NC > kMaxNC) return FVS_E_CAPACITY;
   if (B == 0) return FVS_OK;
   if (!QM || !probe) return FVS_E_ARG;
   hipLaunchKernelGGL(k_route_topk, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, QM, NC, nprobe, probe);
   return fvs_launch_status();
 }
 
+extern "C" int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC) {
+  if (B < 0 || NC <= 0) return -1;
+  return ((int64_t)NC * B * 2 + 255) / 256 * 256;
+}
+
 extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
-                         const float *mnorm, int32_t *ccnt, int32_t *coff, int32_t *fill, int32_t *qid,
-                         int32_t *qrank, float *qcp, void *stream) {
-  if (B < 0 || NC <= 0 || n <= 0 || n > npr || n > 4096) return FVS_E_ARG;
-  if (B >= (1 << 20)) return FVS_E_ARG;
-  if (B > kMaxCellPairs) return FVS_E_CAPACITY;  // a cell can be probed by every query
-  if (!probe || !QM || !ccnt || !coff || !fill || !qid || !qrank || !qcp) return FVS_E_ARG;
+                         const float *mnorm, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes,
+                         int32_t *qid, int32_t *qrank, float *qcp, void *stream) {
+  if (B < 0 || NC <= 0 || n <= 0 || n > npr || n > 65535) return FVS_E_ARG;
+  if (scratch_bytes < fvs_pairs_scratch_bytes(B, NC)) return FVS_E_CAPACITY;
+  if (!probe || !QM || !ccnt || !coff || !scratch || !qid || !qrank || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  int e = fvs_fill_u32(ccnt, NC, 0u, stream);
-  if (e) return e;
-  if (B == 0) {
-    hipLaunchKernelGGL(k_pairs_scan, dim3(1), dim3(256), 0, st, ccnt, NC, coff, fill);
-    return fvs_launch_status();
+  uint16_t *rank = reinterpret_cast<uint16_t *>(scratch);
+  int e;
+  if (B > 0) {
+    if ((e = fvs_fill_u32(rank, ((int64_t)NC * B * 2 + 3) / 4, 0xffffffffu, stream))) return e;
+    const int64_t tot = B * (int64_t)n;
+    hipLaunchKernelGGL(k_rank_scatter, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, probe, B, npr, n, rank);
+    if ((e = fvs_launch_status())) return e;
   }
-  const int64_t tot = B * (int64_t)n;
-  const unsigned g = (unsigned)((tot + 255) / 256);
-  hipLaunchKernelGGL(k_pairs_count, dim3(g), dim3(256), 0, st, probe, B, npr, n, ccnt);
+  hipLaunchKernelGGL(k_cell_count, dim3((unsigned)NC), dim3(256), 0, st, rank, B, ccnt);
   if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_pairs_scan, dim3(1), dim3(256), 0, st, ccnt, NC, coff, fill);
+  hipLaunchKernelGGL(k_cell_scan, dim3(1), dim3(256), 0, st, ccnt, NC, coff);
   if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_pairs_scatter, dim3(g), dim3(256), 0, st, probe, B, npr, n, coff, fill, qid);
-  if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_pairs_sort, dim3((unsigned)NC), dim3(256), 0, st, ccnt, coff, QM, mnorm, NC, qid, qrank, qcp);
+  hipLaunchKernelGGL(k_cell_emit, dim3((unsigned)NC), dim3(256), 0, st, rank, B, coff, QM, mnorm, NC, qid, qrank, qcp);
   return fvs_launch_status();
 }

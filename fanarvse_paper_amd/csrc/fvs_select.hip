@@ -3,7 +3,7 @@
 
 namespace {
 
-constexpr int kMaxK = 4096;     // LDS capacity of the sorted top-K
+constexpr int kMaxK = 4096;     // LDS capacity of the sorted top-K (dynamic)
 constexpr int kMaxN1 = 4096;
 
 __device__ __forceinline__ int cell_blocks(const int32_t *off, int c) {
@@ -43,11 +43,18 @@ __global__ __launch_bounds__(256) void k_threshold(const float *__restrict__ bm,
 }
 
 // One block per query: top-K of the first min(cnt, M) buffer entries by (est desc, pos asc).
+// Buffers of up to kStage entries are staged once into LDS as 64-bit keys (vectorised loads) and the
+// radix passes run over LDS; larger ones (the fallback's 65,536-entry buffers) are read from global.
+constexpr int kStage = 4096;
+
 __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, const int32_t *__restrict__ bpos,
                                                 const int32_t *__restrict__ cntp, int M, int K, int kd, float delta,
                                                 int32_t *__restrict__ pos, float *__restrict__ est1,
                                                 uint8_t *__restrict__ ok, int32_t *__restrict__ ncnt) {
-  __shared__ uint64_t s[kMaxK];
+  extern __shared__ uint64_t dyn64[];
+  const int P = fvs_pow2_ceil(K);
+  uint64_t *s = dyn64;           // [P] the sorted top-K
+  uint64_t *keys = dyn64 + P;    // [min(M, kStage)] staged buffer
   __shared__ int hist[256];
   __shared__ int sh[8];
   __shared__ int gcnt;
@@ -56,18 +63,42 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, 
   const int n = min(cq, M);
   const float *bv = bval + q * (int64_t)M;
   const int32_t *bp = bpos + q * (int64_t)M;
-  auto key = [&](int i) -> uint64_t {
+  auto gkey = [&](int i) -> uint64_t {
     return ((uint64_t)fvs_ord32(bv[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)bp[i]);
   };
+  const bool staged = n <= kStage;
+  if (staged) {
+    const bool vec = (M & 3) == 0;
+    if (vec) {
+      const float4 *bv4 = reinterpret_cast<const float4 *>(bv);
+      const int4 *bp4 = reinterpret_cast<const int4 *>(bp);
+#pragma unroll 4
+      for (int i = threadIdx.x; i < (n + 3) / 4; i += 256) {
+        const float4 v = bv4[i];
+        const int4 p = bp4[i];
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        const int pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+          if (4 * i + u < n) keys[4 * i + u] = ((uint64_t)fvs_ord32(vv[u]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)pp[u]);
+      }
+    } else {
+      for (int i = threadIdx.x; i < n; i += 256) keys[i] = gkey(i);
+    }
+    __syncthreads();
+  }
   int have;
   if (n >= K) {
-    fvs_block_topk_u64(key, n, K, s, hist, sh, &gcnt);
+    if (staged)
+      fvs_block_topk_u64([&](int i) { return keys[i]; }, n, K, s, hist, sh, &gcnt);
+    else
+      fvs_block_topk_u64(gkey, n, K, s, hist, sh, &gcnt);
     have = K;
   } else {
-    const int P = fvs_pow2_ceil(n > 0 ? n : 1);
-    for (int i = threadIdx.x; i < P; i += 256) s[i] = i < n ? key(i) : 0ull;
+    const int Pn = fvs_pow2_ceil(n > 0 ? n : 1);
+    for (int i = threadIdx.x; i < Pn; i += 256) s[i] = i < n ? (staged ? keys[i] : gkey(i)) : 0ull;
     __syncthreads();
-    fvs_block_bitonic<uint64_t, true>(s, P);
+    fvs_block_bitonic<uint64_t, true>(s, Pn);
     have = n;
   }
   float *e1 = est1 + q * (int64_t)K;
@@ -116,7 +147,8 @@ extern "C" int fvs_select(const float *bval, const int32_t *bpos, const int32_t 
   if (K > kMaxK) return FVS_E_CAPACITY;
   if (B == 0) return FVS_OK;
   if (!bval || !bpos || !cnt || !pos || !est1 || !ok || !ncnt) return FVS_E_ARG;
-  hipLaunchKernelGGL(k_select, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bval, bpos, cnt, M, K, kd, delta,
-                     pos, est1, ok, ncnt);
+  const size_t shm = 8 * ((size_t)fvs_pow2_ceil(K) + (size_t)(M < kStage ? M : kStage));
+  hipLaunchKernelGGL(k_select, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, bval, bpos, cnt, M, K, kd,
+                     delta, pos, est1, ok, ncnt);
   return fvs_launch_status();
 }

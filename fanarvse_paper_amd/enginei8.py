@@ -53,7 +53,8 @@ class EngineI8:
         self.s1, self.code, self.Z, self.zs, self.Vr = s1, code, Z, zs, Vr.contiguous()
         self.H = H
         s2lut.prepare_u(code)
-        self.blocks, self.MB = index.static_blocks(s1["off_t"], self.BN)
+        _, self.MB = index.static_blocks(s1["off_t"], self.BN)
+        self.blocks = index.static_chunks(s1["off_t"], self.BN)
         N = Z.shape[0]
         if int(s1["off_t"][-1]) != N or int(self.blocks[3].max()) > N:
             raise ValueError("EngineI8: cell offsets do not match the code rows")
@@ -93,9 +94,10 @@ class EngineI8:
         s1 = self.s1
         NC = len(s1["off"]) - 1
         B = Qb.shape[0]
-        q8, qs, _, _ = qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"])
+        q8, qs = (qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"]))[:2]
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
-        pr = _lib.pairs(probe, n1, NC, QM, self.mnorm)
+        scratch = _lib.pairs_scratch(B, NC, Qb.device)
+        pr = _lib.pairs(probe, n1, NC, QM, self.mnorm, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=Qb.device)
         _lib.i8_scan(0, self.blocks, q8, qs, pr, self.Z, self.zs, bm=bm, MB=self.MB, n1=n1)
         t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
@@ -103,7 +105,7 @@ class EngineI8:
         _lib.fill_u32(cnt, 0)
         bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
         bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
-        pr = _lib.pairs(probe, probe.shape[1], NC, QM, self.mnorm)
+        pr = _lib.pairs(probe, probe.shape[1], NC, QM, self.mnorm, scratch)
         _lib.i8_scan(1, self.blocks, q8, qs, pr, self.Z, self.zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
         pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, min(kd, K - 1), delta)
         self._est1, self._ncnt, self._t0, self._cnt = est1, ncnt, t0, cnt
@@ -115,20 +117,20 @@ class EngineI8:
         return QM, _lib.route_topk(QM, nprobe)
 
     def _gpu(self, Qb, K, z, nprobe, k):
-        """One batch on the GPU without host synchronisation: (ok, I, reads, ids, scores, QM, Zq); the two
-        BLAS products are returned so that the fallback reuses their rows."""
+        """One batch on the GPU without host synchronisation: (ok, I, reads, ids, scores, blas); blas holds the
+        three BLAS products (z, QM, Zq) so that the fallback reuses their rows."""
         self._check_knobs()
         if self.H is None:
             raise RuntimeError("EngineI8.H (fp16 vectors in id order) must be set before searching")
         s1 = self.s1
         qp = _lib.query_prep(Qb, self.Vr, s1["c"])
-        q8, qs, QC, Qh = qp
+        q8, qs, QC, Qh, zq = qp
         QM, probe = self._route(Qh, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         Zq = s2lut.rotate(self.code, Qh)
         ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=self.LUTF and self.LUTH,
                                                  ncnt=self._ncnt if self.DELTA is not None else None)
-        return ok, I, reads, ids, scores, QM, Zq
+        return ok, I, reads, ids, scores, (zq, QM, Zq)
 
     def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt):
         """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95)."""
@@ -157,23 +159,23 @@ class EngineI8:
             with torch.cuda.graph(g):
                 outs = self._gpu(qs, K, z, nprobe, k)
             self.graphs[key] = (g, qs, outs)
-        g, qs, (ok, I, nr, ids, sc, QM, Zq) = self.graphs[key]
+        g, qs, (ok, I, nr, ids, sc, blas) = self.graphs[key]
         qs.copy_(Qb)
         g.replay()
         I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
         if not bool(ok.all()):
             bad = torch.nonzero(~ok).flatten()
             self.nbad += len(bad)
-            a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, QM[bad].contiguous(), Zq[bad].contiguous())
+            a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, *[t[bad].contiguous() for t in blas])
             I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
         return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
 
-    def _fallback(self, Qb, K, z, nprobe, k, QM=None, Zq=None):
+    def _fallback(self, Qb, K, z, nprobe, k, zq=None, QM=None, Zq=None):
         """Flagged queries again with r = K, n1 over 1.5K blocks, M = 65,536, an fp32 LUT and every
-        candidate scored (throughput/enginei8.py:112-120). QM / Zq: the rows of the main pass's BLAS
+        candidate scored (throughput/enginei8.py:112-120). zq / QM / Zq: the rows of the main pass's BLAS
         products for these queries (recomputed when not given)."""
-        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
-        q8, qs, QC, Qh = qp
+        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"], zq)
+        q8, qs, QC, Qh, _ = qp
         if QM is None:
             QM = Qh @ self.meansN.T
         probe = _lib.route_topk(QM, nprobe)
@@ -189,7 +191,7 @@ class EngineI8:
         self._check_knobs()
         Qb = Qb.float().contiguous()
         qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
-        q8, qs, QC, Qh = qp
+        q8, qs, QC, Qh, zq = qp
         QM, probe = self._route(Qh, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         half = self.LUTF and self.LUTH
@@ -198,7 +200,7 @@ class EngineI8:
         pre = _lib.lut_build(Zq, self.code["TS"], half)
         est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
         ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
-        return dict(q8=q8, qs=qs, QC=QC, Qh=Qh, QM=QM, probe=probe, bm=self._bm, n1=self._n1, M=self._M,
+        return dict(q8=q8, qs=qs, QC=QC, Qh=Qh, z=zq, QM=QM, probe=probe, bm=self._bm, n1=self._n1, M=self._M,
                     t0=self._t0, cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, est1=self._est1, ok=ok,
                     ncnt=self._ncnt, Zq=Zq, L=pre[0], qsum=pre[1], qn2=pre[2], est=est, sd=sd, ids=ids, I=I,
                     scores=scores, reads=reads)

@@ -88,6 +88,21 @@ def static_blocks(off_t, BN=32):
     return (i32(cell), i32(blk), i32(s[cell]), i32(e[cell])), MB
 
 
+def static_chunks(off_t, BN=32, CB=8):
+    """Work items of the stage-1 kernels: every cell's static blocks (static_blocks) grouped into chunks of
+    up to CB consecutive blocks. Returns (cell, first global block, cell start, cell end) int32 tensors;
+    each item covers blocks [blk0, min(blk0 + CB, last block of the cell + 1))."""
+    off = off_t.long()
+    s, e = off[:-1], off[1:]
+    nb = torch.where(e > s, (e - 1) // BN - s // BN + 1, torch.zeros_like(s))
+    nch = (nb + CB - 1) // CB
+    cell = torch.repeat_interleave(torch.arange(len(s), device=off.device), nch)
+    first = torch.cumsum(nch, 0) - nch
+    blk0 = s[cell] // BN + CB * (torch.arange(len(cell), device=off.device) - first[cell])
+    i32 = lambda x: x.to(torch.int32).contiguous()
+    return i32(cell), i32(blk0), i32(s[cell]), i32(e[cell])
+
+
 def build_index(X16, nlist=4096, R=256, bits_per_dim=2.5, seed=0, with_codes=True):
     """Everything EngineI8 needs: (s1, code, Z, zs, Vr). X16: fp16 [N, d] in id order."""
     s1 = build_stage1_cells(X16, nlist, seed)

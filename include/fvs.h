@@ -48,16 +48,17 @@ int fvs_fill_u32(void *dst, int64_t n, uint32_t value, void *stream);
 
 /*
  * Query code (a6) plus the global-centre term and the fp16 copy of the queries.
- * Replaces throughput/enginei8.py:38 (z = Qb @ Vr; qs = max|z|/127; q8 = round(z/qs)),
- * throughput/enginei8.py:62 (QC = Qb @ c) and the Qb.half() casts at :67 and s2lut.py:122.
- *   Q  f32 [B, d] row-major; Vr f32 [d, R]; c f32 [d]
+ * Replaces throughput/enginei8.py:38 (qs = max|z|/127; q8 = round(z/qs), with z = Qb @ Vr computed by
+ * the caller's fp32 BLAS as in the reference), throughput/enginei8.py:62 (QC = Qb @ c) and the
+ * Qb.half() casts at :67 and s2lut.py:122.
+ *   Q  f32 [B, d] row-major; z f32 [B, R] = Q @ Vr; c f32 [d]
  *   q8 i8 [B, R]; qs f32 [B]; qc f32 [B]; qh fp16 [B, d]
- * Canonical order: z[j] = fmaf(Q[k], Vr[k][j], z[j]) for k = 0..d-1 from +0;
- *   qs = max(max_j |z[j]|, 1e-12f) / 127.0f; q8[j] = clamp(rintf(z[j] / qs), -127, 127);
- *   qc = (float) sum_k (double)Q[k]*(double)c[k], summed in k order in double.
+ * Canonical order: qs = max(max_j |z[j]|, 1e-12f) / 127.0f; q8[j] = clamp(rintf(z[j] / qs), -127, 127);
+ *   qc = (float) of the double sum of the (exact) products (double)Q[k]*(double)c[k]: lane l = k % 64
+ *   accumulates its products in k order, then lane[l] += lane[l ^ o] for o = 32, 16, 8, 4, 2, 1.
  * R must be 256; d must be a multiple of 8.
  */
-int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *Vr, int32_t R, const float *c,
+int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *z, int32_t R, const float *c,
                    int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream);
 
 /*
@@ -65,8 +66,9 @@ int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *Vr, int32_
  *   X16 fp16 [n_ids, d] in id order; order i32 [N] (sorted position -> id);
  *   cell i32 [N] (cell of each sorted position); means16 fp16 [NC, d]; Vr f32 [d, R]
  *   Z i8 [N, R] in sorted order; zs f32 [N]
- * Canonical order: x[k] = (float)X16[order[n]][k] - (float)means16[cell[n]][k] (one f32 subtraction),
- *   then the projection and quantisation of fvs_query_prep.
+ * Canonical order: x[k] = (float)X16[order[n]][k] - (float)means16[cell[n]][k] (one f32 subtraction);
+ *   z[j] = fmaf(x[k], Vr[k][j], z[j]) for k = 0..d-1 from +0 (a build-time kernel, so every output is
+ *   one sequential chain); then the quantisation of fvs_query_prep.
  */
 int fvs_build_codes(const uint16_t *X16, const int32_t *order, const int32_t *cell, int64_t N, int32_t d,
                     const uint16_t *means16, const float *Vr, int32_t R, int8_t *Z, float *zs, void *stream);
@@ -74,23 +76,24 @@ int fvs_build_codes(const uint16_t *X16, const int32_t *order, const int32_t *ce
 /*
  * Routing top-n_p (a7). Replaces `probe = QM.topk(nprobe, 1).indices` (throughput/enginei8.py:68).
  *   QM fp16 [B, NC]; probe i32 [B, nprobe], each row sorted by (QM value descending, cell ascending);
- *   -0 and +0 compare equal. nprobe <= min(NC, 4096).
+ *   -0 and +0 compare equal. nprobe <= min(NC, 4096), NC <= 16384.
  */
 int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t nprobe, int32_t *probe, void *stream);
 
 /*
  * (query, cell) pairs grouped by cell (a8). Replaces pairs_fast (throughput/enginei8.py:11-16) with
  * scale = |m_c| (the NROUTE branch, :47).
- *   probe i32 [B, npr] (only the first n columns are used); QM fp16 [B, NC]; mnorm f32 [NC] or NULL (scale 1)
+ *   probe i32 [B, npr] (only the first n columns are used; a row holds distinct cells);
+ *   QM fp16 [B, NC]; mnorm f32 [NC] or NULL (scale 1)
  *   ccnt i32 [NC]  number of pairs of each cell      coff i32 [NC]  exclusive prefix of ccnt
- *   fill i32 [NC]  scratch                            qid i32 [B*n]  query of each pair, cell-major,
- *                                                     queries ascending inside a cell (the stable-sort order)
+ *   scratch        at least fvs_pairs_scratch_bytes(B, NC) bytes (a cell-major probe-rank matrix)
+ *   qid i32 [B*n]  query of each pair, cell-major, queries ascending inside a cell (the stable-sort order)
  *   qrank i32 [B*n] rank of the cell in the query's probe row     qcp f32 [B*n] = (float)QM[q][c] * mnorm[c]
- * At most 16384 pairs per cell.
  */
+int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC);
 int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
-              const float *mnorm, int32_t *ccnt, int32_t *coff, int32_t *fill, int32_t *qid, int32_t *qrank,
-              float *qcp, void *stream);
+              const float *mnorm, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes, int32_t *qid,
+              int32_t *qrank, float *qcp, void *stream);
 
 /*
  * int8 stage-1 scan on MFMA (a9, a11). Same inputs and outputs as the reference's CUDA twin
@@ -98,8 +101,10 @@ int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t N
  * bpos, bmc, CAP, MB) (throughput/civf8.py:89-91), which the Triton pair _first8c/_emit8c
  * (throughput/ivf8c_kern.py:2-36) also implements; plus qrank/n1 so that the first pass writes each
  * query's block maxima straight into its own row.
- *   One program per static (cell, 32-row block) item p < P (pcell, pblk, ps, pe: the cell, the global
- *   block index, and the cell's first and end row). For every query q of the cell's pair list:
+ *   One workgroup per item p < P: a cell and up to 8 consecutive global 32-row blocks of it (pcell, pblk,
+ *   ps, pe: the cell, the first global block index, and the cell's first and end row; the item covers
+ *   blocks pblk .. min(pblk + 7, (pe - 1) / 32)). The items must cover each static (cell, block) of the
+ *   reference's work list (src/s1cell.py:161-168) exactly once. For every query q of the cell's pair list:
  *     acc = sum_j q8[q][j] * Z[n][j] (int32, exact), est = fmaf((float)acc * qs[q], zs[n], qcp[pair]).
  *   mode 0 (first pass): bm[(q*n1 + qrank[pair])*MB + blk - cs/32] = max over the block's rows in the
  *     cell; entries of blocks a cell does not have are left untouched.
@@ -141,8 +146,8 @@ int fvs_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64
  *   Zq fp16 [B, D] (the rotated queries, Qb.half() @ VP16[:, :D]); tiers i32 [T][3] = (start, end, bits)
  *   is a HOST array. L [B, D/4*16] is fp16 when half != 0, else f32:
  *     L[q][n*16 + v] = sum_{i<4} Zq[q][4n+i] * ((v >> (3-i)) & 1), as fmaf in i order from +0.
- *   qsum, qn2 f32 [T, B]: (float) of the sums over the tier's coordinates of Zq and Zq^2, in double,
- *   in coordinate order.
+ *   qsum, qn2 f32 [T, B]: (float) of the double sums over the tier's coordinates of Zq and Zq^2, with
+ *   the 64-lane order of qc (lane = offset inside the tier % 64, then the xor butterfly).
  */
 int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int32_t *tiers, int32_t half,
                   void *L, float *qsum, float *qn2, void *stream);
@@ -157,8 +162,9 @@ int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int
  * Canonical arithmetic: each LUT entry is turned into the integer fx = rint(L * 2^(24-s)), with
  * s = max(0, E - 3) where max|L| of the query = f * 2^E, f in [0.5, 1) (frexp); the tier sums
  *   A_t = sum_p 2^(b-1-p) sum_j (fx[hi nibble] + fx[lo nibble]) are exact integers. Then, in f32:
- *   a = ldexpf((float)A_t, s - 24); a = delta_t * (a - mid_t * qsum[t]); est += a * scale_t;
- *   var += (qn2[t] * sig_t) * sig_t, for t = 0..T-1, from est = qc[q], var = 0; sd = sqrtf(var).
+ *   a = ldexpf((float)A_t, s - 24); a = delta_t * fmaf(-mid_t, qsum[t], a); est = fmaf(a, scale_t, est);
+ *   var = fmaf(qn2[t] * sig_t, sig_t, var), for t = 0..T-1, from est = qc[q], var = 0; sd = sqrtf(var)
+ *   (the multiply-adds fused as the reference's compiled kernel fuses them).
  */
 int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
                   const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB, int32_t soff,

@@ -22,17 +22,19 @@ static inline uint16_t f2h(float f) { return (uint16_t)_cvtss_sh(f, _MM_FROUND_T
 
 /* ---------------------------------------------------------------- query code (a6)
  * throughput/enginei8.py:38  z = Qb @ Vr; qs = z.abs().amax(1).clamp(min=1e-12) / 127;
- *                            q8 = round(z / qs).clamp(-127, 127)
+ *                            q8 = round(z / qs).clamp(-127, 127)   (R <= 1024)
  * throughput/enginei8.py:62  QC = Qb @ c
  */
-static void proj_quant_row(const float *x, int d, const float *Vr, int R, int8_t *out8, float *outs) {
-  float z[1024];
+static void project_row(const float *x, int d, const float *Vr, int R, float *z) {
   for (int j = 0; j < R; j++) z[j] = 0.f;
   for (int k = 0; k < d; k++) {
     const float xk = x[k];
     const float *v = Vr + (int64_t)k * R;
     for (int j = 0; j < R; j++) z[j] = fmaf(xk, v[j], z[j]);
   }
+}
+
+static void quant_row(const float *z, int R, int8_t *out8, float *outs) {
   float amax = 0.f;
   for (int j = 0; j < R; j++) amax = fmaxf(amax, fabsf(z[j]));
   const float a = fmaxf(amax, 1e-12f) / 127.0f;
@@ -44,15 +46,33 @@ static void proj_quant_row(const float *x, int d, const float *Vr, int R, int8_t
   *outs = a;
 }
 
-void or_query_prep(const float *Q, int64_t B, int d, const float *Vr, int R, const float *c, int8_t *q8, float *qs,
+/* 64 lane partial sums combined by the xor butterfly of a wave: lane[l] += lane[l ^ o], o = 32..1. */
+static double butterfly64_d(double *lane) {
+  for (int o = 32; o > 0; o >>= 1) {
+    double t[64];
+    for (int l = 0; l < 64; l++) t[l] = lane[l] + lane[l ^ o];
+    memcpy(lane, t, sizeof(t));
+  }
+  return lane[0];
+}
+
+/* z = Q @ Vr with one sequential fmaf chain per output (the CPU baseline's own product; the GPU uses
+ * its BLAS, and parity tests hand the GPU's z to or_query_prep). */
+void or_project(const float *Q, int64_t B, int d, const float *Vr, int R, float *z) {
+#pragma omp parallel for schedule(static)
+  for (int64_t q = 0; q < B; q++) project_row(Q + q * d, d, Vr, R, z + q * R);
+}
+
+void or_query_prep(const float *Q, int64_t B, int d, const float *z, int R, const float *c, int8_t *q8, float *qs,
                    float *qc, uint16_t *qh) {
 #pragma omp parallel for schedule(static)
   for (int64_t q = 0; q < B; q++) {
     const float *x = Q + q * d;
-    proj_quant_row(x, d, Vr, R, q8 + q * R, qs + q);
-    double s = 0.0;
-    for (int k = 0; k < d; k++) s += (double)x[k] * (double)c[k];
-    qc[q] = (float)s;
+    quant_row(z + q * R, R, q8 + q * R, qs + q);
+    double lane[64];
+    for (int l = 0; l < 64; l++) lane[l] = 0.0;
+    for (int k = 0; k < d; k++) lane[k % 64] += (double)x[k] * (double)c[k];
+    qc[q] = (float)butterfly64_d(lane);
     for (int k = 0; k < d; k++) qh[q * d + k] = f2h(x[k]);
   }
 }
@@ -67,8 +87,10 @@ void or_build_codes(const uint16_t *X16, const int32_t *order, const int32_t *ce
     float x[8192];
     const uint16_t *xr = X16 + (int64_t)order[n] * d;
     const uint16_t *mr = means16 + (int64_t)cell[n] * d;
+    float z[1024];
     for (int k = 0; k < d; k++) x[k] = h2f(xr[k]) - h2f(mr[k]);
-    proj_quant_row(x, d, Vr, R, Z + n * R, zs + n);
+    project_row(x, d, Vr, R, z);
+    quant_row(z, R, Z + n * R, zs + n);
   }
 }
 
@@ -300,14 +322,16 @@ void or_lut_build(const uint16_t *Zq, int64_t B, int D, int T, const int32_t *ti
       }
     }
     for (int t = 0; t < T; t++) {
-      double s1 = 0.0, s2 = 0.0;
+      double l1[64], l2[64];
+      for (int l = 0; l < 64; l++) l1[l] = l2[l] = 0.0;
       for (int i = tiers[3 * t]; i < tiers[3 * t + 1]; i++) {
         const double x = (double)h2f(zr[i]);
-        s1 += x;
-        s2 += x * x;
+        const int l = (i - tiers[3 * t]) % 64;
+        l1[l] += x;
+        l2[l] += x * x;
       }
-      qsum[(int64_t)t * B + q] = (float)s1;
-      qn2[(int64_t)t * B + q] = (float)s2;
+      qsum[(int64_t)t * B + q] = (float)butterfly64_d(l1);
+      qn2[(int64_t)t * B + q] = (float)butterfly64_d(l2);
     }
   }
 }

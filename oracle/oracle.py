@@ -99,17 +99,28 @@ def recall(I, GT, k=10):
 
 
 # ------------------------------------------------------------------------------------ C stages
-def query_prep(Q, Vr, c):
+def project(Q, Vr):
     Q = _c(Q, np.float32)
     Vr = _c(Vr, np.float32)
-    c = _c(c, np.float32)
     B, d = Q.shape
     R = Vr.shape[1]
+    z = np.empty((B, R), np.float32)
+    lib().or_project(_p(Q), I64(B), I32(d), _p(Vr), I32(R), _p(z))
+    return z
+
+
+def query_prep(Q, Vr, c, z=None):
+    """(q8, qs, qc, qh); z = Q @ Vr is computed here (sequential fp32) unless given."""
+    Q = _c(Q, np.float32)
+    c = _c(c, np.float32)
+    z = project(Q, Vr) if z is None else _c(z, np.float32)
+    B, d = Q.shape
+    R = z.shape[1]
     q8 = np.empty((B, R), np.int8)
     qs = np.empty(B, np.float32)
     qc = np.empty(B, np.float32)
     qh = np.empty((B, d), np.uint16)
-    lib().or_query_prep(_p(Q), I64(B), I32(d), _p(Vr), I32(R), _p(c), _p(q8), _p(qs), _p(qc), _p(qh))
+    lib().or_query_prep(_p(Q), I64(B), I32(d), _p(z), I32(R), _p(c), _p(q8), _p(qs), _p(qc), _p(qh))
     return q8, qs, qc, qh
 
 
@@ -303,14 +314,16 @@ def stage1(idx, q8, qs, QM16, probe, K, knobs, rho_override=None, M_override=Non
                 ncnt=ncnt)
 
 
-def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, fallback=True):
-    """Every intermediate of one batch (EngineI8._gpu + _fallback). QM16 / Zq16 (fp16 as uint16) are the
-    two BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs, otherwise
-    computed here with sequential fp32 accumulation."""
+def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None, fallback=True):
+    """Every intermediate of one batch (EngineI8._gpu + _fallback). zq (f32), QM16 / Zq16 (fp16 as uint16)
+    are the three BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs,
+    otherwise computed here with sequential fp32 accumulation."""
     knobs = dict(knobs or {})
     delta = knobs.get("DELTA", 0.07)
     half = knobs.get("LUTF", True) and knobs.get("LUTH", True)
-    q8, qs, qc, qh = query_prep(Q, idx["Vr"], idx["c"])
+    if zq is None:
+        zq = project(Q, idx["Vr"])
+    q8, qs, qc, qh = query_prep(Q, idx["Vr"], idx["c"], zq)
     D = idx["TS"][-1][1]
     if QM16 is None:
         QM16 = fp16_gemm_nt(qh, idx["meansN"])
@@ -322,7 +335,7 @@ def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, fallback
     est, sd = lut_score(s1["pos"], qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
                         idx["toff"], s1["ncnt"] if delta is not None else None)
     ids, I, scores, reads = refine(est, sd, s1["pos"], idx["order"], idx["H"], Q, z, k)
-    out = dict(q8=q8, qs=qs, qc=qc, qh=qh, QM=QM16, Zq=Zq16, probe=probe, L=L, qsum=qsum, qn2=qn2, est=est, sd=sd,
+    out = dict(z=zq, q8=q8, qs=qs, qc=qc, qh=qh, QM=QM16, Zq=Zq16, probe=probe, L=L, qsum=qsum, qn2=qn2, est=est, sd=sd,
                ids=ids, I=I.copy(), scores=scores.copy(), reads=reads.copy(), cand=ids.copy(), **s1)
     bad = np.nonzero(s1["ok"] == 0)[0]
     out["bad"] = bad

@@ -45,7 +45,7 @@ def traced(env, oracle_mod):
     torch.cuda.synchronize()
     tr = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in tr.items()}
     out = oracle_mod.pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]),
-                              fallback=False)
+                              zq=npy(tr["z"]), fallback=False)
     return tr, out
 
 
@@ -66,8 +66,11 @@ def test_query_code_bit_exact(traced):
 
 
 def test_blas_products_accuracy(env, traced):
-    """QM and Zq: fp16 outputs of fp16 GEMMs, within one fp16 rounding (+ fp32 accumulation) of float64."""
+    """z: fp32 GEMM, within fp32 accumulation error of float64. QM and Zq: fp16 outputs of fp16 GEMMs,
+    within one fp16 rounding (+ fp32 accumulation) of float64."""
     tr, _ = traced
+    z64 = npy(env["Q"]).astype(np.float64) @ npy(env["Vr"]).astype(np.float64)
+    assert np.all(np.abs(npy(tr["z"]) - z64) <= 1e-5 * np.abs(z64).max(1, keepdims=True))
     Qh = npy(tr["Qh"]).astype(np.float64)
     E = env["E"]
     QM64 = Qh @ npy(E.meansN).astype(np.float64).T
@@ -157,7 +160,7 @@ def test_fallback_matches_oracle(env, oracle_mod):
         torch.cuda.synchronize()
         nbad = int((~tr["ok"]).sum())
         out = oracle_mod.pipeline(env["idx"], npy(Qs), K, Z_, NPROBE, KK, knobs=dict(MSZ=K + 8),
-                                  QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]))
+                                  QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]), zq=npy(tr["z"]))
     finally:
         E.MSZ = old
         E.graphs.clear()

@@ -36,6 +36,7 @@ def test_query_code_matches_float64_projection(tiny, oracle_mod):
     Qn, Vr, c = tiny["Qn"], tiny["idx"]["Vr"], tiny["idx"]["c"]
     q8, qs, qc, qh = oracle_mod.query_prep(Qn, Vr, c)
     z64 = Qn.astype(np.float64) @ Vr.astype(np.float64)
+    assert np.allclose(oracle_mod.project(Qn, Vr), z64, atol=1e-5)
     amax = np.abs(z64).max(1)
     assert np.allclose(qs, amax / 127, rtol=1e-5)
     assert np.all(np.abs(q8).max(1) == 127), "the largest coordinate must map to +-127"
