@@ -23,6 +23,8 @@ sys.path.insert(0, ROOT)
 METRIC = "QPS @ recall@10≥0.99, 1M×1536 fp16, batch 2000; % of int8-MFMA/HBM peak"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+CAL_BYTES = 256 << 20  # plain device copy of known size: the HBM counter calibration dispatch
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_i8_scan_emit.throughput_1Mx1536.traffic.md")
 
 
 def log(msg):
@@ -148,20 +150,27 @@ def main():
 
 
 def _time_launch(fn, reps, torch, setup=None):
-    """Average device time of fn() over reps launches, HIP events on the current stream."""
+    """Average device time of one fn() launch: reps launches back to back between two HIP events on the
+    current stream (the stream the libfvs wrappers launch on). When every launch needs a setup kernel
+    (a counter reset), the same number of setup launches is timed alone and subtracted."""
     st = torch.cuda.current_stream()
-    tot = 0.0
-    for _ in range(reps):
-        if setup is not None:
-            setup()
+
+    def run(body):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
         a.record(st)
-        fn()
+        for _ in range(reps):
+            body()
         b.record(st)
         b.synchronize()
-        tot += a.elapsed_time(b)
-    return tot / reps
+        return a.elapsed_time(b)
+
+    if setup is None:
+        return run(fn) / reps
+    both = run(lambda: (setup(), fn()))
+    alone = run(setup)
+    return max(both - alone, 0.0) / reps
 
 
 def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
@@ -187,6 +196,10 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     pre = (tr["L"], tr["qsum"], tr["qn2"])
     ncnt = tr["ncnt"] if E.DELTA is not None else None
     t_lut = _time_launch(lambda: _lib.lut_score(tr["pos"], tr["QC"], pre, E.code, ncnt), reps, torch)
+    cal = torch.ones(CAL_BYTES // 4, dtype=torch.int32, device=Q.device)
+    cal2 = torch.empty_like(cal)
+    t_copy = _time_launch(lambda: cal2.copy_(cal), reps, torch)
+    del cal, cal2
     # algorithmic work
     off = s1["off_t"].long()
     sizes = (off[1:] - off[:-1])
@@ -200,19 +213,49 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     scored = float(tr["ncnt"].clamp(max=K).sum()) if ncnt is not None else float(B * K)
     lut_bytes = scored * E.code["RB"]
     gbs = lambda byt, ms: byt / (ms * 1e-3) / 1e9
-    emit_gbs = gbs(code_bytes_emit, t_emit)
+    tops = lambda ops, ms: ops / (ms * 1e-3) / 1e12
+    emit_gbs, emit_tops = gbs(code_bytes_emit, t_emit), tops(ops_emit, t_emit)
     kernels = {
-        "i8_emit": {"ms": round(t_emit, 4), "bytes": code_bytes_emit, "GBps": round(emit_gbs, 1),
-                    "int8_TOPS": round(ops_emit / (t_emit * 1e-3) / 1e12, 2),
-                    "mfma_frac": round(ops_emit / (t_emit * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)},
-        "i8_first": {"ms": round(t_first, 4), "bytes": code_bytes_first, "GBps": round(gbs(code_bytes_first, t_first), 1),
-                     "int8_TOPS": round(ops_first / (t_first * 1e-3) / 1e12, 2)},
+        "i8_emit": {"ms": round(t_emit, 4), "bytes": code_bytes_emit, "ops": ops_emit, "GBps": round(emit_gbs, 1),
+                    "int8_TOPS": round(emit_tops, 2), "mfma_frac": round(emit_tops / INT8_PEAK_TOPS, 4),
+                    "hbm_frac": round(emit_gbs / HBM_PEAK_GBS, 4),
+                    "emitted_per_query": round(float(tr["cnt"].float().mean()), 1)},
+        "i8_first": {"ms": round(t_first, 4), "bytes": code_bytes_first, "ops": ops_first,
+                     "GBps": round(gbs(code_bytes_first, t_first), 1), "int8_TOPS": round(tops(ops_first, t_first), 2)},
         "lut_score": {"ms": round(t_lut, 4), "bytes": lut_bytes, "GBps": round(gbs(lut_bytes, t_lut), 1),
                       "hbm_frac": round(gbs(lut_bytes, t_lut) / HBM_PEAK_GBS, 4)},
+        "copy_calibration": {"ms": round(t_copy, 4), "bytes": 2.0 * CAL_BYTES,
+                             "GBps": round(gbs(2.0 * CAL_BYTES, t_copy), 1)},
     }
-    roof = {"bound": "hbm", "achieved": round(emit_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(emit_gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_i8_scan<1> (stage-1 emit)"}
+    # the binding roofline of the emit scan: the larger of its MFMA and HBM time floors
+    if ops_emit / (INT8_PEAK_TOPS * 1e12) >= code_bytes_emit / (HBM_PEAK_GBS * 1e9):
+        roof = {"bound": "mfma", "achieved": round(emit_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                "frac": round(emit_tops / INT8_PEAK_TOPS, 4)}
+    else:
+        roof = {"bound": "hbm", "achieved": round(emit_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(emit_gbs / HBM_PEAK_GBS, 4)}
+    roof["traffic"] = measured_traffic(args, nprobe, K)
+    roof["kernel"] = "k_i8_scan<1> (stage-1 threshold-and-emit scan)"
     return {"roofline": roof, "kernels": kernels}
+
+
+def measured_traffic(args, nprobe, K):
+    """HBM bytes per launch of the emit scan from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary,
+    when it was measured on this exact workload; None otherwise."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    vals = {}
+    for line in open(TRAFFIC_FILE):
+        if ":" in line and line.startswith("- "):
+            k, v = line[2:].split(":", 1)
+            vals[k.strip()] = v.strip()
+    want = {"n": args.n, "d": args.d, "batch": args.batch, "nprobe": nprobe, "K": K}
+    try:
+        if all(int(vals[k]) == v for k, v in want.items()):
+            return int(float(vals["traffic_bytes_per_launch"]))
+    except (KeyError, ValueError):
+        pass
+    return None
 
 
 def cpu_baseline(E, Q, K, args, nprobe, np, torch):

@@ -1,0 +1,90 @@
+"""The C ABI without a GPU: libfvs.so loads and exports every function include/fvs.h declares, the
+argument checks reject out-of-range calls before anything is launched, the Python wrappers refuse CPU
+tensors (there is no CPU fallback), and no device code contains packed-fp32 instructions."""
+import ctypes
+import os
+import re
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fvs.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from fanarvse_paper_amd import _lib, build
+
+    if not os.path.exists(_lib.LIB_PATH):
+        build.build()
+    return _lib.lib()
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char \*)\s*\*?\s*(fvs_\w+)\s*\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported(L):
+    from fanarvse_paper_amd import _lib
+
+    names = declared()
+    assert len(names) >= 13, names
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert L.fvs_abi_version() == 1
+    assert L.fvs_error_string(-1) and L.fvs_error_string(-3) and L.fvs_error_string(0)
+
+
+def test_argument_checks_need_no_gpu(L):
+    """Out-of-range sizes return FVS_E_* codes before any HIP call (null pointers stand in for buffers)."""
+    n = None
+    E_ARG, E_SHAPE, E_CAP = -1, -2, -3
+    assert L.fvs_select(n, n, n, 4, 16, 0, 0, 0.0, n, n, n, n, n) == E_ARG             # K = 0
+    assert L.fvs_select(n, n, n, 4, 16, 5000, 0, 0.0, n, n, n, n, n) == E_CAP          # K > 4096
+    assert L.fvs_select(n, n, n, 4, 16, 8, 8, 0.0, n, n, n, n, n) == E_ARG             # kd >= K
+    assert L.fvs_route_topk(n, 4, 100, 0, n, n) == E_ARG
+    assert L.fvs_route_topk(n, 4, 100, 101, n, n) == E_ARG                             # nprobe > NC
+    assert L.fvs_i8_scan(0, 10, *[n] * 12, 100, 128, *[n] * 6, 1, 1, 1, n) == E_SHAPE  # R != 256
+    assert L.fvs_i8_scan(2, 10, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == E_ARG    # bad mode
+    assert L.fvs_refine(*[n] * 6, 4, 10, 64, 1.0, 10, *[n] * 5) == E_ARG               # K <= k
+    assert L.fvs_refine(*[n] * 6, 4, 20, 60, 1.0, 10, *[n] * 5) == E_ARG               # d % 8
+    assert L.fvs_threshold(n, n, 4, n, 4, 5, 2, 3, n, n) == E_ARG                      # n1 > npr
+    assert L.fvs_pairs_scratch_bytes(10, 7) > 0
+    # zero-sized batches are valid no-ops
+    assert L.fvs_select(n, n, n, 0, 16, 8, 0, 0.0, n, n, n, n, n) == 0
+    assert L.fvs_i8_scan(1, 0, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == 0
+
+
+def test_wrappers_refuse_cpu_tensors(L):
+    from fanarvse_paper_amd import _lib
+
+    QM = torch.zeros((4, 16), dtype=torch.float16)
+    with pytest.raises((RuntimeError, ValueError, TypeError)):
+        _lib.route_topk(QM, 4)
+    with pytest.raises((RuntimeError, ValueError, TypeError)):
+        _lib.fill_u32(torch.zeros(8, dtype=torch.int32), 0)
+
+
+def test_no_packed_fp32_in_device_code():
+    """Every kernel source, compiled with the library's own flags, has no v_pk_{add,mul,fma}_f32."""
+    from fanarvse_paper_amd import build
+
+    def asm(src):
+        out = f"/tmp/fvs_abi_{os.getpid()}_{os.path.basename(src)}.s"
+        cmd = [build.HIPCC, *[f for f in build.FLAGS if f != "-fPIC"], "--cuda-device-only", "-S", src, "-o", out]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+        text = open(out).read()
+        os.remove(out)
+        return src, text
+
+    with ThreadPoolExecutor(4) as ex:
+        for src, text in ex.map(asm, build.sources()):
+            bad = re.findall(r"v_pk_(?:add|mul|fma)_f32", text)
+            assert not bad, f"{os.path.basename(src)}: {len(bad)} packed-fp32 instructions"
+            assert "v_mfma" in text or "fvs_scan" not in src

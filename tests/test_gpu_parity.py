@@ -1,9 +1,10 @@
 """GPU parity: every stage of the gfx950 path against the CPU oracle on the same seeded inputs.
 
 Integer and index results must be bit-exact; so must the floating-point stages, because the kernels
-and oracle.c follow one canonical operation order (include/fvs.h). The two fp16 GEMMs (routing scores
-QM and rotated tier queries Zq) come from the GPU's BLAS and are handed to the oracle as shared
-inputs; their own accuracy is checked against float64 (one fp16 rounding plus fp32 accumulation).
+and oracle.c follow one canonical operation order (include/fvs.h). The three dense products (the
+fp32 projection z = Q @ Vr, the fp16 routing scores QM and the fp16 rotated tier queries Zq) come from
+the GPU's BLAS and are handed to the oracle as shared inputs; their own accuracy is checked against
+float64 (one rounding of the output plus fp32 accumulation).
 """
 import numpy as np
 import pytest
