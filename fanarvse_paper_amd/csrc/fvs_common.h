@@ -38,6 +38,19 @@ __device__ __forceinline__ uint32_t fvs_ord16(uint16_t u) {
   return (u & 0x8000u) ? (uint32_t)((~u) & 0xffffu) : (uint32_t)(u | 0x8000u);
 }
 
+// Workgroup barrier that orders LDS only: outstanding global loads stay in flight across it (a
+// plain __syncthreads() also waits for every outstanding global access of the wave).
+__device__ __forceinline__ void fvs_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Number of set bits of a wave mask below this lane.
+__device__ __forceinline__ int fvs_lane_prefix(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 __device__ __forceinline__ float fvs_wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, FVS_WAVE));

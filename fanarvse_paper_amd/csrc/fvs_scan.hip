@@ -3,10 +3,16 @@
 // Work item = (cell, chunk of up to 8 consecutive global 32-row blocks of the cell), one 4-wave
 // workgroup per item. Wave w keeps blocks 2w and 2w+1 of the chunk (64 code rows) as MFMA A operands
 // in registers for the whole item, so each code byte is read from HBM once per pass. The cell's
-// queries stream through as B operands in tiles of 32: a tile (32 x 256 B) is loaded once per item
-// into LDS (row stride 272 B, so the 16-byte fragment reads of 8 consecutive lanes hit distinct
-// banks) and read by all four waves; the next tile's global loads are issued before the current
-// tile's MFMAs and stored to the other LDS buffer after them.
+// queries stream through as B operands in tiles of 32:
+//   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the
+//     row scales of its 256 rows are staged in LDS up front (kMeta pairs at a time), so no global
+//     load in the tile loop depends on another;
+//   * every wave loads the B fragments of its next tile straight into registers (16-byte lane
+//     loads of the query codes, served by L1/L2: the four waves of an item read the same 8 KB) while
+//     it multiplies the current one. The waves of an item never wait for each other inside the tile
+//     loop; they synchronise only when the pair list is staged and when candidates are flushed.
+// Two blocks per wave halve the B-fragment gathers per MFMA (they are the latency the tile loop
+// waits on) at the cost of occupancy 2.
 //
 // Operand layout: lane l holds row/column (l & 31) and, for MFMA step s (k-block of 32 bytes), the
 // 16 bytes at 32*s + 16*(l >> 5); A and B use the same assignment, so the contraction is exact for
@@ -14,95 +20,43 @@
 // 8*(v/4) + 4*(l/32) + (v%4) and column (query) l%32, so each lane owns one query and 16 rows of a
 // block; the epilogue needs only per-lane scalars for the query.
 //
-// Rows of a block outside the cell get a NaN row scale: their estimate is NaN, which never passes
-// `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
+// The item's row scales sit in LDS; rows outside the cell get a NaN scale: their estimate is NaN,
+// which never passes `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
+//
+// Emit: for each accumulator element the wave takes a ballot of `est >= t0`; the passing lanes get
+// consecutive slots of the wave's own LDS region (a wave-uniform counter, no atomics) and the other
+// lanes write to a private dummy slot, so the store needs no divergent branch. If a wave's region
+// overflows, the item's staged candidates are dropped and the item is redone on the direct path
+// (one global atomic per candidate), which is also the path of cells probed by more than kMaxQ
+// queries. At the end of the item one global atomic per (item, query) reserves the query's buffer
+// range and the staged candidates are written out.
 #include "fvs_common.h"
 
 namespace {
 
 constexpr int kR = 256;
-constexpr int kCB = 8;     // 32-row blocks per work item
-constexpr int kRS = 272;   // LDS row stride of a query tile
+constexpr int kNB = 2;       // 32-row blocks per wave
+constexpr int kCB = 4 * kNB; // 32-row blocks per work item
+constexpr int kMeta = 512;   // pairs staged in LDS at a time
+constexpr int kEW = 1024;    // LDS slots per wave: kEW - 64 for candidates, 64 dummy slots
+constexpr int kCap = kEW - 64;
+constexpr int kMaxQ = 2048;  // queries per cell handled by the staged emit
 
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
-// One thread's share of a query tile in flight between global memory and LDS: thread t stages bytes
-// 32*(t&7) .. +32 of the code of query row t>>3, and the threads with (t&7) == 0 its scalars. Loads
-// are branch-free (indices clamped to the cell's last pair) so that the compiler can keep them in
-// flight across the MFMA work of the current tile.
-struct TileStage {
-  v4i lo, hi;
-  int qid, qrank;
-  float qs, qcp, t0;
+struct Meta {  // one (query, cell) pair of the item
+  int qid;     // query
+  float qs;    // query code scale
+  float qcp;   // centre term of the pair
+  float x;     // mode 1: threshold t0 of the query; mode 0: probe rank (int bits)
 };
 
-__device__ __forceinline__ int tile_pair(int tile, int qn, int qoff) {
-  const int jq = tile * 32 + (int)(threadIdx.x >> 3);
-  return qoff + (jq < qn ? jq : qn - 1);
-}
-
-// Issue the loads of one tile; q is qid[tile_pair(...)], loaded one iteration earlier.
-template <int MODE>
-__device__ __forceinline__ void tile_load(TileStage &st, int tile, int qn, int qoff, int q,
-                                          const int8_t *__restrict__ q8, const float *__restrict__ qs,
-                                          const int32_t *__restrict__ qrank, const float *__restrict__ qcp,
-                                          const float *__restrict__ t0) {
-  const int part = threadIdx.x & 7;
-  const int pidx = tile_pair(tile, qn, qoff);
-  const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)q * kR + part * 32);
-  st.lo = src[0];
-  st.hi = src[1];
-  const bool valid = tile * 32 + (int)(threadIdx.x >> 3) < qn;
-  st.qid = valid ? q : -1;
-  st.qs = qs[q];
-  st.qcp = qcp[pidx];
-  if (MODE == 0) {
-    st.qrank = qrank[pidx];
-  } else {
-    st.t0 = valid ? t0[q] : __builtin_inff();
-  }
-}
-
-struct TileLds {
-  int8_t q[2][32 * kRS];
-  int qid[2][32];
-  int qrank[2][32];
-  float qs[2][32], qcp[2][32], t0[2][32];
-};
-
-// Emit staging: candidates that pass are collected in LDS for the whole item; at its end one global
-// atomic per query reserves the query's buffer range, so the atomic round trip is paid once per item
-// instead of once per query tile. Candidates beyond kES (or items of cells probed by more than kMaxQ
-// queries) take the direct path: one global atomic per candidate.
-constexpr int kES = 2048;
-constexpr int kMaxQ = 2048;
 struct EmitLds {
-  float est[kES];
-  int row[kES];
-  uint16_t jq[kES];
-  uint16_t rk[kES];
+  float est[4][kEW];
+  uint32_t tag[4][kEW];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | rank (20-27)
   int qcount[kMaxQ];
-  int qbase[kMaxQ];
-  int n;
+  int n[4];
 };
-
-template <int MODE>
-__device__ __forceinline__ void tile_store(const TileStage &st, TileLds &L, int buf) {
-  const int tid = threadIdx.x;
-  const int row = tid >> 3, part = tid & 7;
-  v4i *dst = reinterpret_cast<v4i *>(&L.q[buf][row * kRS + part * 32]);
-  dst[0] = st.lo;
-  dst[1] = st.hi;
-  if (part == 0) {
-    L.qid[buf][row] = st.qid;
-    L.qs[buf][row] = st.qs;
-    L.qcp[buf][row] = st.qcp;
-    if (MODE == 0)
-      L.qrank[buf][row] = st.qrank;
-    else
-      L.t0[buf][row] = st.t0;
-  }
-}
 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_i8_scan(
@@ -112,7 +66,8 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
     const int32_t *__restrict__ pe, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
     const float *__restrict__ qcp, const float *__restrict__ t0, int32_t *__restrict__ cnt,
     float *__restrict__ bval, int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
-  __shared__ __align__(16) TileLds L;
+  __shared__ __align__(16) Meta meta[kMeta];
+  __shared__ __align__(16) float zsl[32 * kCB];
   const int p = blockIdx.x;
   const int c = pcell[p];
   const int qn = ccnt[c];
@@ -121,145 +76,196 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
   if constexpr (MODE == 1) {
     __shared__ EmitLds Es;
     E = &Es;
-    if (threadIdx.x == 0) Es.n = 0;
   }
   const bool staged = MODE == 1 && qn <= kMaxQ;
   const int qoff = coff[c];
   const int blk0 = pblk[p];
   const int cs = ps[p], ce = pe[p];
   const int lastblk = (ce - 1) / 32;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
   const int h = lane >> 5, li = lane & 31;
+  const int row0 = blk0 * 32;  // first row of the item
 
-  // this wave's two blocks: A operands and row scales
-  int bk[2];
-  bool act[2];
-  v4i a[2][8];
-  float zsv[2][16];
+  // the first chunk's pair ids are requested before the code block, so both latencies overlap
+  int pq[kMeta / 256];
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
-    bk[u] = blk0 + 2 * w + u;
-    act[u] = bk[u] <= lastblk && 2 * w + u < kCB;
+  for (int i = 0; i < kMeta / 256; i++) {
+    const int j = tid + 256 * i;
+    pq[i] = j < min(kMeta, qn) ? qid[qoff + j] : 0;
+  }
+  if (tid < 32 * kCB) {
+    const int r = row0 + tid;
+    zsl[tid] = (r >= cs && r < ce) ? zs[r] : __builtin_nanf("");
+  }
+  // this wave's blocks: the A operands
+  int bk[kNB];
+  bool act[kNB];
+  v4i a[kNB][8];
+#pragma unroll
+  for (int u = 0; u < kNB; u++) {
+    bk[u] = blk0 + kNB * w + u;
+    act[u] = bk[u] <= lastblk;
     int64_t zr = (int64_t)bk[u] * 32 + li;
     if (!act[u] || zr > N - 1) zr = N - 1;
     const v4i *zp = reinterpret_cast<const v4i *>(Z + zr * kR + h * 16);
 #pragma unroll
     for (int s = 0; s < 8; s++) a[u][s] = zp[2 * s];
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int64_t r = (int64_t)bk[u] * 32 + acc_row(v, h);
-      zsv[u][v] = (act[u] && r >= cs && r < ce) ? zs[r] : __builtin_nanf("");
-    }
   }
-  const bool any = act[0] || act[1];
+  const bool any = act[0];
+  int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
 
-  // three-stage pipeline over query tiles: while tile t is multiplied, the codes of tile t+1 are in
-  // flight to registers and the query ids of tile t+2 are being fetched
-  const int ntiles = (qn + 31) / 32;
-  TileStage st;
-  int qnext = qid[tile_pair(0, qn, qoff)];
-  tile_load<MODE>(st, 0, qn, qoff, qnext, q8, qs, qrank, qcp, t0);
-  qnext = qid[tile_pair(1, qn, qoff)];
-  tile_store<MODE>(st, L, 0);
-  __syncthreads();
-  int buf = 0;
-  for (int t = 0; t < ntiles; t++) {
-    const bool more = t + 1 < ntiles;
-    tile_load<MODE>(st, t + 1, qn, qoff, qnext, q8, qs, qrank, qcp, t0);
-    qnext = qid[tile_pair(t + 2, qn, qoff)];
-    if (any) {
-      v4i b[8];
-      const int8_t *qrow = &L.q[buf][li * kRS + h * 16];
+  auto scan = [&](const bool direct, bool first) {
+    for (int c0 = 0; c0 < qn; c0 += kMeta) {
+      const int nq = min(kMeta, qn - c0);
+      if (c0 > 0 || !first) {
 #pragma unroll
-      for (int s = 0; s < 8; s++) b[s] = *reinterpret_cast<const v4i *>(qrow + 32 * s);
-      v16i acc[2];
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        if (act[u]) {
-#pragma unroll
-          for (int s = 0; s < 8; s++) acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
+        for (int i = 0; i < kMeta / 256; i++) {
+          const int j = tid + 256 * i;
+          pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
         }
       }
-      const int q = L.qid[buf][li];
-      const float qsj = L.qs[buf][li];
-      const float qcj = L.qcp[buf][li];
-      if (MODE == 0) {
-        const int rk = L.qrank[buf][li];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-          if (!act[u]) continue;
-          float m = -1e30f;
-#pragma unroll
-          for (int v = 0; v < 16; v++) m = fmaxf(m, __builtin_fmaf((float)acc[u][v] * qsj, zsv[u][v], qcj));
-          m = fmaxf(m, __shfl_xor(m, 32, FVS_WAVE));
-          if (h == 0 && q >= 0) bm[((int64_t)q * n1 + rk) * MB + (bk[u] - cs / 32)] = m;
+      for (int i = 0; i < kMeta / 256; i++) {
+        const int j = tid + 256 * i;
+        if (j < nq) {
+          const int pidx = qoff + c0 + j;
+          const int q = pq[i];
+          Meta m;
+          m.qid = q;
+          m.qs = qs[q];
+          m.qcp = qcp[pidx];
+          m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
+          meta[j] = m;
         }
-      } else {
-        const float th = L.t0[buf][li];
-        float e[2][16];
-        int nk = 0;
+      }
+      __syncthreads();
+
+      if (any) {
+        const int ntiles = (nq + 31) / 32;
+        // B fragments of a tile: lane (li, h) reads bytes 32*s + 16*h of the code of the tile's query li
+        auto load = [&](v4i (&b)[8], int tile) {
+          const int jr = min(tile * 32 + li, nq - 1);
+          const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)meta[jr].qid * kR + h * 16);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+          for (int s = 0; s < 8; s++) b[s] = src[2 * s];
+        };
+        auto compute = [&](const v4i (&b)[8], int t) {
+          v16i acc[kNB];
 #pragma unroll
-          for (int v = 0; v < 16; v++) {
-            e[u][v] = __builtin_fmaf((float)acc[u][v] * qsj, zsv[u][v], qcj);
-            nk += (e[u][v] >= th) ? 1 : 0;
+          for (int u = 0; u < kNB; u++) {
+            acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            if (act[u]) {
+#pragma unroll
+              for (int s = 0; s < 8; s++) acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
+            }
           }
-        }
-        if (nk) {
-          int sp = staged ? atomicAdd(&E->n, nk) : kES;  // LDS slot range of this lane's candidates
-          const uint16_t jq = (uint16_t)(t * 32 + li);
+          const int jl = t * 32 + li;  // pair index inside the chunk
+          const bool valid = jl < nq;
+          const Meta m = meta[valid ? jl : nq - 1];
+          const float th = MODE == 1 && valid ? m.x : __builtin_inff();
+          const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
 #pragma unroll
-          for (int u = 0; u < 2; u++) {
+          for (int u = 0; u < kNB; u++) {
+            if (MODE == 0 && !act[u]) continue;
+            // estimates of the block's 16 elements; the row scales are read from LDS up front
+            float ev[16];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-              if (e[u][v] >= th) {
-                const int row = bk[u] * 32 + acc_row(v, h);
-                if (sp < kES) {
-                  E->est[sp] = e[u][v];
-                  E->row[sp] = row;
-                  E->jq[sp] = jq;
-                } else {  // direct path
-                  const int idx = atomicAdd(&cnt[q], 1);
+            for (int g = 0; g < 4; g++) {
+              const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
+              const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+              for (int i = 0; i < 4; i++) ev[4 * g + i] = __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp);
+            }
+            if (MODE == 0) {
+              float mx = -1e30f;
+#pragma unroll
+              for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
+              mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
+              if (h == 0 && valid) bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + (bk[u] - cs / 32)] = mx;
+            } else if (!direct) {
+              float *est = E->est[w];
+              uint32_t *tag = E->tag[w];
+#pragma unroll
+              for (int v = 0; v < 16; v++) {
+                const bool pass = ev[v] >= th;
+                const uint64_t bal = __ballot(pass);
+                if (bal) {
+                  const int slot = pass ? min(ebase + fvs_lane_prefix(bal), kCap - 1) : kCap + lane;
+                  est[slot] = ev[v];
+                  tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
+                  ebase += __popcll(bal);
+                }
+              }
+            } else {  // direct path
+#pragma unroll
+              for (int v = 0; v < 16; v++) {
+                if (ev[v] >= th) {
+                  const int idx = atomicAdd(&cnt[m.qid], 1);
                   if (idx < CAP) {
-                    bval[(int64_t)q * CAP + idx] = e[u][v];
-                    bpos[(int64_t)q * CAP + idx] = row;
+                    bval[(int64_t)m.qid * CAP + idx] = ev[v];
+                    bpos[(int64_t)m.qid * CAP + idx] = bk[u] * 32 + acc_row(v, h);
                   }
                 }
-                sp++;
               }
             }
           }
+        };
+        v4i b0[8], b1[8];
+        load(b0, 0);
+        for (int t = 0; t < ntiles; t += 2) {
+          load(b1, min(t + 1, ntiles - 1));
+          compute(b0, t);
+          if (t + 1 >= ntiles) break;
+          load(b0, min(t + 2, ntiles - 1));
+          compute(b1, t + 1);
         }
       }
+      __syncthreads();
     }
-    if (more) tile_store<MODE>(st, L, buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-  }
+  };
 
-  if constexpr (MODE == 1) {
-    // flush the staged candidates: rank within the query, one global reservation per query, write out
+  if constexpr (MODE == 0) {
+    scan(true, true);
+  } else {
+    scan(!staged, true);
     if (!staged) return;
-    const int n = min(E->n, kES);
-    if (n == 0) return;
-    for (int j = threadIdx.x; j < qn; j += 256) E->qcount[j] = 0;
+    // a wave whose region overflowed: drop the staged candidates and redo the item on the direct path
+    if (lane == 0) E->n[w] = ebase;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) E->rk[i] = (uint16_t)atomicAdd(&E->qcount[E->jq[i]], 1);
+    if (E->n[0] > kCap || E->n[1] > kCap || E->n[2] > kCap || E->n[3] > kCap) {
+      __syncthreads();
+      scan(true, false);
+      return;
+    }
+    // flush the staged candidates: rank within the query, one global reservation per query, write out
+    for (int j = tid; j < qn; j += 256) E->qcount[j] = 0;
     __syncthreads();
-    for (int j = threadIdx.x; j < qn; j += 256) {
-      const int m = E->qcount[j];
-      if (m) E->qbase[j] = atomicAdd(&cnt[qid[qoff + j]], m);
+    for (int i = tid; i < 4 * kCap; i += 256) {
+      const int ww = i / kCap, k = i - ww * kCap;
+      if (k < E->n[ww]) {
+        const uint32_t tg = E->tag[ww][k];
+        const int r = atomicAdd(&E->qcount[(tg >> 8) & 0xfffu], 1);  // < 256: a query has <= 256 rows here
+        E->tag[ww][k] = tg | ((uint32_t)r << 20);
+      }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) {
-      const int j = E->jq[i];
-      const int idx = E->qbase[j] + E->rk[i];
-      if (idx < CAP) {
-        const int64_t q = qid[qoff + j];
-        bval[q * CAP + idx] = E->est[i];
-        bpos[q * CAP + idx] = E->row[i];
+    for (int j = tid; j < qn; j += 256) {
+      const int m = E->qcount[j];
+      if (m) E->qcount[j] = atomicAdd(&cnt[qid[qoff + j]], m);  // now the query's base in its buffer
+    }
+    __syncthreads();
+    for (int i = tid; i < 4 * kCap; i += 256) {
+      const int ww = i / kCap, k = i - ww * kCap;
+      if (k < E->n[ww]) {
+        const uint32_t tg = E->tag[ww][k];
+        const int j = (tg >> 8) & 0xfffu;
+        const int idx = E->qcount[j] + (int)(tg >> 20);
+        if (idx < CAP) {
+          const int64_t q = qid[qoff + j];
+          bval[q * CAP + idx] = E->est[ww][k];
+          bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
+        }
       }
     }
   }
