@@ -35,6 +35,10 @@ SIGNATURES = {
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
     "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
+    "fvs_trellis_encode": [P, P, I64, I32, P, I32, P, I32, P, P, P],
+    "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I32, P, P, I32, I32, P, P, P, P, P, P, I32, I32, I32, P],
+    "fvs_route_topk_scaled": [P, P, I64, I32, I32, P, P],
+    "fvs_tiered_score": [P, P, P, I32, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
 }
 
 _lib = None
@@ -282,3 +286,65 @@ def refine(est, sd, pos, order, H, Q, z, k):
                             _dev(scores, torch.float32, "scores"), _dev(reads, torch.int32, "reads"), _stream()),
            "fvs_refine")
     return ids, I, scores, reads
+
+
+# ------------------------------------------------------------------------------ trellis engine
+def trellis_encode(Zs, nz, tab, L, words, scale1, paths=None):
+    """Viterbi paths of normalised rows Zs [n, R] (f32) through the 2^L-state trellis with table tab, packed
+    into words [n, W] (int32 bit patterns) and scale1 [n] fp16 (src/viterbi_fused.py, engine_cell.py:16-22)."""
+    n, R = Zs.shape
+    W = words.shape[1]
+    _check(lib().fvs_trellis_encode(_dev(Zs, torch.float32, "Zs"), _dev(nz, torch.float32, "nz", (n,)), n, R,
+                                    _dev(tab, torch.float32, "tab", (2 ** L,)), L, _dev(words, torch.int32, "words", (n, W)),
+                                    W, _dev(scale1, torch.float16, "scale1", (n,)),
+                                    _opt(paths, torch.int32, "paths", (n, R)), _stream()), "fvs_trellis_encode")
+
+
+def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1,
+            MB=1, n1=1):
+    """Trellis stage-1 first pass (mode 0) or emit (mode 1) over the static (cell, block) items
+    (src/s1cell.py:121-154 semantics with the canonical fp32 dot of include/fvs.h)."""
+    pcell, pblk, ps, pe = blocks
+    qid, qrank, coff, ccnt, qcp = pr
+    P_ = pcell.shape[0]
+    B, R = Qr.shape
+    N, W = words.shape
+    if mode == 0 and (bm is None or bm.numel() != B * n1 * MB):
+        raise ValueError("tr_scan: bm must hold B*n1*MB values")
+    if mode == 1 and (bval is None or bval.shape != (B, CAP) or bpos.shape != (B, CAP) or cnt.shape != (B,)):
+        raise ValueError("tr_scan: emit buffers must be [B, CAP]")
+    f32, i32 = torch.float32, torch.int32
+    _check(lib().fvs_tr_scan(mode, P_, _dev(Qr, f32, "Qr"), _dev(qid, i32, "qid"), _dev(qrank, i32, "qrank"),
+                             _dev(coff, i32, "coff"), _dev(ccnt, i32, "ccnt"), _dev(pcell, i32, "pcell"),
+                             _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"), _dev(pe, i32, "pe"), _dev(words, i32, "words"),
+                             W, _dev(scale1, torch.float16, "scale1", (N,)), _dev(tab, f32, "tab", (2 ** L,)), L, R,
+                             _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"),
+                             _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1, _stream()), "fvs_tr_scan")
+
+
+def route_topk_scaled(QM, scale, nprobe):
+    """Top-n_p cells by the fp32 key (float)QM * scale (src/engine_cell.py:40-42)."""
+    B, NC = QM.shape
+    probe = _empty((B, nprobe), torch.int32, QM.device)
+    _check(lib().fvs_route_topk_scaled(_dev(QM, torch.float16, "QM"), _dev(scale, torch.float32, "scale", (NC,)), B,
+                                       NC, nprobe, _dev(probe, torch.int32, "probe"), _stream()), "fvs_route_topk_scaled")
+    return probe
+
+
+def tiered_score(pos, qc, Zq, code, ncnt=None):
+    """(est, sd) [B, K] of the Lloyd-Max tiered code (src/tiered_fused.py:47-72) from the packed records."""
+    B, K = pos.shape
+    D = Zq.shape[1]
+    TS = code["TS"]
+    T = len(TS)
+    rec = code["rec"]
+    N, RB = rec.shape
+    toff = (ctypes.c_int32 * T)(*[int(x) for x in code["toff"]])
+    est = _empty((B, K), torch.float32, pos.device)
+    sd = _empty((B, K), torch.float32, pos.device)
+    _check(lib().fvs_tiered_score(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
+                                  _dev(Zq, torch.float32, "Zq", (B, D)), D, _dev(rec, torch.uint8, "rec"), N, RB,
+                                  int(code["soff"]), T, _tiers_arr(TS), toff, _dev(code["cb"], torch.float32, "cb", (T, 256)),
+                                  _opt(ncnt, torch.int32, "ncnt", (B,)), B, K, _dev(est, torch.float32, "est"),
+                                  _dev(sd, torch.float32, "sd"), _stream()), "fvs_tiered_score")
+    return est, sd

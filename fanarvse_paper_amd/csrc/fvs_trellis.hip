@@ -1,0 +1,394 @@
+// The trellis cell-residual engine of the latency mode: bitshift-trellis encoder (Viterbi), stage-1
+// scan over the decoded codes, routing on fp32 keys, and the Lloyd-Max tiered stage 2.
+//
+// Trellis code (L-bit states, one bit per coordinate): a vector's bit stream is the L bits of its
+// first state (MSB first) followed by the newest bit of every later state; state_j is the window
+// bits[j .. j+L) read MSB first and the decoded coordinate j is tab[state_j]. The stream is stored
+// as W = ceil((R + L - 1) / 32) 32-bit words, first bit in the most significant position.
+#include "fvs_common.h"
+
+namespace {
+
+constexpr int kTrR = 256;      // coordinates per trellis code
+constexpr int kMaxL = 12;      // largest state width the encoder's LDS holds (4096 states)
+constexpr int kMaxT = FVS_MAX_TIERS;
+
+// ------------------------------------------------------------------------------------ encoder
+// One workgroup (256 threads) per vector. Path costs ping-pong in LDS; backpointers are one bit per
+// state per step (ballots), all in LDS; the backtrack, the words and the scale follow in the same
+// workgroup. Canonical arithmetic (shared with the CPU checker):
+//   cost_0(s) = d*d, d = x_0 - tab[s];  cost_j(s) = min(cost(p0), cost(p1)) + d*d, d = x_j - tab[s],
+//   with p0 = s >> 1, p1 = p0 | 2^(L-1), taking p1 only when cost(p1) < cost(p0) (strictly);
+//   the final state is the smallest index of minimum cost.
+template <int S>
+__global__ __launch_bounds__(256) void k_trellis_encode(const float *__restrict__ Zs, const float *__restrict__ nz,
+                                                        int L, const float *__restrict__ tab, int W,
+                                                        uint32_t *__restrict__ words, uint16_t *__restrict__ scale1,
+                                                        int32_t *__restrict__ paths) {
+  __shared__ float x[kTrR];
+  __shared__ float vals[S];
+  __shared__ float cost[2][S];
+  __shared__ uint32_t back[kTrR - 1][S / 32];
+  __shared__ int path[kTrR];
+  __shared__ unsigned long long best;
+  const int64_t v = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < S; i += 256) vals[i] = tab[i];
+  x[tid] = Zs[v * kTrR + tid];
+  if (tid == 0) best = ~0ull;
+  __syncthreads();
+  constexpr int PER = S / 256;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int s = tid + 256 * i;
+    const float d = x[0] - vals[s];
+    cost[0][s] = d * d;
+  }
+  __syncthreads();
+  const int half = S >> 1;
+  for (int j = 1; j < kTrR; j++) {
+    const float *cp = cost[(j - 1) & 1];
+    float *cn = cost[j & 1];
+    const float xj = x[j];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int s = tid + 256 * i;
+      const int p0 = s >> 1, p1 = p0 | half;
+      const float c0 = cp[p0], c1 = cp[p1];
+      const bool take1 = c1 < c0;
+      const float d = xj - vals[s];
+      cn[s] = (take1 ? c1 : c0) + d * d;
+      const uint64_t bal = __ballot(take1);
+      if (lane == 0) {
+        back[j - 1][(256 * i + 64 * w) >> 5] = (uint32_t)bal;
+        back[j - 1][((256 * i + 64 * w) >> 5) + 1] = (uint32_t)(bal >> 32);
+      }
+    }
+    __syncthreads();
+  }
+  // smallest index of minimum cost (costs are non-negative: their bit patterns order like the values)
+  const float *cf = cost[(kTrR - 1) & 1];
+  unsigned long long mine = ~0ull;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int s = tid + 256 * i;
+    const unsigned long long k = ((unsigned long long)__float_as_uint(cf[s]) << 32) | (unsigned)s;
+    mine = k < mine ? k : mine;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long t = __shfl_xor(mine, o, FVS_WAVE);
+    mine = t < mine ? t : mine;
+  }
+  if (lane == 0) atomicMin(&best, mine);
+  __syncthreads();
+  if (tid == 0) {
+    int st = (int)(best & 0xffffffffu);
+    path[kTrR - 1] = st;
+    for (int j = kTrR - 1; j > 0; j--) {
+      const int u = (int)((back[j - 1][st >> 5] >> (st & 31)) & 1u);
+      st = (st >> 1) | (u << (L - 1));
+      path[j - 1] = st;
+    }
+  }
+  __syncthreads();
+  if (paths) paths[v * kTrR + tid] = path[tid];
+  // words: bit b of the stream is (b < L) ? bit L-1-b of path[0] : lowest bit of path[b - L + 1]
+  if (tid < W) {
+    uint32_t word = 0;
+    for (int t = 0; t < 32; t++) {
+      const int b = 32 * tid + t;
+      uint32_t bit = 0;
+      if (b < L)
+        bit = ((uint32_t)path[0] >> (L - 1 - b)) & 1u;
+      else if (b < kTrR + L - 1)
+        bit = (uint32_t)path[b - L + 1] & 1u;
+      word |= bit << (31 - t);
+    }
+    words[v * W + tid] = word;
+  }
+  // scale = |z| / (<Zs, Y> / (|Y| sqrt(R)) * |Y|), Y = tab[path]; sums in double, lane = j % 64
+  if (w == 0) {
+    double yy = 0.0, zy = 0.0;
+    for (int j = lane; j < kTrR; j += 64) {
+      const double y = (double)vals[path[j]];
+      yy += y * y;
+      zy += (double)x[j] * y;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      yy += __shfl_xor(yy, o, FVS_WAVE);
+      zy += __shfl_xor(zy, o, FVS_WAVE);
+    }
+    if (lane == 0) {
+      const float yn = sqrtf((float)yy);
+      const float fip = (float)zy / (yn * sqrtf((float)kTrR));
+      scale1[v] = fvs_f2h(nz[v] / (fip * yn));
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------ stage 1
+// One wave per static (cell, 32-row block) item, four items per workgroup. Lane l decodes row l % 32,
+// coordinates [128 h, 128 h + 128) with h = l / 32, into registers; for each query of the cell it
+// forms the half dot product as a sequential fmaf chain and adds the two halves:
+//   est = fmaf(scale1, lo + hi, qcp),  lo / hi = sum over j < 128 / j >= 128 of tab[state_j] * Qr[j].
+// mode 0: bm[(q*n1 + qrank)*MB + blk - cs/32] = max over the block's rows in the cell.
+// mode 1: every (q, row) with est >= t0[q] is appended to the query's buffer (one atomic each).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, const int32_t *__restrict__ qid,
+                                                 const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff,
+                                                 const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
+                                                 const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
+                                                 const int32_t *__restrict__ pe, int P, const uint32_t *__restrict__ words,
+                                                 int W, const uint16_t *__restrict__ scale1, const float *__restrict__ tab,
+                                                 int L, const float *__restrict__ qcp, const float *__restrict__ t0,
+                                                 int32_t *__restrict__ cnt, float *__restrict__ bval,
+                                                 int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
+  __shared__ float stab[1 << kMaxL];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int S = 1 << L;
+  for (int i = tid; i < S; i += 256) stab[i] = tab[i];
+  __syncthreads();
+  const int p = blockIdx.x * 4 + w;
+  if (p >= P) return;
+  const int c = pcell[p];
+  const int qn = ccnt[c];
+  if (qn == 0) return;
+  const int qoff = coff[c];
+  const int blk = pblk[p], cs = ps[p], ce = pe[p];
+  const int h = lane >> 5, li = lane & 31;
+  const int r = blk * 32 + li;
+  const bool valid = r >= cs && r < ce;
+  const int rr = valid ? r : cs;  // decode a valid row for padding lanes (their results are dropped)
+  // coordinates [128 h, 128 h + 128) need words 4h .. 4h + 4 of the stream
+  uint32_t ww[5];
+#pragma unroll
+  for (int k = 0; k < 5; k++) {
+    const int i = 4 * h + k;
+    ww[k] = i < W ? words[(int64_t)rr * W + i] : 0u;
+  }
+  float v[128];
+  const uint32_t mask = (uint32_t)S - 1u;
+#pragma unroll
+  for (int i = 0; i < 128; i++) {
+    const uint64_t comb = ((uint64_t)ww[i >> 5] << 32) | (uint64_t)ww[(i >> 5) + 1];
+    v[i] = stab[(uint32_t)(comb >> (64 - L - (i & 31))) & mask];
+  }
+  const float s1 = fvs_h2f(scale1[rr]);
+  for (int i = 0; i < qn; i++) {
+    const int pidx = qoff + i;
+    const int q = qid[pidx];
+    const float4 *qv = reinterpret_cast<const float4 *>(Qr + (int64_t)q * kTrR + 128 * h);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < 32; g++) {
+      const float4 x4 = qv[g];
+      acc = __builtin_fmaf(v[4 * g + 0], x4.x, acc);
+      acc = __builtin_fmaf(v[4 * g + 1], x4.y, acc);
+      acc = __builtin_fmaf(v[4 * g + 2], x4.z, acc);
+      acc = __builtin_fmaf(v[4 * g + 3], x4.w, acc);
+    }
+    const float other = __shfl_xor(acc, 32, FVS_WAVE);
+    const float est = __builtin_fmaf(s1, acc + other, qcp[pidx]);
+    if (MODE == 0) {
+      float m = valid ? est : -__builtin_inff();
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, FVS_WAVE));
+      if (lane == 0) bm[((int64_t)q * n1 + qrank[pidx]) * MB + (blk - cs / 32)] = m;
+    } else {
+      if (h == 0 && valid && est >= t0[q]) {
+        const int idx = atomicAdd(&cnt[q], 1);
+        if (idx < CAP) {
+          bval[(int64_t)q * CAP + idx] = est;
+          bpos[(int64_t)q * CAP + idx] = r;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------ routing
+// Top-n_p cells by the fp32 key (float)QM[q][c] * scale[c], sorted by (key descending, cell ascending).
+__global__ __launch_bounds__(256) void k_route_f32(const uint16_t *__restrict__ QM, const float *__restrict__ scale,
+                                                   int NC, int np, int32_t *__restrict__ probe) {
+  extern __shared__ uint64_t rk[];  // [NC] keys, then [pow2(np)] the sorted top
+  __shared__ int hist[256];
+  __shared__ int sh[8];
+  __shared__ int gcnt;
+  const int64_t q = blockIdx.x;
+  uint64_t *top = rk + NC;
+  for (int i = threadIdx.x; i < NC; i += 256) {
+    const float key = fvs_h2f(QM[q * NC + i]) * scale[i];
+    rk[i] = ((uint64_t)fvs_ord32(key) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  }
+  __syncthreads();
+  fvs_block_topk_u64([&](int i) { return rk[i]; }, NC, np, top, hist, sh, &gcnt);
+  for (int i = threadIdx.x; i < np; i += 256) probe[q * np + i] = (int32_t)(0xffffffffu - (uint32_t)(top[i] & 0xffffffffu));
+}
+
+// ------------------------------------------------------------------------------------ stage 2
+struct LmTiers {
+  int T;
+  int start[kMaxT], width[kMaxT], bits[kMaxT], toff[kMaxT];
+};
+
+// One workgroup per query, one wave per candidate at a time. Canonical arithmetic:
+//   a_t = (xor butterfly over 64 lanes of) the lane sums, lane l summing fmaf(cb_t[code_k], Zq[s_t + k], .)
+//   over the tier's coordinates k = l, l + 64, ... in order;
+//   est = fmaf(a_t, scale_t, est) and var = fmaf(qn2_t * sig_t, sig_t, var) for t = 0..T-1 from
+//   est = qc[q], var = 0; sd = sqrtf(var). qn2_t = (float) of the double sum of Zq^2 over the tier
+//   (lane = offset in the tier % 64, then the butterfly).
+__global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict__ pos, const float *__restrict__ qc,
+                                                      const float *__restrict__ Zq, int D, const uint8_t *__restrict__ rec,
+                                                      int RB, int soff, LmTiers tiers, const float *__restrict__ cb,
+                                                      const int32_t *__restrict__ ncnt, int K, float *__restrict__ est,
+                                                      float *__restrict__ sd) {
+  extern __shared__ __align__(16) uint8_t dyn[];
+  float *zq = reinterpret_cast<float *>(dyn);                  // [D]
+  float *cbs = zq + D;                                         // [T][256]
+  uint8_t *recs = reinterpret_cast<uint8_t *>(cbs + 256 * tiers.T);  // [4][RB]
+  __shared__ float qn2[kMaxT];
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < D; i += 256) zq[i] = Zq[q * D + i];
+  for (int i = tid; i < 256 * tiers.T; i += 256) cbs[i] = cb[i];
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int t = 0; t < kMaxT; t++) {
+      if (t >= tiers.T) break;
+      double a = 0.0;
+      for (int k = lane; k < tiers.width[t]; k += 64) {
+        const double z = (double)zq[tiers.start[t] + k];
+        a += z * z;
+      }
+      for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, FVS_WAVE);
+      if (lane == 0) qn2[t] = (float)a;
+    }
+  }
+  __syncthreads();
+  const int nc = ncnt ? min(ncnt[q], K) : K;
+  uint8_t *rw = recs + w * RB;
+  for (int m = w; m < K; m += 4) {
+    if (m >= nc) {
+      if (lane == 0) {
+        est[q * K + m] = -1e30f;
+        sd[q * K + m] = 0.f;
+      }
+      continue;
+    }
+    const int64_t row = pos[q * K + m];
+    const uint4 *src = reinterpret_cast<const uint4 *>(rec + row * RB);
+    for (int i = lane; i < RB / 16; i += 64) reinterpret_cast<uint4 *>(rw)[i] = src[i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    float e = qc[q], var = 0.f;
+#pragma unroll
+    for (int t = 0; t < kMaxT; t++) {
+      if (t >= tiers.T) break;
+      const int d = tiers.width[t], b = tiers.bits[t], kb = d >> 3;
+      const uint8_t *pl = rw + tiers.toff[t];
+      const float *cbt = cbs + 256 * t;
+      const float *zt = zq + tiers.start[t];
+      float acc = 0.f;
+      for (int k = lane; k < d; k += 64) {
+        int code = 0;
+        for (int pp = 0; pp < b; pp++) code |= (((int)pl[pp * kb + (k >> 3)] >> (7 - (k & 7))) & 1) << (b - 1 - pp);
+        acc = __builtin_fmaf(cbt[code], zt[k], acc);
+      }
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, FVS_WAVE);
+      const uint16_t *ss = reinterpret_cast<const uint16_t *>(rw + soff + 4 * t);
+      const float sc = fvs_h2f(ss[0]), sg = fvs_h2f(ss[1]);
+      e = __builtin_fmaf(acc, sc, e);
+      var = __builtin_fmaf(qn2[t] * sg, sg, var);
+    }
+    if (lane == 0) {
+      est[q * K + m] = e;
+      sd[q * K + m] = sqrtf(var);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+}
+
+}  // namespace
+
+extern "C" int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, const float *tab, int32_t L,
+                                  uint32_t *words, int32_t W, uint16_t *scale1, int32_t *paths, void *stream) {
+  if (R != kTrR) return FVS_E_SHAPE;
+  if (L < 8 || L > kMaxL || n < 0) return FVS_E_ARG;
+  if (W != (R + L - 1 + 31) / 32) return FVS_E_ARG;
+  if (n == 0) return FVS_OK;
+  if (!Zs || !nz || !tab || !words || !scale1) return FVS_E_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (L == 8)
+    hipLaunchKernelGGL(k_trellis_encode<256>, dim3((unsigned)n), dim3(256), 0, st, Zs, nz, L, tab, W, words, scale1, paths);
+  else if (L == 9)
+    hipLaunchKernelGGL(k_trellis_encode<512>, dim3((unsigned)n), dim3(256), 0, st, Zs, nz, L, tab, W, words, scale1, paths);
+  else if (L == 10)
+    hipLaunchKernelGGL(k_trellis_encode<1024>, dim3((unsigned)n), dim3(256), 0, st, Zs, nz, L, tab, W, words, scale1, paths);
+  else
+    return FVS_E_SHAPE;  // 11 and 12 exceed the encoder's LDS budget
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
+                           const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk,
+                           const int32_t *ps, const int32_t *pe, const uint32_t *words, int32_t W, const uint16_t *scale1,
+                           const float *tab, int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt,
+                           float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream) {
+  if (R != kTrR) return FVS_E_SHAPE;
+  if (mode != 0 && mode != 1) return FVS_E_ARG;
+  if (L < 2 || L > kMaxL || W != (R + L - 1 + 31) / 32 || W > 10 || P < 0) return FVS_E_ARG;
+  if (P == 0) return FVS_OK;
+  if (!Qr || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !words || !scale1 || !tab || !qcp)
+    return FVS_E_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)((P + 3) / 4));
+  if (mode == 0) {
+    if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
+    hipLaunchKernelGGL(k_tr_scan<0>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
+                       W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+  } else {
+    if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
+    hipLaunchKernelGGL(k_tr_scan<1>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
+                       W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+  }
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int32_t NC, int32_t nprobe,
+                                     int32_t *probe, void *stream) {
+  if (B < 0 || NC <= 0 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
+  if (NC > 8192 || nprobe > 4096) return FVS_E_CAPACITY;
+  if (B == 0) return FVS_OK;
+  if (!QM || !scale || !probe) return FVS_E_ARG;
+  const size_t shm = 8 * ((size_t)NC + (size_t)fvs_pow2_ceil(nprobe));
+  hipLaunchKernelGGL(k_route_f32, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, QM, scale, NC, nprobe, probe);
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_tiered_score(const int32_t *pos, const float *qc, const float *Zq, int32_t D, const uint8_t *rec,
+                                int64_t N, int32_t RB, int32_t soff, int32_t T, const int32_t *tiers, const int32_t *toff,
+                                const float *cb, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
+                                void *stream) {
+  if (B < 0 || K <= 0 || D <= 0 || N <= 0 || RB <= 0 || RB % 16 != 0) return FVS_E_ARG;
+  if (T <= 0 || T > kMaxT) return FVS_E_SHAPE;
+  if (B == 0) return FVS_OK;
+  if (!pos || !qc || !Zq || !rec || !tiers || !toff || !cb || !est || !sd) return FVS_E_ARG;
+  LmTiers ta{};
+  ta.T = T;
+  for (int t = 0; t < T; t++) {
+    const int s = tiers[3 * t], e = tiers[3 * t + 1], b = tiers[3 * t + 2];
+    if (s < 0 || e > D || e <= s || (e - s) % 8 != 0 || b < 1 || b > 8) return FVS_E_SHAPE;
+    if (toff[t] < 0 || toff[t] + b * (e - s) / 8 > soff || soff + 4 * T > RB) return FVS_E_SHAPE;
+    ta.start[t] = s;
+    ta.width[t] = e - s;
+    ta.bits[t] = b;
+    ta.toff[t] = toff[t];
+  }
+  const size_t shm = 4 * (size_t)D + 4 * 256 * (size_t)T + 4 * (size_t)RB;
+  if (shm > 160 * 1024) return FVS_E_CAPACITY;
+  hipLaunchKernelGGL(k_tiered_score, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, pos, qc, Zq, D, rec, RB,
+                     soff, ta, cb, ncnt, K, est, sd);
+  return fvs_launch_status();
+}

@@ -1,0 +1,153 @@
+"""EngineS on MI355X: the default (trellis cell-residual) engine of FanarVSE, used by the latency mode.
+
+Same entry points as the reference (src/engine_cell.py:70-102 EngineS, with Engine8's stage 2 and
+stage 3, src/engine3.py:135-175):
+    s1, code = trellis.build_index(X16, nlist)          # compact(cellify(...)) tables + Lloyd-Max code
+    E = EngineS(s1, code, H=X16)
+    I, reads, cand_ids = E.search(Qb, K, z, nprobe, k)
+A batch is one hipGraph replay per (B, K, z, nprobe, k) and one host synchronisation on the exactness
+flags; flagged queries are redone with rho = 1, beta = 1.5 and a 65,536-entry buffer.
+
+Stage 1 is the static work-list scan (src/s1cell.py:176-195) for every batch size. The reference
+switches to per-(query, cell) programs for B <= 8 and to a dense probe mask for B <= 32
+(src/s1small_cell.py:29-88); those kernels select by the same threshold-and-emit rule but estimate
+with different dot-product arithmetic (fp32 sums vs fp16 tensor-core dots). Here a single kernel with
+one canonical fp32 dot order serves all batch sizes, so a query's results do not depend on the
+batch it arrives in. For ok queries, Lemma 2 (paper/main.tex:206-213) makes the candidate set
+independent of the threshold heuristic anyway.
+"""
+import numpy as np
+import torch
+
+from . import _lib, index, s2lut
+
+
+class EngineS:
+    BN = 32
+    M = None          # emit buffer size; None = max(4096, 16 K) (src/s1cell.py:180)
+    SMALL, TINY = 32, 8
+
+    def __init__(self, s1, code, H=None):
+        self.s1, self.code, self.H = s1, code, H
+        s2lut.prepare_u(code)
+        if "VP" not in code:
+            raise ValueError("EngineS needs a Lloyd-Max tiered code (s2lut.encode_lloyd)")
+        self.blocks, self.MB = index.static_blocks(s1["off_t"], self.BN)
+        self.W1 = s1["W1"].contiguous()
+        self.inv_mnorm = s1["inv_mnorm"].float().contiguous()
+        self.means16 = s1["means16"].contiguous()
+        self.graphs = {}
+        self.nbad = 0
+        if int(s1["off_t"][-1]) != s1["words"].shape[0]:
+            raise ValueError("EngineS: cell offsets do not match the code rows")
+
+    def _params(self, K, nprobe, rho_override=None, M_override=None):
+        NC = len(self.s1["off"]) - 1
+        N = self.s1["words"].shape[0]
+        M = M_override or self.M or max(4096, 16 * K)
+        beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
+        if rho_override:
+            beta, rho = 1.5, rho_override
+        n1 = min(max(int(np.ceil(beta * K / (N / NC / self.BN + 1))), 1), nprobe)
+        return M, n1, int(np.ceil(rho * K))
+
+    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None):
+        """Threshold-and-emit over the trellis codes (src/s1cell.py:176-195). Returns (pos, ok)."""
+        s1 = self.s1
+        NC = len(s1["off"]) - 1
+        B = Qr.shape[0]
+        dev = Qr.device
+        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
+        L = int(s1["L"])
+        scratch = _lib.pairs_scratch(B, NC, dev)
+        pr = _lib.pairs(probe, n1, NC, QM, None, scratch)
+        bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
+        _lib.tr_scan(0, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=self.MB, n1=n1)
+        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
+        cnt = torch.empty((B,), dtype=torch.int32, device=dev)
+        _lib.fill_u32(cnt, 0)
+        bval = torch.empty((B, M), dtype=torch.float32, device=dev)
+        bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
+        pr = _lib.pairs(probe, probe.shape[1], NC, QM, None, scratch)
+        _lib.tr_scan(1, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, t0=t0, cnt=cnt, bval=bval,
+                     bpos=bpos, CAP=M)
+        pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
+        self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
+        return pos, ok.bool()
+
+    def _dense(self, Qb):
+        """The dense products: Qr = Qb @ W1 (f32), QM = fp16(Qb) @ means16.T (fp16), Zq = Qb @ VP (f32);
+        and qc = <Qb, c> (canonical double sum)."""
+        Qr = (Qb @ self.W1).contiguous()
+        _, _, QC, Qh, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
+        QM = (Qh @ self.means16.T).contiguous()
+        Zq = (Qb @ self.code["VP"]).contiguous()
+        return Qr, QC, QM, Zq
+
+    def _finish(self, Qb, QC, Zq, pos, z, k):
+        est, sd = _lib.tiered_score(pos, QC, Zq, self.code)
+        self._est, self._sd = est, sd
+        return _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
+
+    def _gpu(self, Qb, K, z, nprobe, k):
+        if self.H is None:
+            raise RuntimeError("EngineS.H (fp16 vectors in id order) must be set before searching")
+        Qr, QC, QM, Zq = self._dense(Qb)
+        probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
+        pos, ok = self.stage1(Qr, QM, probe, K)
+        ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
+        return ok, I, reads, ids, scores, (Qr, QC, QM, Zq, probe)
+
+    def search(self, Qb, K, z, nprobe, k, ret_scores=False):
+        """(I [B,k], reads [B], cand_ids [B,K]) (+ scores) as src/engine_cell.py:85-102."""
+        Qb = Qb.float().contiguous()
+        B = len(Qb)
+        key = (B, K, float(z), nprobe, k)
+        if key not in self.graphs:
+            qs = Qb.clone()
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                for _ in range(3):
+                    self._gpu(qs, K, z, nprobe, k)
+            torch.cuda.current_stream().wait_stream(st)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs = self._gpu(qs, K, z, nprobe, k)
+            self.graphs[key] = (g, qs, outs)
+        g, qs, (ok, I, nr, ids, sc, dense) = self.graphs[key]
+        qs.copy_(Qb)
+        g.replay()
+        I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
+        if not bool(ok.all()):
+            bad = torch.nonzero(~ok).flatten()
+            self.nbad += len(bad)
+            a, b, c, s = self._fallback(Qb[bad], K, z, k, *[t[bad].contiguous() for t in dense])
+            I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
+        return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
+
+    def _fallback(self, Qb, K, z, k, Qr, QC, QM, Zq, probe):
+        """Flagged queries again with rho = 1, beta = 1.5 and M = 65,536 (the reference recomputes them with
+        the work-list path and a larger buffer, src/engine_cell.py:98-101)."""
+        pos, _ = self.stage1(Qr, QM, probe, K, rho_override=1.0, M_override=65536)
+        ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
+        return I, reads, ids, scores
+
+    def trace(self, Qb, K, z, nprobe, k):
+        """Eager run of one batch returning every intermediate (parity tests)."""
+        Qb = Qb.float().contiguous()
+        Qr, QC, QM, Zq = self._dense(Qb)
+        probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
+        pos, ok = self.stage1(Qr, QM, probe, K)
+        ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
+        return dict(Qr=Qr, QC=QC, QM=QM, Zq=Zq, probe=probe, bm=self._bm, n1=self._n1, M=self._M, t0=self._t0,
+                    cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, ok=ok, est=self._est, sd=self._sd,
+                    ids=ids, I=I, scores=scores, reads=reads)
+
+    def gpu_bytes(self):
+        """Bytes per vector on the GPU (src/v19_final.py:29-32): trellis words + scale + id, the record, tables."""
+        s1 = self.s1
+        N = s1["words"].shape[0]
+        per = s1["words"].shape[1] * 4 + 2 + 4 + self.code["RB"]
+        tables = self.means16.numel() * 2 + self.W1.numel() * 4 + self.inv_mnorm.numel() * 4 + s1["tab"].numel() * 4
+        return per + tables / N

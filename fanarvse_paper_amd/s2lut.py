@@ -152,17 +152,39 @@ def _pack_bits(bit):
     return (bit.reshape(bit.shape[0], -1, 8).to(torch.uint8) << sh).sum(2).to(torch.uint8)
 
 
+def lloyd_cb(b):
+    """(levels, thresholds) of the b-bit Lloyd-Max quantiser of N(0, 1) (the reference's tiered.CB[b],
+    src/tiered.py:6-10, fitted there by faiss k-means on 400k samples; here the exact fixed point)."""
+    y, _ = lloyd_max(b)
+    return y, (y[1:] + y[:-1]) / 2
+
+
 def encode_uniform(X16, order, c, V, TS, seed=0, chunk=16384):
     """Uniform-codebook tiered code of x - c for the vectors in sorted order (throughput/s2lut.py:18-29
     with src/tiered.py:155-170), written straight into packed records.
     Returns the code dict: TS, V, rots, deltas, cb_uniform, rec [N, RB] uint8, RB, soff, toff, bytes."""
+    return encode_tiered(X16, order, c, V, TS, seed, chunk, kind="uniform")
+
+
+def encode_lloyd(X16, order, c, V, TS, seed=0, chunk=16384):
+    """Lloyd-Max tiered code of x - c (src/tiered.py:29-44, the default engine's stage 2) in the same
+    packed record layout (src/tiered_fused.py:112-125). The code dict has `levels` {b: levels} and `cb`,
+    the [T, 256] f32 table of each tier's levels that the GPU scorer reads."""
+    return encode_tiered(X16, order, c, V, TS, seed, chunk, kind="lloyd")
+
+
+def encode_tiered(X16, order, c, V, TS, seed=0, chunk=16384, kind="uniform"):
     dev = X16.device
     N = len(order)
     rots = tier_rotations(TS, seed)
-    deltas, cbs = {}, {}
+    deltas, cbs, levels = {}, {}, {}
     for b in sorted({bb for _, _, bb in TS}):
-        _, delta, lv, th = uniform_cb(b)
-        deltas[b] = delta
+        if kind == "uniform":
+            _, delta, lv, th = uniform_cb(b)
+            deltas[b] = delta
+        else:
+            lv, th = lloyd_cb(b)
+        levels[b] = np.asarray(lv, dtype=np.float32)
         cbs[b] = (torch.tensor(lv, dtype=torch.float32, device=dev), torch.tensor(th, dtype=torch.float32, device=dev))
     toff, soff, RB = record_layout(TS)
     rec = torch.zeros((N, RB), dtype=torch.uint8, device=dev)
@@ -190,8 +212,14 @@ def encode_uniform(X16, order, c, V, TS, seed=0, chunk=16384):
             ss[j:j + n, t, 1] = (nf * torch.sqrt((1 - ct ** 2).clamp(min=0)) / (ct * (dt - 1) ** 0.5)).half()
     rec[:, soff:soff + 4 * len(TS)] = ss.reshape(N, -1).view(torch.uint8)
     nbytes = sum((e - s) * bb for s, e, bb in TS) / 8 + 4 * len(TS)
+    cbt = torch.zeros((len(TS), 256), dtype=torch.float32)
+    for t, (_, _, bb) in enumerate(TS):
+        cbt[t, :2 ** bb] = torch.from_numpy(levels[bb])
+    if kind == "lloyd":
+        return dict(TS=TS, V=V, rots=rots, kind=kind, levels=levels, cb=cbt.to(dev), rec=rec, RB=RB, soff=soff,
+                    toff=toff, bytes=nbytes)
     cb_uniform = {b: (torch.arange(2 ** b).float() - (2 ** b - 1) / 2) * d_ for b, d_ in deltas.items()}
-    return dict(TS=TS, V=V, rots=rots, deltas=deltas, cb_uniform=cb_uniform, rec=rec, RB=RB, soff=soff, toff=toff,
+    return dict(TS=TS, V=V, rots=rots, kind=kind, deltas=deltas, cb_uniform=cb_uniform, rec=rec, RB=RB, soff=soff, toff=toff,
                 bytes=nbytes)
 
 
@@ -205,7 +233,10 @@ def prepare_u(code):
     D = torch.zeros(d, d, device=V.device)
     for (s, e, _), P in zip(code["TS"], code["rots"]):
         D[s:e, s:e] = P.to(V.device)
-    code["VP16"] = (V @ D).half().contiguous()
+    VP = V @ D
+    code["VP16"] = VP.half().contiguous()
+    if code.get("kind") == "lloyd":
+        code["VP"] = VP.contiguous()  # the default engine rotates fp32 queries (src/tiered_fused.py:47-57)
 
 
 # --------------------------------------------------------------------------- search-time entry points

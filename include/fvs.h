@@ -188,6 +188,65 @@ int fvs_refine(const float *est, const float *sd, const int32_t *pos, const int3
                const float *Q, int64_t B, int32_t K, int32_t d, float z, int32_t k, int32_t *ids, int32_t *I,
                float *scores, int32_t *reads, void *stream);
 
+/* ============================================================ trellis engine (latency mode)
+ * The default engine of the reference (src/engine_cell.py:70-102 EngineS, src/engine3.py:135-175 Engine8):
+ * cell-residual bitshift-trellis codes in stage 1 and the Lloyd-Max tiered code in stage 2. */
+
+/*
+ * Trellis encoder (a20). Replaces viterbi_fused.viterbi_paths_fused (src/viterbi_fused.py:7-46), the
+ * word packing paths_to_words (src/trellis_scan.py:10-18) and the scale of cellify (src/engine_cell.py:19-22).
+ *   Zs f32 [n, R] normalised residual rows (|row| = sqrt(R)); nz f32 [n] their norms; tab f32 [2^L] = alpha*T.
+ *   words u32 [n, W], W = (R + L - 1 + 31) / 32: the L bits of the first state (MSB first), then the lowest
+ *   bit of each later state, first bit in the most significant position of word 0.
+ *   scale1 fp16 [n] = nz / (fip * |Y|), fip = <Zs, Y> / (|Y| sqrt(R)), Y = tab[path];
+ *   paths i32 [n, R] or NULL.
+ * Canonical order: cost_0(s) = d*d, d = Zs[0] - tab[s]; cost_j(s) = min(cost(s >> 1), cost((s >> 1) | 2^(L-1)))
+ *   + d*d, the second predecessor taken only when strictly cheaper; the last state is the smallest index of
+ *   minimum cost. |Y|^2 and <Zs, Y> are double sums (lane = j % 64, xor butterfly), then f32.
+ * R must be 256; L in 8..10.
+ */
+int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, const float *tab, int32_t L,
+                       uint32_t *words, int32_t W, uint16_t *scale1, int32_t *paths, void *stream);
+
+/*
+ * Trellis stage-1 scan (a20 decode, a21 search_static kernels _first_compact_s / _emit_loop_s,
+ * src/s1cell.py:121-154; the same selection serves a22's batch sizes). Same work list, pair lists and
+ * outputs as fvs_i8_scan, over the static (cell, 32-row block) items of static_blocks (not the grouped
+ * chunks); qcp = (float)QM[q][c] (no norm factor).
+ *   Qr f32 [B, R] = Qb @ W1; words u32 [N, W]; scale1 fp16 [N]; tab f32 [2^L].
+ *   state_j = bits j .. j+L-1 of the row's stream (MSB first), v_j = tab[state_j];
+ *   est = fmaf((float)scale1, lo + hi, qcp), lo = sequential fmaf over j < R/2 of v_j * Qr[j] from +0,
+ *   hi likewise over j >= R/2.
+ * R must be 256; 2 <= L <= 12.
+ */
+int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
+                const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk, const int32_t *ps,
+                const int32_t *pe, const uint32_t *words, int32_t W, const uint16_t *scale1, const float *tab,
+                int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt, float *bval, int32_t *bpos,
+                float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
+
+/*
+ * Routing on fp32 keys (a7 for the default engine). Replaces route() (src/engine_cell.py:40-42):
+ * (QM.float() * inv_mnorm).topk(nprobe). QM fp16 [B, NC]; scale f32 [NC]; probe i32 [B, nprobe] sorted by
+ * (key descending, cell ascending), key = (float)QM[q][c] * scale[c]. NC <= 8192, nprobe <= 4096.
+ */
+int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int32_t NC, int32_t nprobe,
+                          int32_t *probe, void *stream);
+
+/*
+ * Lloyd-Max tiered stage 2 (a23). Replaces tiered_fused.score / _tiered_score_rec (src/tiered_fused.py:47-141).
+ *   pos i32 [B, K]; qc f32 [B] = <q, c>; Zq f32 [B, D] = Qb @ VP (fp32); rec u8 [N, RB] packed records;
+ *   tiers i32 [T][3] (start, end, bits) and toff i32 [T] are HOST arrays; cb f32 [T, 256]: tier t's levels
+ *   in code order; ncnt i32 [B] or NULL. est, sd f32 [B, K]; slots m >= ncnt[q] get (-1e30, 0).
+ * Canonical order: code_k from the tier's planes (MSB plane first); lane l (0..63) sums
+ *   fmaf(cb[t][code_k], Zq[start_t + k], .) over k = l, l + 64, ... from +0, then the xor butterfly gives
+ *   a_t; est = fmaf(a_t, scale_t, est), var = fmaf(qn2_t * sig_t, sig_t, var) for t = 0..T-1 from
+ *   est = qc, var = 0; sd = sqrtf(var); qn2_t = (float) double sum of Zq^2 over the tier (lane tree).
+ */
+int fvs_tiered_score(const int32_t *pos, const float *qc, const float *Zq, int32_t D, const uint8_t *rec, int64_t N,
+                     int32_t RB, int32_t soff, int32_t T, const int32_t *tiers, const int32_t *toff, const float *cb,
+                     const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,5 +1,6 @@
 /*
- * oracle.c - CPU restatement of the FanarVSE throughput-mode search path (TEST INFRASTRUCTURE).
+ * oracle.c - CPU restatement of the FanarVSE search paths (throughput int8 engine and the trellis
+ * latency engine) -- TEST INFRASTRUCTURE.
  *
  * This file is the checker, not the product: only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load it. Each function restates one reference function (cited
@@ -181,9 +182,25 @@ static inline float pair_const(const uint16_t *QM, int64_t q, int NC, int c, con
 
 /* First pass (a9), throughput/ivf8c_kern.py:2-16: block maxima over the first n1 probed cells.
  * bm[q][j][b] for b < blocks(cell); other entries are not written. */
-void or_first_pass(const int8_t *q8, const float *qs, const int32_t *probe, int npr, int n1, const int32_t *off,
-                   const int8_t *Z, const float *zs, int R, const uint16_t *QM, int NC, const float *mnorm, int64_t B,
-                   int MB, float *bm) {
+/* An estimator of est(q, row) for one (query, cell) pair constant qcp. */
+typedef float (*est_fn)(const void *ctx, int64_t q, int64_t row, float qcp);
+
+typedef struct {
+  const int8_t *q8;
+  const float *qs;
+  const int8_t *Z;
+  const float *zs;
+  int R;
+} i8_ctx;
+
+static float est_i8_cb(const void *ctx, int64_t q, int64_t r, float qcp) {
+  const i8_ctx *c = (const i8_ctx *)ctx;
+  return est_i8(c->q8 + q * c->R, c->qs[q], c->Z + r * c->R, c->zs[r], qcp, c->R);
+}
+
+/* First pass over the first n1 probed cells: maxima per (query, probe rank, block of the cell). */
+static void first_pass_gen(est_fn f, const void *ctx, const int32_t *probe, int npr, int n1, const int32_t *off,
+                           const uint16_t *QM, int NC, const float *mnorm, int64_t B, int MB, float *bm) {
 #pragma omp parallel for schedule(dynamic, 1)
   for (int64_t q = 0; q < B; q++) {
     for (int j = 0; j < n1; j++) {
@@ -196,8 +213,7 @@ void or_first_pass(const int8_t *q8, const float *qs, const int32_t *probe, int 
         float m = -1e30f;
         for (int r = blk * 32; r < blk * 32 + 32; r++) {
           if (r < cs || r >= ce) continue;
-          const float e = est_i8(q8 + q * R, qs[q], Z + (int64_t)r * R, zs[r], qcp, R);
-          m = fmaxf(m, e);
+          m = fmaxf(m, f(ctx, q, r, qcp));
         }
         bm[((int64_t)q * n1 + j) * MB + b] = m;
       }
@@ -205,7 +221,53 @@ void or_first_pass(const int8_t *q8, const float *qs, const int32_t *probe, int 
   }
 }
 
-/* Threshold t0 (a10), throughput/enginei8.py:53-55. */
+/* Emit: every probed row with est >= t0, kept in canonical order (est desc, row asc), first M stored. */
+static void emit_gen(est_fn f, const void *ctx, const int32_t *probe, int npr, int np, const int32_t *off,
+                     const uint16_t *QM, int NC, const float *mnorm, const float *t0, int64_t B, int M, int32_t *cnt,
+                     float *bval, int32_t *bpos) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t q = 0; q < B; q++) {
+    size_t cap = 1024, n = 0;
+    uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * cap);
+    const float th = t0[q];
+    for (int j = 0; j < np; j++) {
+      const int c = probe[q * npr + j];
+      const float qcp = pair_const(QM, q, NC, c, mnorm);
+      for (int r = off[c]; r < off[c + 1]; r++) {
+        const float e = f(ctx, q, r, qcp);
+        if (e >= th) {
+          if (n == cap) {
+            cap *= 2;
+            keys = (uint64_t *)realloc(keys, sizeof(uint64_t) * cap);
+          }
+          keys[n++] = ((uint64_t)ord32(e) << 32) | (uint64_t)(0xffffffffu - (uint32_t)r);
+        }
+      }
+    }
+    qsort(keys, n, sizeof(uint64_t), cmp_u64_desc);
+    cnt[q] = (int32_t)n;
+    for (size_t i = 0; i < (size_t)M; i++) {
+      if (i < n) {
+        const uint32_t k = (uint32_t)(keys[i] >> 32);
+        const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+        memcpy(&bval[q * M + i], &u, 4);
+        bpos[q * M + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
+      } else {
+        bval[q * M + i] = -1e30f;
+        bpos[q * M + i] = 0;
+      }
+    }
+    free(keys);
+  }
+}
+
+void or_first_pass(const int8_t *q8, const float *qs, const int32_t *probe, int npr, int n1, const int32_t *off,
+                   const int8_t *Z, const float *zs, int R, const uint16_t *QM, int NC, const float *mnorm, int64_t B,
+                   int MB, float *bm) {
+  const i8_ctx ctx = {q8, qs, Z, zs, R};
+  first_pass_gen(est_i8_cb, &ctx, probe, npr, n1, off, QM, NC, mnorm, B, MB, bm);
+}
+
 void or_threshold(const float *bm, const int32_t *probe, int npr, const int32_t *off, int64_t B, int n1, int MB, int r,
                   float *t0) {
 #pragma omp parallel for schedule(static)
@@ -235,44 +297,10 @@ void or_threshold(const float *bm, const int32_t *probe, int npr, const int32_t 
 void or_emit(const int8_t *q8, const float *qs, const int32_t *probe, int npr, int np, const int32_t *off,
              const int8_t *Z, const float *zs, int R, const uint16_t *QM, int NC, const float *mnorm, const float *t0,
              int64_t B, int M, int32_t *cnt, float *bval, int32_t *bpos) {
-#pragma omp parallel for schedule(dynamic, 1)
-  for (int64_t q = 0; q < B; q++) {
-    size_t cap = 1024, n = 0;
-    uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * cap);
-    const float th = t0[q];
-    for (int j = 0; j < np; j++) {
-      const int c = probe[q * npr + j];
-      const float qcp = pair_const(QM, q, NC, c, mnorm);
-      for (int r = off[c]; r < off[c + 1]; r++) {
-        const float e = est_i8(q8 + q * R, qs[q], Z + (int64_t)r * R, zs[r], qcp, R);
-        if (e >= th) {
-          if (n == cap) {
-            cap *= 2;
-            keys = (uint64_t *)realloc(keys, sizeof(uint64_t) * cap);
-          }
-          keys[n++] = ((uint64_t)ord32(e) << 32) | (uint64_t)(0xffffffffu - (uint32_t)r);
-        }
-      }
-    }
-    qsort(keys, n, sizeof(uint64_t), cmp_u64_desc);
-    cnt[q] = (int32_t)n;
-    for (size_t i = 0; i < (size_t)M; i++) {
-      if (i < n) {
-        const uint32_t k = (uint32_t)(keys[i] >> 32);
-        const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-        memcpy(&bval[q * M + i], &u, 4);
-        bpos[q * M + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
-      } else {
-        bval[q * M + i] = -1e30f;
-        bpos[q * M + i] = 0;
-      }
-    }
-    free(keys);
-  }
+  const i8_ctx ctx = {q8, qs, Z, zs, R};
+  emit_gen(est_i8_cb, &ctx, probe, npr, np, off, QM, NC, mnorm, t0, B, M, cnt, bval, bpos);
 }
 
-/* Final stage-1 selection (a12) and the delta rule (a14): throughput/enginei8.py:60, :87-88.
- * bval/bpos hold each query's entries in canonical order (as or_emit writes them). */
 void or_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64_t B, int M, int K, int kd, float delta,
                int32_t *pos, float *est1, uint8_t *ok, int32_t *ncnt) {
 #pragma omp parallel for schedule(static)
@@ -469,5 +497,195 @@ void or_refine(const float *est, const float *sd, const int32_t *pos, const int3
     free(score);
     free(flag);
     free(keys);
+  }
+}
+
+/* ================================================================ trellis engine (latency mode)
+ * Bitshift trellis (k = 1 bit per coordinate, L-bit states), src/trellis.py:12-33,
+ * src/trellis_scan.py:10-44, src/viterbi_fused.py:7-46. */
+
+/* Viterbi over one vector (n = R coordinates): predecessors of s are (s >> 1) | (u << (L-1)); p1 is
+ * taken only when its cost is strictly smaller (viterbi_fused.py:20); the final state is the smallest
+ * index of minimum cost (:29-30). Costs in f32: d = x - tab[s]; cost = best + d * d. */
+static void viterbi_row(const float *x, int R, const float *tab, int L, int32_t *path) {
+  const int S = 1 << L, half = S >> 1;
+  float *ca = (float *)malloc(sizeof(float) * S), *cb = (float *)malloc(sizeof(float) * S);
+  uint8_t *back = (uint8_t *)malloc((size_t)(R - 1) * S);
+  for (int s = 0; s < S; s++) {
+    const float d = x[0] - tab[s];
+    ca[s] = d * d;
+  }
+  for (int j = 1; j < R; j++) {
+    for (int s = 0; s < S; s++) {
+      const int p0 = s >> 1, p1 = p0 | half;
+      const float c0 = ca[p0], c1 = ca[p1];
+      const int take1 = c1 < c0;
+      const float d = x[j] - tab[s];
+      cb[s] = (take1 ? c1 : c0) + d * d;
+      back[(size_t)(j - 1) * S + s] = (uint8_t)take1;
+    }
+    float *t = ca;
+    ca = cb;
+    cb = t;
+  }
+  int st = 0;
+  for (int s = 1; s < S; s++)
+    if (ca[s] < ca[st]) st = s;
+  path[R - 1] = st;
+  for (int j = R - 1; j > 0; j--) {
+    const int u = back[(size_t)(j - 1) * S + st];
+    st = (st >> 1) | (u << (L - 1));
+    path[j - 1] = st;
+  }
+  free(ca);
+  free(cb);
+  free(back);
+}
+
+/* Encoder: paths, words (trellis_scan.py:10-18) and the fp16 scale (engine_cell.py:21-22) with the
+ * canonical double sums (lane = j % 64, xor butterfly) of the GPU kernel. */
+void or_trellis_encode(const float *Zs, const float *nz, int64_t n, int R, const float *tab, int L, int W,
+                       uint32_t *words, uint16_t *scale1, int32_t *paths) {
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t v = 0; v < n; v++) {
+    const float *x = Zs + v * R;
+    int32_t *path = paths + v * R;
+    viterbi_row(x, R, tab, L, path);
+    for (int w = 0; w < W; w++) {
+      uint32_t word = 0;
+      for (int t = 0; t < 32; t++) {
+        const int b = 32 * w + t;
+        uint32_t bit = 0;
+        if (b < L)
+          bit = ((uint32_t)path[0] >> (L - 1 - b)) & 1u;
+        else if (b < R + L - 1)
+          bit = (uint32_t)path[b - L + 1] & 1u;
+        word |= bit << (31 - t);
+      }
+      words[v * W + w] = word;
+    }
+    double l1[64], l2[64];
+    for (int l = 0; l < 64; l++) l1[l] = l2[l] = 0.0;
+    for (int j = 0; j < R; j++) {
+      const double y = (double)tab[path[j]];
+      l1[j % 64] += y * y;
+      l2[j % 64] += (double)x[j] * y;
+    }
+    const float yn = sqrtf((float)butterfly64_d(l1));
+    const float fip = (float)butterfly64_d(l2) / (yn * sqrtf((float)R));
+    scale1[v] = f2h(nz[v] / (fip * yn));
+  }
+}
+
+/* Decoded coordinate j of a word stream (trellis_scan.py:36-44). */
+static inline uint32_t tr_window(const uint32_t *w, int W, int j, int L) {
+  const int wi = j >> 5, off = j & 31;
+  const uint64_t w0 = w[wi], w1 = wi + 1 < W ? w[wi + 1] : 0u;
+  return (uint32_t)((((w0 << 32) | w1) >> (64 - L - off)) & ((1u << L) - 1u));
+}
+
+void or_trellis_decode(const uint32_t *words, int64_t n, int W, int R, int L, int32_t *states) {
+  for (int64_t v = 0; v < n; v++)
+    for (int j = 0; j < R; j++) states[v * R + j] = (int32_t)tr_window(words + v * W, W, j, L);
+}
+
+typedef struct {
+  const float *Qr;
+  const uint32_t *words;
+  int W;
+  const uint16_t *scale1;
+  const float *tab;
+  int L, R;
+} tr_ctx;
+
+/* est = fmaf(scale1, lo + hi, qcp); lo and hi are sequential fmaf chains over the two halves. */
+static float est_tr_cb(const void *ctx, int64_t q, int64_t r, float qcp) {
+  const tr_ctx *c = (const tr_ctx *)ctx;
+  const float *qv = c->Qr + q * c->R;
+  const uint32_t *w = c->words + r * c->W;
+  float lo = 0.f, hi = 0.f;
+  const int H = c->R / 2;
+  for (int j = 0; j < H; j++) lo = fmaf(c->tab[tr_window(w, c->W, j, c->L)], qv[j], lo);
+  for (int j = H; j < c->R; j++) hi = fmaf(c->tab[tr_window(w, c->W, j, c->L)], qv[j], hi);
+  return fmaf(h2f(c->scale1[r]), lo + hi, qcp);
+}
+
+void or_tr_first_pass(const float *Qr, const int32_t *probe, int npr, int n1, const int32_t *off,
+                      const uint32_t *words, int W, const uint16_t *scale1, const float *tab, int L, int R,
+                      const uint16_t *QM, int NC, int64_t B, int MB, float *bm) {
+  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  first_pass_gen(est_tr_cb, &ctx, probe, npr, n1, off, QM, NC, NULL, B, MB, bm);
+}
+
+void or_tr_emit(const float *Qr, const int32_t *probe, int npr, int np, const int32_t *off, const uint32_t *words,
+                int W, const uint16_t *scale1, const float *tab, int L, int R, const uint16_t *QM, int NC,
+                const float *t0, int64_t B, int M, int32_t *cnt, float *bval, int32_t *bpos) {
+  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  emit_gen(est_tr_cb, &ctx, probe, npr, np, off, QM, NC, NULL, t0, B, M, cnt, bval, bpos);
+}
+
+/* Routing on fp32 keys (float)QM * scale (engine_cell.py:40-42), sorted by (key desc, cell asc). */
+void or_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int NC, int np, int32_t *probe) {
+#pragma omp parallel for schedule(static)
+  for (int64_t q = 0; q < B; q++) {
+    uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * NC);
+    for (int c = 0; c < NC; c++)
+      keys[c] = ((uint64_t)ord32(h2f(QM[q * NC + c]) * scale[c]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+    qsort(keys, NC, sizeof(uint64_t), cmp_u64_desc);
+    for (int i = 0; i < np; i++) probe[q * np + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
+    free(keys);
+  }
+}
+
+/* Lloyd-Max tiered stage 2 (src/tiered_fused.py:47-72, packed records :112-125). cb: [T][256] levels. */
+void or_tiered_score(const int32_t *pos, const float *qc, const float *Zq, int D, const uint8_t *rec, int RB,
+                     int soff, int T, const int32_t *tiers, const int32_t *toff, const float *cb, const int32_t *ncnt,
+                     int64_t B, int K, float *est, float *sd) {
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t q = 0; q < B; q++) {
+    const float *zq = Zq + q * D;
+    float qn2[OR_MAXT];
+    for (int t = 0; t < T; t++) {
+      double l2[64];
+      for (int l = 0; l < 64; l++) l2[l] = 0.0;
+      for (int k = 0; k < tiers[3 * t + 1] - tiers[3 * t]; k++) {
+        const double z = (double)zq[tiers[3 * t] + k];
+        l2[k % 64] += z * z;
+      }
+      qn2[t] = (float)butterfly64_d(l2);
+    }
+    const int nc = ncnt ? (ncnt[q] < K ? ncnt[q] : K) : K;
+    for (int m = 0; m < K; m++) {
+      if (m >= nc) {
+        est[q * K + m] = -1e30f;
+        sd[q * K + m] = 0.f;
+        continue;
+      }
+      const uint8_t *r = rec + (int64_t)pos[q * K + m] * RB;
+      float e = qc[q], var = 0.f;
+      for (int t = 0; t < T; t++) {
+        const int s = tiers[3 * t], d = tiers[3 * t + 1] - s, b = tiers[3 * t + 2], kb = d / 8;
+        const uint8_t *pl = r + toff[t];
+        float lane[64];
+        for (int l = 0; l < 64; l++) lane[l] = 0.f;
+        for (int k = 0; k < d; k++) {
+          int code = 0;
+          for (int p = 0; p < b; p++) code |= ((pl[p * kb + (k >> 3)] >> (7 - (k & 7))) & 1) << (b - 1 - p);
+          lane[k % 64] = fmaf(cb[256 * t + code], zq[s + k], lane[k % 64]);
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+          float nl[64];
+          for (int l = 0; l < 64; l++) nl[l] = lane[l] + lane[l ^ o];
+          memcpy(lane, nl, sizeof(nl));
+        }
+        uint16_t ss[2];
+        memcpy(ss, r + soff + 4 * t, 4);
+        const float sc = h2f(ss[0]), sg = h2f(ss[1]);
+        e = fmaf(lane[0], sc, e);
+        var = fmaf(qn2[t] * sg, sg, var);
+      }
+      est[q * K + m] = e;
+      sd[q * K + m] = sqrtf(var);
+    }
   }
 }

@@ -11,6 +11,8 @@ References (under /root/reference):
     params             throughput/enginei8.py:40-47
     pipeline           throughput/enginei8.py:36-120 (stage1_i8, _gpu NROUTE branch, _finish, _fallback)
     recall             src/rev_fanardb.py:134-136
+    tr_params          src/s1cell.py:176-190, src/engine_cell.py:78
+    tr_pipeline        src/engine_cell.py:74-102 (EngineS._gpu and its fallback), src/engine3.py:135-146
 Pinned by tests/test_oracle_*.py (closed forms, brute force, the paper's lemmas, planted mistakes).
 """
 import ctypes
@@ -110,7 +112,7 @@ def project(Q, Vr):
 
 
 def query_prep(Q, Vr, c, z=None):
-    """(q8, qs, qc, qh); z = Q @ Vr is computed here (sequential fp32) unless given."""
+    """(q8, qs, qc, qh); z = Q @ Vr is computed here (sequential fp32) unless given (then Vr is unused)."""
     Q = _c(Q, np.float32)
     c = _c(c, np.float32)
     z = project(Q, Vr) if z is None else _c(z, np.float32)
@@ -346,6 +348,149 @@ def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None,
         estf, sdf = lut_score(f1["pos"], qc[bad], Lf, False, qsf, qnf, idx["rec"], idx["soff"], idx["TS"],
                               idx["deltas"], idx["toff"], None)
         idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], idx["order"], idx["H"], np.asarray(Q)[bad], z, k)
+        out["I"][bad], out["scores"][bad], out["reads"][bad], out["cand"][bad] = If, scf, rf_, idsf
+        out["fallback_ok"] = f1["ok"]
+    return out
+
+
+# ------------------------------------------------------------------------------------ trellis engine
+def trellis_encode(Zs, nz, tab, L):
+    """(words [n, W] uint32, scale1 [n] fp16 bits, paths [n, R] int32) of normalised rows (or_trellis_encode)."""
+    Zs = _c(Zs, np.float32)
+    nz = _c(nz, np.float32)
+    tab = _c(tab, np.float32)
+    n, R = Zs.shape
+    W = (R + L - 1 + 31) // 32
+    words = np.empty((n, W), np.uint32)
+    scale1 = np.empty(n, np.uint16)
+    paths = np.empty((n, R), np.int32)
+    lib().or_trellis_encode(_p(Zs), _p(nz), I64(n), I32(R), _p(tab), I32(L), I32(W), _p(words), _p(scale1), _p(paths))
+    return words, scale1, paths
+
+
+def trellis_decode(words, R, L):
+    words = _c(words, np.uint32)
+    n, W = words.shape
+    st = np.empty((n, R), np.int32)
+    lib().or_trellis_decode(_p(words), I64(n), I32(W), I32(R), I32(L), _p(st))
+    return st
+
+
+def route_topk_scaled(QM16, scale, nprobe):
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    scale = _c(scale, np.float32)
+    B, NC = QM16.shape
+    probe = np.empty((B, nprobe), np.int32)
+    lib().or_route_topk_scaled(_p(QM16), _p(scale), I64(B), I32(NC), I32(nprobe), _p(probe))
+    return probe
+
+
+def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB):
+    Qr = _c(Qr, np.float32)
+    probe = _c(probe, np.int32)
+    off = _c(off, np.int32)
+    words = _c(words, np.uint32)
+    scale1 = _c(np.asarray(scale1).view(np.uint16), np.uint16)
+    tab = _c(tab, np.float32)
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    B, npr = probe.shape
+    bm = np.full((B, n1, MB), -1e30, np.float32)
+    lib().or_tr_first_pass(_p(Qr), _p(probe), I32(npr), I32(n1), _p(off), _p(words), I32(words.shape[1]), _p(scale1),
+                           _p(tab), I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), I64(B), I32(MB), _p(bm))
+    return bm
+
+
+def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M):
+    Qr = _c(Qr, np.float32)
+    probe = _c(probe, np.int32)
+    off = _c(off, np.int32)
+    words = _c(words, np.uint32)
+    scale1 = _c(np.asarray(scale1).view(np.uint16), np.uint16)
+    tab = _c(tab, np.float32)
+    QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
+    t0 = _c(t0, np.float32)
+    B, npr = probe.shape
+    cnt = np.empty(B, np.int32)
+    bval = np.empty((B, M), np.float32)
+    bpos = np.empty((B, M), np.int32)
+    lib().or_tr_emit(_p(Qr), _p(probe), I32(npr), I32(npr), _p(off), _p(words), I32(words.shape[1]), _p(scale1), _p(tab),
+                     I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), _p(t0), I64(B), I32(M), _p(cnt), _p(bval),
+                     _p(bpos))
+    return cnt, bval, bpos
+
+
+def tiered_score(pos, qc, Zq, rec, soff, TS, toff, cb, ncnt=None):
+    pos = _c(pos, np.int32)
+    qc = _c(qc, np.float32)
+    Zq = _c(Zq, np.float32)
+    rec = _c(rec, np.uint8)
+    cb = _c(cb, np.float32)
+    tiers = _tiers(TS)
+    to = _c(toff, np.int32)
+    B, K = pos.shape
+    est = np.empty((B, K), np.float32)
+    sd = np.empty((B, K), np.float32)
+    nc = None if ncnt is None else _c(ncnt, np.int32)
+    lib().or_tiered_score(_p(pos), _p(qc), _p(Zq), I32(Zq.shape[1]), _p(rec), I32(rec.shape[1]), I32(soff), I32(len(TS)),
+                          _p(tiers), _p(to), _p(cb), _p(nc) if nc is not None else None, I64(B), I32(K), _p(est), _p(sd))
+    return est, sd
+
+
+def trellis_index_from_tables(s1, code, H):
+    """Host copies of the default engine's tables (fanarvse_paper_amd.trellis.build_index)."""
+    import torch
+
+    t = lambda x: x.detach().cpu().numpy() if torch.is_tensor(x) else np.asarray(x)
+    return dict(order=t(s1["order"]).astype(np.int32), off=np.asarray(s1["off"]).astype(np.int32),
+                inv_mnorm=t(s1["inv_mnorm"]).astype(np.float32), c=t(s1["c"]).astype(np.float32),
+                W1=t(s1["W1"]).astype(np.float32), tab=t(s1["tab"]).astype(np.float32), L=int(s1["L"]),
+                words=t(s1["words"]).view(np.uint32), scale1=t(s1["scale1"]).view(np.uint16),
+                means16=t(s1["means16"]).view(np.uint16), TS=list(code["TS"]), toff=np.array(code["toff"], np.int32),
+                soff=int(code["soff"]), rec=t(code["rec"]), cb=t(code["cb"]).astype(np.float32), H=t(H).view(np.uint16))
+
+
+def tr_params(K, nprobe, N, NC, M=None, rho_override=None, M_override=None, BN=32):
+    """(M, n1, r) of search_static (src/s1cell.py:176-190) with the reference's (beta, rho) by K
+    (src/engine_cell.py:78) and the fallback's (1.5, 1.0)."""
+    M = M_override or M or max(4096, 16 * K)
+    beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
+    if rho_override:
+        beta, rho = 1.5, rho_override
+    n1 = min(max(int(np.ceil(beta * K / (N / NC / BN + 1))), 1), nprobe)
+    return M, n1, int(np.ceil(rho * K))
+
+
+def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=None):
+    N = idx["words"].shape[0]
+    NC = len(idx["off"]) - 1
+    M, n1, r = tr_params(K, probe.shape[1], N, NC, M, rho_override, M_override)
+    MB = static_blocks(idx["off"])[4]
+    bm = tr_first_pass(Qr, probe[:, :n1], n1, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, MB)
+    t0 = threshold(bm, probe, idx["off"], n1, MB, r)
+    cnt, bval, bpos = tr_emit(Qr, probe, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, t0, M)
+    pos, est1, ok, ncnt = select(bval, bpos, cnt, K, 0, None)
+    return dict(n1=n1, r=r, M=M, MB=MB, bm=bm, t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos, est1=est1, ok=ok)
+
+
+def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True):
+    """The default engine's batch (EngineS._gpu + the fallback): Qr = Q @ W1 (f32), QM16 = fp16(Q) @ means16.T
+    (fp16), Zq = Q @ VP (f32) are the shared dense products."""
+    Q = _c(Q, np.float32)
+    _, _, qc, _ = query_prep(Q, None, idx["c"], Qr)
+    probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe)
+    s1 = tr_stage1(idx, Qr, QM16, probe, K, M)
+    est, sd = tiered_score(s1["pos"], qc, Zq, idx["rec"], idx["soff"], idx["TS"], idx["toff"], idx["cb"])
+    ids, I, scores, reads = refine(est, sd, s1["pos"], idx["order"], idx["H"], Q, z, k)
+    out = dict(qc=qc, probe=probe, est=est, sd=sd, ids=ids, I=I.copy(), scores=scores.copy(), reads=reads.copy(),
+               cand=ids.copy(), **s1)
+    bad = np.nonzero(s1["ok"] == 0)[0]
+    out["bad"] = bad
+    if fallback and len(bad):
+        f1 = tr_stage1(idx, np.asarray(Qr)[bad], np.asarray(QM16)[bad], probe[bad], K, M, rho_override=1.0,
+                       M_override=65536)
+        estf, sdf = tiered_score(f1["pos"], qc[bad], np.asarray(Zq)[bad], idx["rec"], idx["soff"], idx["TS"],
+                                 idx["toff"], idx["cb"])
+        idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], idx["order"], idx["H"], Q[bad], z, k)
         out["I"][bad], out["scores"][bad], out["reads"][bad], out["cand"][bad] = If, scf, rf_, idsf
         out["fallback_ok"] = f1["ok"]
     return out
