@@ -49,6 +49,13 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=("throughput", "latency"), default="throughput",
+                    help="throughput: the headline config (EngineI8, batch 2000); latency: the trellis default "
+                         "engine at batches 1/16/64 (BASELINE.json configs[2])")
+    ap.add_argument("--lat-points", default="256:200,384:400", help="n_p:K points of the latency mode")
+    ap.add_argument("--lat-batches", default="1,16,64")
+    ap.add_argument("--lat-z", default="1.5,2,3")
+    ap.add_argument("--lat-reps", type=int, default=200, help="timed batches per (point, z, batch) at most")
     return ap.parse_args()
 
 
@@ -68,6 +75,8 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = "cuda"
+    if args.mode == "latency":
+        return latency_mode(args)
     _lib.lib()
     t = time.time()
     X = datagen.gen(args.n, args.d, args.clusters, 0.7, seed=0, device=dev)
@@ -281,6 +290,60 @@ def cpu_baseline(E, Q, K, args, nprobe, np, torch):
     return {"value": round(nq / best, 1), "unit": "queries/s", "cores": min(cores, threads), "kind": "port",
             "sample": f"first {nq} queries of the batch, same index and operating point (n_p={nprobe}, K={K}), "
                       f"best of 3 after a warm-up; includes the two fp16 products computed on the CPU"}
+
+
+def latency_mode(args):
+    """the trellis cell-residual default engine on the same 1M x 1536 set, searched
+    with batches of 1, 16 and 64 at z in {1.5, 2, 3}; per batch the median and p99 wall time of one search
+    call (host to host: queries already on the GPU, ids copied back), as src/v19_final.py:51-59 times it."""
+    import numpy as np
+    import torch
+
+    from fanarvse_paper_amd import datagen, metrics, trellis
+    from fanarvse_paper_amd.engine_cell import EngineS
+
+    dev = "cuda"
+    t = time.time()
+    X = datagen.gen(args.n, args.d, args.clusters, 0.7, seed=0, device=dev)
+    Q = datagen.gen(2000, args.d, args.clusters, 0.7, seed=1, device=dev, dtype=torch.float32)
+    GT = datagen.ground_truth(X, Q, args.k).cpu().numpy()
+    torch.cuda.synchronize()
+    log(f"data + ground truth in {time.time() - t:.1f}s")
+    t = time.time()
+    s1, code = trellis.build_index(X, nlist=args.nlist)
+    torch.cuda.synchronize()
+    build_s = time.time() - t
+    log(f"trellis index built in {build_s:.1f}s (alpha {s1['alpha']:.3f}, tiers {code['TS']})")
+    E = EngineS(s1, code, H=X)
+    rows = []
+    for p in args.lat_points.split(","):
+        nprobe, K = (int(v) for v in p.split(":"))
+        for z in (float(v) for v in args.lat_z.split(",")):
+            # recall over the 2000 queries, in batches of 64
+            I = torch.cat([E.search(Q[i:i + 64], K, z, nprobe, args.k)[0] for i in range(0, 2000, 64)])
+            rec = metrics.recall(I.cpu().numpy(), GT, args.k)
+            for B in (int(v) for v in args.lat_batches.split(",")):
+                nb = max(20, min(args.lat_reps, 2000 // B))
+                ts = []
+                for i in range(nb + 3):
+                    Qb = Q[(i * B) % 2000:(i * B) % 2000 + B]
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    E.search(Qb, K, z, nprobe, args.k)[0].cpu()
+                    ts.append(time.perf_counter() - t0)
+                ts = np.array(ts[3:]) * 1000
+                row = dict(nprobe=nprobe, K=K, z=z, batch=B, recall=rec, median_ms=round(float(np.median(ts)), 3),
+                           p99_ms=round(float(np.percentile(ts, 99)), 3),
+                           qps=round(B / float(np.median(ts)) * 1000, 1), fallback=E.nbad)
+                rows.append(row)
+                log(f"latency {row}")
+    out = {"metric": "search latency per batch (median / p99 ms), trellis default engine, 1M x 1536",
+           "unit": "ms", "n_gpus": 1, "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"latency mode, {args.n}x{args.d} fp16 synthetic, batches {args.lat_batches}, "
+                                  f"k={args.k}", "nlist": args.nlist, "build_s": round(build_s, 1),
+                      "gpu_bytes_per_vector": round(E.gpu_bytes(), 1)},
+           "rows": rows}
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -28,7 +28,7 @@ SIGNATURES = {
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
     "fvs_pairs_scratch_bytes": [I64, I32],
-    "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, I64, P, P, P, P],
+    "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
@@ -36,8 +36,8 @@ SIGNATURES = {
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
     "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
     "fvs_trellis_encode": [P, P, I64, I32, P, I32, P, I32, P, P, P],
-    "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I32, P, P, I32, I32, P, P, P, P, P, P, I32, I32, I32, P],
-    "fvs_route_topk_scaled": [P, P, I64, I32, I32, P, P],
+    "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, I32, I32, P, P, P, P, P, P, I32, I32, I32, P],
+    "fvs_route_topk_scaled": [P, P, P, I64, I32, I32, P, P],
     "fvs_tiered_score": [P, P, P, I32, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
 }
 
@@ -156,7 +156,7 @@ def pairs_scratch(B, NC, device):
     return torch.empty((nbytes,), dtype=torch.uint8, device=device)
 
 
-def pairs(probe, n, NC, QM, mnorm, scratch=None):
+def pairs(probe, n, NC, QM, mnorm, scratch=None, qadd=None):
     """(qid, qrank, coff, ccnt, qcp) of the first n probe columns (throughput/enginei8.py:11-16)."""
     B, npr = probe.shape
     dev = probe.device
@@ -170,7 +170,8 @@ def pairs(probe, n, NC, QM, mnorm, scratch=None):
     qrank = _empty((B * n,), torch.int32, dev)
     qcp = _empty((B * n,), torch.float32, dev)
     _check(lib().fvs_pairs(_dev(probe, torch.int32, "probe"), B, npr, n, NC, _dev(QM, torch.float16, "QM"),
-                           _opt(mnorm, torch.float32, "mnorm", (NC,)), _dev(ccnt, torch.int32, "ccnt"),
+                           _opt(mnorm, torch.float32, "mnorm", (NC,)), _opt(qadd, torch.float32, "qadd", (B,)),
+                           _dev(ccnt, torch.int32, "ccnt"),
                            _dev(coff, torch.int32, "coff"), _dev(scratch, torch.uint8, "scratch"), scratch.numel(),
                            _dev(qid, torch.int32, "qid"), _dev(qrank, torch.int32, "qrank"),
                            _dev(qcp, torch.float32, "qcp"), _stream()), "fvs_pairs")
@@ -280,7 +281,7 @@ def refine(est, sd, pos, order, H, Q, z, k):
     scores = _empty((B, k), torch.float32, dev)
     reads = _empty((B,), torch.int32, dev)
     _check(lib().fvs_refine(_dev(est, torch.float32, "est"), _dev(sd, torch.float32, "sd", (B, K)),
-                            _dev(pos, torch.int32, "pos", (B, K)), _dev(order, torch.int32, "order"),
+                            _dev(pos, torch.int32, "pos", (B, K)), _opt(order, torch.int32, "order"),
                             _dev(H, torch.float16, "H", host_ok=True), _dev(Q, torch.float32, "Q", (B, d)), B, K, d,
                             F32(z), k, _dev(ids, torch.int32, "ids"), _dev(I, torch.int32, "I"),
                             _dev(scores, torch.float32, "scores"), _dev(reads, torch.int32, "reads"), _stream()),
@@ -301,9 +302,10 @@ def trellis_encode(Zs, nz, tab, L, words, scale1, paths=None):
 
 
 def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1,
-            MB=1, n1=1):
+            MB=1, n1=1, row0=0):
     """Trellis stage-1 first pass (mode 0) or emit (mode 1) over the static (cell, block) items
-    (src/s1cell.py:121-154 semantics with the canonical fp32 dot of include/fvs.h)."""
+    (src/s1cell.py:121-154 semantics with the canonical fp32 dot of include/fvs.h). words/scale1 hold index
+    rows row0 .. (device or pinned host memory)."""
     pcell, pblk, ps, pe = blocks
     qid, qrank, coff, ccnt, qcp = pr
     P_ = pcell.shape[0]
@@ -316,17 +318,20 @@ def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval
     f32, i32 = torch.float32, torch.int32
     _check(lib().fvs_tr_scan(mode, P_, _dev(Qr, f32, "Qr"), _dev(qid, i32, "qid"), _dev(qrank, i32, "qrank"),
                              _dev(coff, i32, "coff"), _dev(ccnt, i32, "ccnt"), _dev(pcell, i32, "pcell"),
-                             _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"), _dev(pe, i32, "pe"), _dev(words, i32, "words"),
-                             W, _dev(scale1, torch.float16, "scale1", (N,)), _dev(tab, f32, "tab", (2 ** L,)), L, R,
+                             _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"), _dev(pe, i32, "pe"),
+                             _dev(words, i32, "words", host_ok=True), row0, W,
+                             _dev(scale1, torch.float16, "scale1", (N,), host_ok=True), _dev(tab, f32, "tab", (2 ** L,)), L, R,
                              _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"),
                              _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1, _stream()), "fvs_tr_scan")
 
 
-def route_topk_scaled(QM, scale, nprobe):
-    """Top-n_p cells by the fp32 key (float)QM * scale (src/engine_cell.py:40-42)."""
+def route_topk_scaled(QM, scale, nprobe, qadd=None):
+    """Top-n_p cells by the fp32 key (float)QM * scale, or ((float)QM + qadd[q]) * scale
+    (src/engine_cell.py:40-42, host_resident/space_x.py:33-39)."""
     B, NC = QM.shape
     probe = _empty((B, nprobe), torch.int32, QM.device)
-    _check(lib().fvs_route_topk_scaled(_dev(QM, torch.float16, "QM"), _dev(scale, torch.float32, "scale", (NC,)), B,
+    _check(lib().fvs_route_topk_scaled(_dev(QM, torch.float16, "QM"), _dev(scale, torch.float32, "scale", (NC,)),
+                                       _opt(qadd, torch.float32, "qadd", (B,)), B,
                                        NC, nprobe, _dev(probe, torch.int32, "probe"), _stream()), "fvs_route_topk_scaled")
     return probe
 
@@ -343,7 +348,7 @@ def tiered_score(pos, qc, Zq, code, ncnt=None):
     est = _empty((B, K), torch.float32, pos.device)
     sd = _empty((B, K), torch.float32, pos.device)
     _check(lib().fvs_tiered_score(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
-                                  _dev(Zq, torch.float32, "Zq", (B, D)), D, _dev(rec, torch.uint8, "rec"), N, RB,
+                                  _dev(Zq, torch.float32, "Zq", (B, D)), D, _dev(rec, torch.uint8, "rec", host_ok=True), N, RB,
                                   int(code["soff"]), T, _tiers_arr(TS), toff, _dev(code["cb"], torch.float32, "cb", (T, 256)),
                                   _opt(ncnt, torch.int32, "ncnt", (B,)), B, K, _dev(est, torch.float32, "est"),
                                   _dev(sd, torch.float32, "sd"), _stream()), "fvs_tiered_score")

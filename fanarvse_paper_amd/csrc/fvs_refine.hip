@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, c
     const float t = z * g[i];
     lo[i] = e[i] - t;
     hi[i] = e[i] + t;
-    const int32_t id = order[pq[i]];
+    const int32_t id = order ? order[pq[i]] : pq[i];
     sid[i] = id;
     ids[q * (int64_t)K + i] = id;
   }
@@ -142,7 +142,7 @@ extern "C" int fvs_refine(const float *est, const float *sd, const int32_t *pos,
   if (B < 0 || k <= 0 || K <= k || d <= 0 || d % 8 != 0 || !(z >= 0.f)) return FVS_E_ARG;
   if (K > kMaxK || k > kMaxk || d > 8 * 64 * kMaxG) return FVS_E_CAPACITY;
   if (B == 0) return FVS_OK;
-  if (!est || !sd || !pos || !order || !H || !Q || !ids || !I || !scores || !reads) return FVS_E_ARG;
+  if (!est || !sd || !pos || !H || !Q || !ids || !I || !scores || !reads) return FVS_E_ARG;
   const size_t shm = (size_t)K * (4 * 5 + 2 + 1);
   hipStream_t st = (hipStream_t)stream;
   const int ng = (d / 8 + 63) / 64;

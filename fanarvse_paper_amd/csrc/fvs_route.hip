@@ -122,7 +122,8 @@ __global__ __launch_bounds__(256) void k_cell_scan(const int32_t *__restrict__ c
 // One block per cell: its queries in ascending order, their probe ranks and pair constants.
 __global__ __launch_bounds__(256) void k_cell_emit(const uint16_t *__restrict__ rank, int64_t B,
                                                    const int32_t *__restrict__ coff, const uint16_t *__restrict__ QM,
-                                                   const float *__restrict__ mnorm, int NC, int32_t *__restrict__ qid,
+                                                   const float *__restrict__ mnorm, const float *__restrict__ qadd,
+                                                   int NC, int32_t *__restrict__ qid,
                                                    int32_t *__restrict__ qrank, float *__restrict__ qcp) {
   __shared__ int sh[8];
   const int c = blockIdx.x;
@@ -138,7 +139,8 @@ __global__ __launch_bounds__(256) void k_cell_emit(const uint16_t *__restrict__ 
       const int o = run + inc - 1;
       qid[o] = (int32_t)q;
       qrank[o] = (int32_t)r;
-      qcp[o] = fvs_h2f(QM[q * NC + c]) * sc;
+      const float v = fvs_h2f(QM[q * NC + c]) * sc;
+      qcp[o] = qadd ? v + qadd[q] : v;
     }
     if (threadIdx.x == 255) sh[6] = inc;
     __syncthreads();
@@ -164,7 +166,8 @@ extern "C" int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC) {
 }
 
 extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
-                         const float *mnorm, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes,
+                         const float *mnorm, const float *qadd, int32_t *ccnt, int32_t *coff, void *scratch,
+                         int64_t scratch_bytes,
                          int32_t *qid, int32_t *qrank, float *qcp, void *stream) {
   if (B < 0 || NC <= 0 || n <= 0 || n > npr || n > 65535) return FVS_E_ARG;
   if (scratch_bytes < fvs_pairs_scratch_bytes(B, NC)) return FVS_E_CAPACITY;
@@ -182,6 +185,6 @@ extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n
   if ((e = fvs_launch_status())) return e;
   hipLaunchKernelGGL(k_cell_scan, dim3(1), dim3(256), 0, st, ccnt, NC, coff);
   if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_cell_emit, dim3((unsigned)NC), dim3(256), 0, st, rank, B, coff, QM, mnorm, NC, qid, qrank, qcp);
+  hipLaunchKernelGGL(k_cell_emit, dim3((unsigned)NC), dim3(256), 0, st, rank, B, coff, QM, mnorm, qadd, NC, qid, qrank, qcp);
   return fvs_launch_status();
 }

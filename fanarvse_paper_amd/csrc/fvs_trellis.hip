@@ -133,13 +133,15 @@ __global__ __launch_bounds__(256) void k_trellis_encode(const float *__restrict_
 //   est = fmaf(scale1, lo + hi, qcp),  lo / hi = sum over j < 128 / j >= 128 of tab[state_j] * Qr[j].
 // mode 0: bm[(q*n1 + qrank)*MB + blk - cs/32] = max over the block's rows in the cell.
 // mode 1: every (q, row) with est >= t0[q] is appended to the query's buffer (one atomic each).
+// words and scale1 hold rows row0 .. of the index (a staged chunk, or the whole index with row0 = 0).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, const int32_t *__restrict__ qid,
                                                  const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff,
                                                  const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
                                                  const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
                                                  const int32_t *__restrict__ pe, int P, const uint32_t *__restrict__ words,
-                                                 int W, const uint16_t *__restrict__ scale1, const float *__restrict__ tab,
+                                                 int64_t row0, int W, const uint16_t *__restrict__ scale1,
+                                                 const float *__restrict__ tab,
                                                  int L, const float *__restrict__ qcp, const float *__restrict__ t0,
                                                  int32_t *__restrict__ cnt, float *__restrict__ bval,
                                                  int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     const int i = 4 * h + k;
-    ww[k] = i < W ? words[(int64_t)rr * W + i] : 0u;
+    ww[k] = i < W ? words[((int64_t)rr - row0) * W + i] : 0u;
   }
   float v[128];
   const uint32_t mask = (uint32_t)S - 1u;
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
     const uint64_t comb = ((uint64_t)ww[i >> 5] << 32) | (uint64_t)ww[(i >> 5) + 1];
     v[i] = stab[(uint32_t)(comb >> (64 - L - (i & 31))) & mask];
   }
-  const float s1 = fvs_h2f(scale1[rr]);
+  const float s1 = fvs_h2f(scale1[(int64_t)rr - row0]);
   for (int i = 0; i < qn; i++) {
     const int pidx = qoff + i;
     const int q = qid[pidx];
@@ -207,17 +209,20 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
 }
 
 // ------------------------------------------------------------------------------------ routing
-// Top-n_p cells by the fp32 key (float)QM[q][c] * scale[c], sorted by (key descending, cell ascending).
+// Top-n_p cells by the fp32 key (float)QM[q][c] * scale[c] (or ((float)QM[q][c] + qadd[q]) * scale[c]),
+// sorted by (key descending, cell ascending).
 __global__ __launch_bounds__(256) void k_route_f32(const uint16_t *__restrict__ QM, const float *__restrict__ scale,
-                                                   int NC, int np, int32_t *__restrict__ probe) {
+                                                   const float *__restrict__ qadd, int NC, int np,
+                                                   int32_t *__restrict__ probe) {
   extern __shared__ uint64_t rk[];  // [NC] keys, then [pow2(np)] the sorted top
   __shared__ int hist[256];
   __shared__ int sh[8];
   __shared__ int gcnt;
   const int64_t q = blockIdx.x;
   uint64_t *top = rk + NC;
+  const float add = qadd ? qadd[q] : 0.f;
   for (int i = threadIdx.x; i < NC; i += 256) {
-    const float key = fvs_h2f(QM[q * NC + i]) * scale[i];
+    const float key = qadd ? (fvs_h2f(QM[q * NC + i]) + add) * scale[i] : fvs_h2f(QM[q * NC + i]) * scale[i];
     rk[i] = ((uint64_t)fvs_ord32(key) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   }
   __syncthreads();
@@ -333,12 +338,13 @@ extern "C" int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, i
 
 extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
                            const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk,
-                           const int32_t *ps, const int32_t *pe, const uint32_t *words, int32_t W, const uint16_t *scale1,
+                           const int32_t *ps, const int32_t *pe, const uint32_t *words, int64_t row0, int32_t W,
+                           const uint16_t *scale1,
                            const float *tab, int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt,
                            float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream) {
   if (R != kTrR) return FVS_E_SHAPE;
   if (mode != 0 && mode != 1) return FVS_E_ARG;
-  if (L < 2 || L > kMaxL || W != (R + L - 1 + 31) / 32 || W > 10 || P < 0) return FVS_E_ARG;
+  if (L < 2 || L > kMaxL || W != (R + L - 1 + 31) / 32 || W > 10 || P < 0 || row0 < 0) return FVS_E_ARG;
   if (P == 0) return FVS_OK;
   if (!Qr || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !words || !scale1 || !tab || !qcp)
     return FVS_E_ARG;
@@ -347,23 +353,23 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<0>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<1>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   }
   return fvs_launch_status();
 }
 
-extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int32_t NC, int32_t nprobe,
-                                     int32_t *probe, void *stream) {
+extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC,
+                                     int32_t nprobe, int32_t *probe, void *stream) {
   if (B < 0 || NC <= 0 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
   if (NC > 8192 || nprobe > 4096) return FVS_E_CAPACITY;
   if (B == 0) return FVS_OK;
   if (!QM || !scale || !probe) return FVS_E_ARG;
   const size_t shm = 8 * ((size_t)NC + (size_t)fvs_pow2_ceil(nprobe));
-  hipLaunchKernelGGL(k_route_f32, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, QM, scale, NC, nprobe, probe);
+  hipLaunchKernelGGL(k_route_f32, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, QM, scale, qadd, NC, nprobe, probe);
   return fvs_launch_status();
 }
 

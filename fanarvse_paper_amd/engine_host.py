@@ -1,0 +1,198 @@
+"""SpaceX on MI355X: the host-resident default engine (host_resident/space_x.py:13-78, SURVEY config 5).
+
+Every per-vector array lives in pinned host memory: the trellis words and scales, the packed stage-2
+records, and the fp16 rows (kept in sorted order, so no id table is needed on the GPU; ids are mapped
+on the host, as the reference's ids_host variant does). The GPU keeps only shared tables: the cell
+means projected on the stage-1 basis (meansR, fp16 [NC, R]; proj variant, space_x.py:26-27,33-36),
+W1, the stage-2 rotation VP, the trellis table, the cell offsets and the static work list, plus two
+staging slots for stage-1 chunks.
+
+Stage 1 streams: the index is cut into cell-aligned chunks of about CHUNK rows; a side stream copies
+chunk i+1's words and scales into the free staging slot (hipMemcpyAsync) while the main stream scans
+chunk i (fvs_tr_scan with row0 = the chunk's first row). Stage 2 and stage 3 read their records and
+rows zero-copy from pinned memory. Results equal EngineS's with the projected-means routing.
+"""
+import numpy as np
+import torch
+
+from . import _lib, index, s2lut
+from .engine_cell import EngineS
+
+
+def _pin(t):
+    out = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    out.copy_(t.cpu())
+    return out
+
+
+class SpaceX(EngineS):
+    CHUNK = 32768  # rows per staged stage-1 chunk
+
+    def __init__(self, s1, code, H16, proj=True):
+        if not proj:
+            raise NotImplementedError("only the projected-means variant keeps the GPU under 8 B per vector")
+        s2lut.prepare_u(code)
+        if "VP" not in code:
+            raise ValueError("SpaceX needs a Lloyd-Max tiered code (s2lut.encode_lloyd)")
+        dev = s1["words"].device
+        self.order_np = s1["order"].cpu().numpy()
+        order = s1["order"].long()
+        self.Hs = _pin(H16[order.to(H16.device)])
+        self.words_h = _pin(s1["words"])
+        self.scale1_h = _pin(s1["scale1"])
+        self.code = dict(TS=code["TS"], rec=_pin(code["rec"]), RB=code["RB"], soff=code["soff"], toff=code["toff"],
+                         cb=code["cb"].to(dev), VP=code["VP"].to(dev), kind=code.get("kind"))
+        W1 = s1["W1"].to(dev)
+        meansR = ((s1["means16"].float() - s1["c"]) @ W1).half().contiguous()
+        self.s1 = dict(off=np.asarray(s1["off"]), off_t=s1["off_t"].to(dev), c=s1["c"].to(dev), W1=W1,
+                       tab=s1["tab"].to(dev), L=int(s1["L"]), inv_mnorm=s1["inv_mnorm"].float().to(dev),
+                       meansR=meansR)
+        self.W1, self.inv_mnorm, self.meansR = W1, self.s1["inv_mnorm"], meansR
+        self.N = int(self.words_h.shape[0])
+        self.Wd = int(self.words_h.shape[1])
+        self.blocks, self.MB = index.static_blocks(self.s1["off_t"], self.BN)
+        self.H = self.Hs
+        self.graphs = {}
+        self.nbad = 0
+        self._chunks()
+        self.side = torch.cuda.Stream()
+        self.slots = [(torch.empty((self.chunk_rows, self.Wd), dtype=torch.int32, device=dev),
+                       torch.empty((self.chunk_rows,), dtype=torch.float16, device=dev)) for _ in range(2)]
+        self.copied_bytes = 0
+
+    def _params(self, K, nprobe, rho_override=None, M_override=None):
+        NC = len(self.s1["off"]) - 1
+        M = M_override or self.M or max(4096, 16 * K)
+        beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
+        if rho_override:
+            beta, rho = 1.5, rho_override
+        n1 = min(max(int(np.ceil(beta * K / (self.N / NC / self.BN + 1))), 1), nprobe)
+        return M, n1, int(np.ceil(rho * K))
+
+    def _chunks(self):
+        """Cell-aligned chunks [(row0, row1, item0, item1)] of at most chunk_rows rows."""
+        off = self.s1["off"].astype(np.int64)
+        sizes = np.diff(off)
+        self.chunk_rows = int(max(self.CHUNK, sizes.max()))
+        pcell = self.blocks[0].cpu().numpy()
+        first_item = np.searchsorted(pcell, np.arange(len(off)))  # first item of each cell (items are cell-sorted)
+        chunks, c0 = [], 0
+        NC = len(off) - 1
+        while c0 < NC:
+            c1 = c0
+            while c1 < NC and off[c1 + 1] - off[c0] <= self.chunk_rows:
+                c1 += 1
+            c1 = max(c1, c0 + 1)
+            chunks.append((int(off[c0]), int(off[c1]), int(first_item[c0]), int(first_item[c1])))
+            c0 = c1
+        self.chunks = [c for c in chunks if c[3] > c[2]]
+
+    def _scan_streamed(self, mode, Qr, pr, **kw):
+        """One stage-1 pass over every chunk, copies on the side stream overlapped with the scans."""
+        main = torch.cuda.current_stream()
+        done = [None, None]
+        for i, (r0, r1, i0, i1) in enumerate(self.chunks):
+            slot = i % 2
+            w, s = self.slots[slot]
+            with torch.cuda.stream(self.side):
+                if done[slot] is not None:
+                    self.side.wait_event(done[slot])
+                w[:r1 - r0].copy_(self.words_h[r0:r1], non_blocking=True)
+                s[:r1 - r0].copy_(self.scale1_h[r0:r1], non_blocking=True)
+                ready = torch.cuda.Event()
+                ready.record(self.side)
+            self.copied_bytes += (r1 - r0) * (4 * self.Wd + 2)
+            main.wait_event(ready)
+            blocks = tuple(b[i0:i1] for b in self.blocks)
+            _lib.tr_scan(mode, blocks, Qr, pr, w, s, self.s1["tab"], self.s1["L"], row0=r0, **kw)
+            ev = torch.cuda.Event()
+            ev.record(main)
+            done[slot] = ev
+
+    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None, QC=None):
+        NC = len(self.s1["off"]) - 1
+        B = Qr.shape[0]
+        dev = Qr.device
+        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
+        scratch = _lib.pairs_scratch(B, NC, dev)
+        pr = _lib.pairs(probe, n1, NC, QM, None, scratch, qadd=QC)
+        bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
+        self._scan_streamed(0, Qr, pr, bm=bm, MB=self.MB, n1=n1)
+        t0 = _lib.threshold(bm, probe, self.s1["off_t"], n1, self.MB, r)
+        cnt = torch.empty((B,), dtype=torch.int32, device=dev)
+        _lib.fill_u32(cnt, 0)
+        bval = torch.empty((B, M), dtype=torch.float32, device=dev)
+        bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
+        pr = _lib.pairs(probe, probe.shape[1], NC, QM, None, scratch, qadd=QC)
+        self._scan_streamed(1, Qr, pr, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
+        pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
+        self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
+        return pos, ok.bool()
+
+    def _dense(self, Qb):
+        """Qr = Qb @ W1 (f32), QC = <Qb, c>, QM = fp16(Qr) @ meansR.T (fp16; the pair term and routing key add
+        QC), Zq = Qb @ VP (f32)."""
+        Qr = (Qb @ self.W1).contiguous()
+        _, _, QC, _, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
+        QM = (Qr.half() @ self.meansR.T).contiguous()
+        Zq = (Qb @ self.code["VP"]).contiguous()
+        return Qr, QC, QM, Zq
+
+    def _finish(self, Qb, QC, Zq, pos, z, k):
+        est, sd = _lib.tiered_score(pos, QC, Zq, self.code)
+        self._est, self._sd = est, sd
+        return _lib.refine(est, sd, pos, None, self.Hs, Qb, z, k)
+
+    def _run(self, Qb, K, z, nprobe, k, rho_override=None, M_override=None, dense=None):
+        Qr, QC, QM, Zq = dense if dense is not None else self._dense(Qb)
+        probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe, qadd=QC)
+        pos, ok = self.stage1(Qr, QM, probe, K, rho_override, M_override, QC=QC)
+        ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
+        return ok, I, reads, ids, scores, (Qr, QC, QM, Zq)
+
+    def search(self, Qb, K, z, nprobe, k, ret_scores=False, sorted_ids=False):
+        """(I, reads, cand_ids) (+ scores): ids mapped to the original ids on the host (numpy -> torch CPU
+        tensors), as SpaceX.run does (host_resident/space_x.py:71-78); sorted_ids keeps sorted positions."""
+        Qb = Qb.float().contiguous()
+        ok, I, nr, ids, sc, dense = self._run(Qb, K, z, nprobe, k)
+        if not bool(ok.all()):
+            bad = torch.nonzero(~ok).flatten()
+            self.nbad += len(bad)
+            sub = tuple(t[bad].contiguous() for t in dense)
+            _, a, b, c, s, _ = self._run(Qb[bad], K, z, nprobe, k, rho_override=1.0, M_override=65536, dense=sub)
+            I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
+            I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
+        if not sorted_ids:
+            I = torch.from_numpy(self.order_np[I.cpu().numpy()])
+            ids = torch.from_numpy(self.order_np[ids.cpu().numpy()])
+        return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
+
+    def trace(self, Qb, K, z, nprobe, k):
+        Qb = Qb.float().contiguous()
+        ok, I, reads, ids, scores, (Qr, QC, QM, Zq) = self._run(Qb, K, z, nprobe, k)
+        return dict(Qr=Qr, QC=QC, QM=QM, Zq=Zq, pos=None, ok=ok, I=I, ids=ids, scores=scores, reads=reads,
+                    cnt=self._cnt, t0=self._t0, est=self._est, sd=self._sd)
+
+    def gpu_bytes(self):
+        """Bytes per vector resident on the GPU (host_resident/space_x.py:80-88): every device tensor the
+        engine holds (tables, work list, staging slots), divided by N."""
+        seen, tot = set(), 0
+
+        def walk(x):
+            nonlocal tot
+            if isinstance(x, torch.Tensor):
+                if x.is_cuda and x.untyped_storage().data_ptr() not in seen:
+                    seen.add(x.untyped_storage().data_ptr())
+                    tot += x.untyped_storage().nbytes()
+            elif isinstance(x, dict):
+                for v in x.values():
+                    walk(v)
+            elif isinstance(x, (list, tuple)):
+                for v in x:
+                    walk(v)
+
+        walk(self.s1)
+        walk(self.code)
+        walk(self.blocks)
+        walk(self.slots)
+        return tot / self.N

@@ -89,11 +89,13 @@ int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t nprobe, in
  *   scratch        at least fvs_pairs_scratch_bytes(B, NC) bytes (a cell-major probe-rank matrix)
  *   qid i32 [B*n]  query of each pair, cell-major, queries ascending inside a cell (the stable-sort order)
  *   qrank i32 [B*n] rank of the cell in the query's probe row     qcp f32 [B*n] = (float)QM[q][c] * mnorm[c]
+ *   qadd f32 [B] or NULL: when given, qcp += qadd[q] (the projected-means variant of the host-resident engine,
+ *   host_resident/space_x.py:33-36, where QM holds q.(m_c - c) in the stage-1 subspace and qadd = <q, c>)
  */
 int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC);
 int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
-              const float *mnorm, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes, int32_t *qid,
-              int32_t *qrank, float *qcp, void *stream);
+              const float *mnorm, const float *qadd, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes,
+              int32_t *qid, int32_t *qrank, float *qcp, void *stream);
 
 /*
  * int8 stage-1 scan on MFMA (a9, a11). Same inputs and outputs as the reference's CUDA twin
@@ -178,7 +180,8 @@ int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t ha
  *   pinned device-mapped host buffer); Q f32 [B, d].
  *   lo = est - z*sd, hi = est + z*sd; sure = lo > (k+1)-th largest hi; amb = hi >= k-th largest lo and not sure.
  *   score = est + 10 (sure), exact <H[id], Q> (amb), -1e9 (other).
- *   ids i32 [B, K] = order[pos]; I i32 [B, k] = ids of the top-k scores (score descending, slot ascending);
+ *   ids i32 [B, K] = order[pos] (pos itself when order is NULL, for rows H stored in sorted order);
+ *   I i32 [B, k] = ids of the top-k scores (score descending, slot ascending);
  *   scores f32 [B, k]: the exact score of an ambiguous pick, the estimate of a sure one;
  *   reads i32 [B] = #amb. Exact dot canonical order: lane l (0..63) sums elements 8g..8g+7 of groups
  *   g = l, l+64, ... with fmaf in element order, then acc += shfl_xor(acc, o) for o = 32, 16, 8, 4, 2, 1.
@@ -213,7 +216,9 @@ int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, c
  * src/s1cell.py:121-154; the same selection serves a22's batch sizes). Same work list, pair lists and
  * outputs as fvs_i8_scan, over the static (cell, 32-row block) items of static_blocks (not the grouped
  * chunks); qcp = (float)QM[q][c] (no norm factor).
- *   Qr f32 [B, R] = Qb @ W1; words u32 [N, W]; scale1 fp16 [N]; tab f32 [2^L].
+ *   Qr f32 [B, R] = Qb @ W1; words u32 [n, W] and scale1 fp16 [n] hold index rows row0 .. row0 + n - 1 (the
+ *   whole index with row0 = 0, or a staged chunk that covers every row of the P items); tab f32 [2^L].
+ *   words/scale1 may be device memory or pinned, device-mapped host memory.
  *   state_j = bits j .. j+L-1 of the row's stream (MSB first), v_j = tab[state_j];
  *   est = fmaf((float)scale1, lo + hi, qcp), lo = sequential fmaf over j < R/2 of v_j * Qr[j] from +0,
  *   hi likewise over j >= R/2.
@@ -221,17 +226,18 @@ int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, c
  */
 int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
                 const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk, const int32_t *ps,
-                const int32_t *pe, const uint32_t *words, int32_t W, const uint16_t *scale1, const float *tab,
+                const int32_t *pe, const uint32_t *words, int64_t row0, int32_t W, const uint16_t *scale1, const float *tab,
                 int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt, float *bval, int32_t *bpos,
                 float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
 
 /*
  * Routing on fp32 keys (a7 for the default engine). Replaces route() (src/engine_cell.py:40-42):
  * (QM.float() * inv_mnorm).topk(nprobe). QM fp16 [B, NC]; scale f32 [NC]; probe i32 [B, nprobe] sorted by
- * (key descending, cell ascending), key = (float)QM[q][c] * scale[c]. NC <= 8192, nprobe <= 4096.
+ * (key descending, cell ascending), key = (float)QM[q][c] * scale[c], or ((float)QM[q][c] + qadd[q]) * scale[c]
+ * when qadd (f32 [B]) is given (host_resident/space_x.py:33-39). NC <= 8192, nprobe <= 4096.
  */
-int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int32_t NC, int32_t nprobe,
-                          int32_t *probe, void *stream);
+int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC,
+                          int32_t nprobe, int32_t *probe, void *stream);
 
 /*
  * Lloyd-Max tiered stage 2 (a23). Replaces tiered_fused.score / _tiered_score_rec (src/tiered_fused.py:47-141).

@@ -176,8 +176,10 @@ static inline int cell_blocks(const int32_t *off, int c) {
   const int s = off[c], e = off[c + 1];
   return e > s ? (e - 1) / 32 - s / 32 + 1 : 0;
 }
+static const float *g_qadd = NULL; /* per-query additive pair term of the projected-means variant */
 static inline float pair_const(const uint16_t *QM, int64_t q, int NC, int c, const float *mnorm) {
-  return h2f(QM[q * NC + c]) * (mnorm ? mnorm[c] : 1.0f);  /* throughput/enginei8.py:14-15 */
+  const float v = h2f(QM[q * NC + c]) * (mnorm ? mnorm[c] : 1.0f);  /* throughput/enginei8.py:14-15 */
+  return g_qadd ? v + g_qadd[q] : v;  /* host_resident/space_x.py:33-36 */
 }
 
 /* First pass (a9), throughput/ivf8c_kern.py:2-16: block maxima over the first n1 probed cells.
@@ -612,25 +614,31 @@ static float est_tr_cb(const void *ctx, int64_t q, int64_t r, float qcp) {
 
 void or_tr_first_pass(const float *Qr, const int32_t *probe, int npr, int n1, const int32_t *off,
                       const uint32_t *words, int W, const uint16_t *scale1, const float *tab, int L, int R,
-                      const uint16_t *QM, int NC, int64_t B, int MB, float *bm) {
+                      const uint16_t *QM, int NC, const float *qadd, int64_t B, int MB, float *bm) {
   const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  g_qadd = qadd;
   first_pass_gen(est_tr_cb, &ctx, probe, npr, n1, off, QM, NC, NULL, B, MB, bm);
+  g_qadd = NULL;
 }
 
 void or_tr_emit(const float *Qr, const int32_t *probe, int npr, int np, const int32_t *off, const uint32_t *words,
                 int W, const uint16_t *scale1, const float *tab, int L, int R, const uint16_t *QM, int NC,
-                const float *t0, int64_t B, int M, int32_t *cnt, float *bval, int32_t *bpos) {
+                const float *qadd, const float *t0, int64_t B, int M, int32_t *cnt, float *bval, int32_t *bpos) {
   const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  g_qadd = qadd;
   emit_gen(est_tr_cb, &ctx, probe, npr, np, off, QM, NC, NULL, t0, B, M, cnt, bval, bpos);
+  g_qadd = NULL;
 }
 
 /* Routing on fp32 keys (float)QM * scale (engine_cell.py:40-42), sorted by (key desc, cell asc). */
-void or_route_topk_scaled(const uint16_t *QM, const float *scale, int64_t B, int NC, int np, int32_t *probe) {
+void or_route_topk_scaled(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int NC, int np,
+                          int32_t *probe) {
 #pragma omp parallel for schedule(static)
   for (int64_t q = 0; q < B; q++) {
     uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * NC);
     for (int c = 0; c < NC; c++)
-      keys[c] = ((uint64_t)ord32(h2f(QM[q * NC + c]) * scale[c]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
+      keys[c] = ((uint64_t)ord32(qadd ? (h2f(QM[q * NC + c]) + qadd[q]) * scale[c] : h2f(QM[q * NC + c]) * scale[c])
+                 << 32) | (uint64_t)(0xffffffffu - (uint32_t)c);
     qsort(keys, NC, sizeof(uint64_t), cmp_u64_desc);
     for (int i = 0; i < np; i++) probe[q * np + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
     free(keys);

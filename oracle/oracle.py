@@ -65,7 +65,7 @@ def static_blocks(off, BN=32):
     return cell.astype(np.int32), blk.astype(np.int32), s[cell].astype(np.int32), e[cell].astype(np.int32), MB
 
 
-def pairs(probe, NC, QM16, mnorm=None):
+def pairs(probe, NC, QM16, mnorm=None, qadd=None):
     """(qid, coff, ccnt, qcp, o) of the (query, cell) pairs (throughput/enginei8.py:11-16): a stable sort of
     the flattened cell ids, per-cell counts and offsets, qcp = f32(QM[q, c]) * |m_c|."""
     B, npr = probe.shape
@@ -78,6 +78,8 @@ def pairs(probe, NC, QM16, mnorm=None):
     qcp = np.asarray(QM16).view(np.float16)[qid, fo].astype(np.float32)
     if mnorm is not None:
         qcp = qcp * np.asarray(mnorm, np.float32)[fo]
+    if qadd is not None:
+        qcp = (qcp.astype(np.float32) + np.asarray(qadd, np.float32)[qid]).astype(np.float32)
     return qid, coff, ccnt, qcp.astype(np.float32), o
 
 
@@ -376,16 +378,18 @@ def trellis_decode(words, R, L):
     return st
 
 
-def route_topk_scaled(QM16, scale, nprobe):
+def route_topk_scaled(QM16, scale, nprobe, qadd=None):
     QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
     scale = _c(scale, np.float32)
+    qa = None if qadd is None else _c(qadd, np.float32)
     B, NC = QM16.shape
     probe = np.empty((B, nprobe), np.int32)
-    lib().or_route_topk_scaled(_p(QM16), _p(scale), I64(B), I32(NC), I32(nprobe), _p(probe))
+    lib().or_route_topk_scaled(_p(QM16), _p(scale), _p(qa) if qa is not None else None, I64(B), I32(NC), I32(nprobe),
+                               _p(probe))
     return probe
 
 
-def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB):
+def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB, qadd=None):
     Qr = _c(Qr, np.float32)
     probe = _c(probe, np.int32)
     off = _c(off, np.int32)
@@ -395,12 +399,14 @@ def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB):
     QM16 = _c(np.asarray(QM16).view(np.uint16), np.uint16)
     B, npr = probe.shape
     bm = np.full((B, n1, MB), -1e30, np.float32)
+    qa = None if qadd is None else _c(qadd, np.float32)
     lib().or_tr_first_pass(_p(Qr), _p(probe), I32(npr), I32(n1), _p(off), _p(words), I32(words.shape[1]), _p(scale1),
-                           _p(tab), I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), I64(B), I32(MB), _p(bm))
+                           _p(tab), I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]),
+                           _p(qa) if qa is not None else None, I64(B), I32(MB), _p(bm))
     return bm
 
 
-def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M):
+def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M, qadd=None):
     Qr = _c(Qr, np.float32)
     probe = _c(probe, np.int32)
     off = _c(off, np.int32)
@@ -413,9 +419,10 @@ def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M):
     cnt = np.empty(B, np.int32)
     bval = np.empty((B, M), np.float32)
     bpos = np.empty((B, M), np.int32)
+    qa = None if qadd is None else _c(qadd, np.float32)
     lib().or_tr_emit(_p(Qr), _p(probe), I32(npr), I32(npr), _p(off), _p(words), I32(words.shape[1]), _p(scale1), _p(tab),
-                     I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), _p(t0), I64(B), I32(M), _p(cnt), _p(bval),
-                     _p(bpos))
+                     I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), _p(qa) if qa is not None else None, _p(t0),
+                     I64(B), I32(M), _p(cnt), _p(bval), _p(bpos))
     return cnt, bval, bpos
 
 
@@ -460,37 +467,43 @@ def tr_params(K, nprobe, N, NC, M=None, rho_override=None, M_override=None, BN=3
     return M, n1, int(np.ceil(rho * K))
 
 
-def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=None):
+def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=None, qadd=None):
     N = idx["words"].shape[0]
     NC = len(idx["off"]) - 1
     M, n1, r = tr_params(K, probe.shape[1], N, NC, M, rho_override, M_override)
     MB = static_blocks(idx["off"])[4]
-    bm = tr_first_pass(Qr, probe[:, :n1], n1, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, MB)
+    bm = tr_first_pass(Qr, probe[:, :n1], n1, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, MB,
+                       qadd)
     t0 = threshold(bm, probe, idx["off"], n1, MB, r)
-    cnt, bval, bpos = tr_emit(Qr, probe, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, t0, M)
+    cnt, bval, bpos = tr_emit(Qr, probe, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, t0, M,
+                              qadd)
     pos, est1, ok, ncnt = select(bval, bpos, cnt, K, 0, None)
     return dict(n1=n1, r=r, M=M, MB=MB, bm=bm, t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos, est1=est1, ok=ok)
 
 
-def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True):
+def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, proj=False, order=True):
     """The default engine's batch (EngineS._gpu + the fallback): Qr = Q @ W1 (f32), QM16 = fp16(Q) @ means16.T
-    (fp16), Zq = Q @ VP (f32) are the shared dense products."""
+    (fp16), Zq = Q @ VP (f32) are the shared dense products. proj: QM16 = fp16(Qr) @ meansR.T and the pair term
+    and routing key add <q, c> (host_resident/space_x.py:33-39). order=False: ids are sorted positions."""
     Q = _c(Q, np.float32)
     _, _, qc, _ = query_prep(Q, None, idx["c"], Qr)
-    probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe)
-    s1 = tr_stage1(idx, Qr, QM16, probe, K, M)
+    qadd = qc if proj else None
+    probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe, qadd)
+    s1 = tr_stage1(idx, Qr, QM16, probe, K, M, qadd=qadd)
     est, sd = tiered_score(s1["pos"], qc, Zq, idx["rec"], idx["soff"], idx["TS"], idx["toff"], idx["cb"])
-    ids, I, scores, reads = refine(est, sd, s1["pos"], idx["order"], idx["H"], Q, z, k)
+    ordr = idx["order"] if order else np.arange(len(idx["order"]), dtype=np.int32)
+    H = idx["H"] if order else idx["Hs"]
+    ids, I, scores, reads = refine(est, sd, s1["pos"], ordr, H, Q, z, k)
     out = dict(qc=qc, probe=probe, est=est, sd=sd, ids=ids, I=I.copy(), scores=scores.copy(), reads=reads.copy(),
                cand=ids.copy(), **s1)
     bad = np.nonzero(s1["ok"] == 0)[0]
     out["bad"] = bad
     if fallback and len(bad):
         f1 = tr_stage1(idx, np.asarray(Qr)[bad], np.asarray(QM16)[bad], probe[bad], K, M, rho_override=1.0,
-                       M_override=65536)
+                       M_override=65536, qadd=None if qadd is None else qadd[bad])
         estf, sdf = tiered_score(f1["pos"], qc[bad], np.asarray(Zq)[bad], idx["rec"], idx["soff"], idx["TS"],
                                  idx["toff"], idx["cb"])
-        idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], idx["order"], idx["H"], Q[bad], z, k)
+        idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], ordr, H, Q[bad], z, k)
         out["I"][bad], out["scores"][bad], out["reads"][bad], out["cand"][bad] = If, scf, rf_, idsf
         out["fallback_ok"] = f1["ok"]
     return out
