@@ -49,9 +49,10 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("throughput", "latency"), default="throughput",
+    ap.add_argument("--mode", choices=("throughput", "latency", "host", "largek"), default="throughput",
                     help="throughput: the headline config (EngineI8, batch 2000); latency: the trellis default "
-                         "engine at batches 1/16/64 (BASELINE.json configs[2])")
+                         "engine at batches 1/16/64 (BASELINE.json configs[2]); host: the host-resident engine "
+                         "(configs[4]); largek: k=100 with the z sweep (configs[3])")
     ap.add_argument("--lat-points", default="256:200,384:400", help="n_p:K points of the latency mode")
     ap.add_argument("--lat-batches", default="1,16,64")
     ap.add_argument("--lat-z", default="1.5,2,3")
@@ -77,6 +78,10 @@ def main():
     dev = "cuda"
     if args.mode == "latency":
         return latency_mode(args)
+    if args.mode == "host":
+        return host_mode(args)
+    if args.mode == "largek":
+        return largek_mode(args)
     _lib.lib()
     t = time.time()
     X = datagen.gen(args.n, args.d, args.clusters, 0.7, seed=0, device=dev)
@@ -343,6 +348,116 @@ def latency_mode(args):
                                   f"k={args.k}", "nlist": args.nlist, "build_s": round(build_s, 1),
                       "gpu_bytes_per_vector": round(E.gpu_bytes(), 1)},
            "rows": rows}
+    print(json.dumps(out), flush=True)
+
+
+PCIE_PEAK_GBS = 63.0  # PCIe Gen5 x16, one direction
+
+
+def host_mode(args):
+    """1.28M x 768, every per-vector array in pinned host memory, batch 2000, k=10.
+    Reports queries/s, bytes per vector on the GPU and the PCIe rate of the streamed stage-1 chunks."""
+    import numpy as np
+    import torch
+
+    from fanarvse_paper_amd import datagen, metrics, trellis
+    from fanarvse_paper_amd.engine_host import SpaceX
+
+    n, d, B = 1_280_000, 768, 2000
+    dev = "cuda"
+    t = time.time()
+    X = datagen.gen(n, d, args.clusters, 0.7, seed=0, device=dev)
+    Q = datagen.gen(B, d, args.clusters, 0.7, seed=1, device=dev, dtype=torch.float32)
+    GT = datagen.ground_truth(X, Q, args.k).cpu().numpy()
+    s1, code = trellis.build_index(X, nlist=args.nlist)
+    E = SpaceX(s1, code, X)
+    del s1, code
+    X = None
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    log(f"host-resident index ready in {time.time() - t:.1f}s; GPU bytes/vector {E.gpu_bytes():.2f}; "
+        f"{len(E.chunks)} chunks of <= {E.chunk_rows} rows")
+    rows = []
+    for p in args.lat_points.split(","):
+        nprobe, K = (int(v) for v in p.split(":"))
+        z = 2.0
+        I, reads, _ = E.search(Q, K, z, nprobe, args.k)
+        rec = metrics.recall(I.numpy(), GT, args.k)
+        E.nbad = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            E.search(Q, K, z, nprobe, args.k)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / args.steps
+        E.timing, E.copy_events, E.copied_bytes = True, [], 0
+        E.search(Q, K, z, nprobe, args.k)
+        torch.cuda.synchronize()
+        ct = sum(a.elapsed_time(b) for a, b, _ in E.copy_events) * 1e-3
+        cb = sum(x for _, _, x in E.copy_events)
+        E.timing = False
+        row = dict(nprobe=nprobe, K=K, z=z, recall=rec, qps=round(B / dt, 1), ms_per_batch=round(dt * 1e3, 3),
+                   reads=round(float(reads.float().mean()), 2), fallback=E.nbad,
+                   stage1_streamed_MB=round(cb / 1e6, 1), pcie_GBps=round(cb / ct / 1e9, 2),
+                   pcie_frac=round(cb / ct / 1e9 / PCIE_PEAK_GBS, 3),
+                   stream_share_of_batch=round(ct / dt, 3))
+        rows.append(row)
+        log(f"host {row}")
+    out = {"metric": "QPS of the host-resident engine (< 8 B/vector on the GPU), PCIe GB/s of the streamed stage 1",
+           "unit": "queries/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"host-resident mode, {n}x{d} fp16 synthetic, batch {B}, k={args.k}",
+                      "gpu_bytes_per_vector": round(E.gpu_bytes(), 2), "pcie_peak_GBps": PCIE_PEAK_GBS},
+           "rows": rows}
+    print(json.dumps(out), flush=True)
+
+
+def largek_mode(args):
+    """2.25M x 768 (4,096 clusters, spectrum 0.5), batch 2000, k=100, z in {1,2,3,4}:
+    recall@100, exact reads, the fraction of candidates read, and the refine gather rate (HIP events)."""
+    import numpy as np
+    import torch
+
+    from fanarvse_paper_amd import _lib, datagen, index, metrics
+    from fanarvse_paper_amd.enginei8 import EngineI8
+
+    n, d, B, k = 2_250_000, 768, 2000, 100
+    dev = "cuda"
+    t = time.time()
+    X = datagen.gen(n, d, 4096, 0.5, seed=0, device=dev)
+    Q = datagen.gen(B, d, 4096, 0.5, seed=1, device=dev, dtype=torch.float32)
+    GT = datagen.ground_truth(X, Q, k).cpu().numpy()
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=8192)
+    E = EngineI8(s1, code, Z, zs, Vr, H=X)
+    E.MSZ = None  # M = max(4096, 16 K) (throughput/enginei8.py:39)
+    torch.cuda.synchronize()
+    log(f"2.25M index built in {time.time() - t:.1f}s")
+    rows = []
+    for p in args.points.split(","):
+        nprobe, K = (int(v) for v in p.split(":")[:2])
+        for z in (1.0, 2.0, 3.0, 4.0):
+            E.nbad = 0
+            I, reads, ids = E.search(Q, K, z, nprobe, k)
+            rec = metrics.recall(I.cpu().numpy(), GT, k)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                E.search(Q, K, z, nprobe, k)
+            torch.cuda.synchronize()
+            dt = (time.perf_counter() - t0) / args.steps
+            tr = E.trace(Q, K, z, nprobe, k)
+            est, sd, pos = tr["est"], tr["sd"], tr["pos"]
+            ms = _time_launch(lambda: _lib.refine(est, sd, pos, s1["order"], E.H, Q, z, k), 5, torch)
+            nr = float(tr["reads"].float().sum())
+            row = dict(nprobe=nprobe, K=K, z=z, recall_at_100=rec, qps=round(B / dt, 1),
+                       reads_per_query=round(nr / B, 1), fraction_read=round(nr / (B * K), 4),
+                       refine_ms=round(ms, 4), refine_GBps=round(nr * d * 2 / (ms * 1e-3) / 1e9, 1),
+                       refine_hbm_frac=round(nr * d * 2 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), fallback=E.nbad)
+            rows.append(row)
+            log(f"largek {row}")
+    out = {"metric": "k=100 error-bar sweep: recall@100, fraction of candidates read, refine gather GB/s",
+           "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "int8", "data": "synthetic",
+           "config": {"workload": f"large-N high-k, {n}x{d} fp16 synthetic (4096 clusters, alpha 0.5), batch {B}, "
+                                  f"k={k}", "nlist": 8192}, "rows": rows}
     print(json.dumps(out), flush=True)
 
 

@@ -108,7 +108,7 @@ def query_prep(Q, Vr, c, z=None):
     z = Q @ Vr is an fp32 BLAS product, as in the reference (pass it to reuse rows of an earlier product);
     the rest runs in one kernel."""
     B, d = Q.shape
-    R = Vr.shape[1]
+    R = z.shape[1] if z is not None else Vr.shape[1]
     dev = Q.device
     z = (Q @ Vr).contiguous() if z is None else z.contiguous()
     q8 = _empty((B, R), torch.int8, dev)

@@ -3,9 +3,15 @@
 Every per-vector array lives in pinned host memory: the trellis words and scales, the packed stage-2
 records, and the fp16 rows (kept in sorted order, so no id table is needed on the GPU; ids are mapped
 on the host, as the reference's ids_host variant does). The GPU keeps only shared tables: the cell
-means projected on the stage-1 basis (meansR, fp16 [NC, R]; proj variant, space_x.py:26-27,33-36),
-W1, the stage-2 rotation VP, the trellis table, the cell offsets and the static work list, plus two
-staging slots for stage-1 chunks.
+means for routing and the pair constants, W1, the stage-2 rotation VP, the trellis table, the cell
+offsets and the static work list, plus two staging slots for stage-1 chunks. The reference's two
+switches are kept (space_x.py:19-36):
+  proj: the means projected on the stage-1 basis, meansR = fp16((m_c - c) @ W1) [NC, R], with
+        QM = fp16(Qr) @ meansR.T and the pair term and routing key adding <q, c>. It is exact only when
+        the cell means lie in the span of W1 (true of the reference's embeddings, not of isotropic
+        cluster centres), so it is off by default;
+  vp16: W1 and VP in fp16, with Qr = f32(fp16(Qb) @ W1h) and Zq = f32(fp16(Qb) @ VP16).
+The default (proj off, vp16 on, 16,384-row chunks) stays under 8 B per vector at 1.28M vectors.
 
 Stage 1 streams: the index is cut into cell-aligned chunks of about CHUNK rows; a side stream copies
 chunk i+1's words and scales into the free staging slot (hipMemcpyAsync) while the main stream scans
@@ -26,11 +32,9 @@ def _pin(t):
 
 
 class SpaceX(EngineS):
-    CHUNK = 32768  # rows per staged stage-1 chunk
+    CHUNK = 16384  # rows per staged stage-1 chunk
 
-    def __init__(self, s1, code, H16, proj=True):
-        if not proj:
-            raise NotImplementedError("only the projected-means variant keeps the GPU under 8 B per vector")
+    def __init__(self, s1, code, H16, proj=False, vp16=True):
         s2lut.prepare_u(code)
         if "VP" not in code:
             raise ValueError("SpaceX needs a Lloyd-Max tiered code (s2lut.encode_lloyd)")
@@ -40,14 +44,16 @@ class SpaceX(EngineS):
         self.Hs = _pin(H16[order.to(H16.device)])
         self.words_h = _pin(s1["words"])
         self.scale1_h = _pin(s1["scale1"])
+        self.proj, self.vp16 = proj, vp16
+        VP = code["VP"].to(dev)
         self.code = dict(TS=code["TS"], rec=_pin(code["rec"]), RB=code["RB"], soff=code["soff"], toff=code["toff"],
-                         cb=code["cb"].to(dev), VP=code["VP"].to(dev), kind=code.get("kind"))
+                         cb=code["cb"].to(dev), VP=VP.half().contiguous() if vp16 else VP, kind=code.get("kind"))
         W1 = s1["W1"].to(dev)
-        meansR = ((s1["means16"].float() - s1["c"]) @ W1).half().contiguous()
-        self.s1 = dict(off=np.asarray(s1["off"]), off_t=s1["off_t"].to(dev), c=s1["c"].to(dev), W1=W1,
-                       tab=s1["tab"].to(dev), L=int(s1["L"]), inv_mnorm=s1["inv_mnorm"].float().to(dev),
-                       meansR=meansR)
-        self.W1, self.inv_mnorm, self.meansR = W1, self.s1["inv_mnorm"], meansR
+        means = (((s1["means16"].float() - s1["c"]) @ W1).half() if proj else s1["means16"]).contiguous()
+        self.s1 = dict(off=np.asarray(s1["off"]), off_t=s1["off_t"].to(dev), c=s1["c"].to(dev),
+                       W1=W1.half().contiguous() if vp16 else W1, tab=s1["tab"].to(dev), L=int(s1["L"]),
+                       inv_mnorm=s1["inv_mnorm"].float().to(dev), means=means)
+        self.W1, self.inv_mnorm, self.means = self.s1["W1"], self.s1["inv_mnorm"], means
         self.N = int(self.words_h.shape[0])
         self.Wd = int(self.words_h.shape[1])
         self.blocks, self.MB = index.static_blocks(self.s1["off_t"], self.BN)
@@ -59,6 +65,7 @@ class SpaceX(EngineS):
         self.slots = [(torch.empty((self.chunk_rows, self.Wd), dtype=torch.int32, device=dev),
                        torch.empty((self.chunk_rows,), dtype=torch.float16, device=dev)) for _ in range(2)]
         self.copied_bytes = 0
+        self.copy_events = []
 
     def _params(self, K, nprobe, rho_override=None, M_override=None):
         NC = len(self.s1["off"]) - 1
@@ -87,6 +94,8 @@ class SpaceX(EngineS):
             c0 = c1
         self.chunks = [c for c in chunks if c[3] > c[2]]
 
+    timing = False  # when set, every chunk copy is bracketed by events (copy_events) for the PCIe rate
+
     def _scan_streamed(self, mode, Qr, pr, **kw):
         """One stage-1 pass over every chunk, copies on the side stream overlapped with the scans."""
         main = torch.cuda.current_stream()
@@ -97,10 +106,15 @@ class SpaceX(EngineS):
             with torch.cuda.stream(self.side):
                 if done[slot] is not None:
                     self.side.wait_event(done[slot])
+                if self.timing:
+                    a = torch.cuda.Event(enable_timing=True)
+                    a.record(self.side)
                 w[:r1 - r0].copy_(self.words_h[r0:r1], non_blocking=True)
                 s[:r1 - r0].copy_(self.scale1_h[r0:r1], non_blocking=True)
-                ready = torch.cuda.Event()
+                ready = torch.cuda.Event(enable_timing=self.timing)
                 ready.record(self.side)
+                if self.timing:
+                    self.copy_events.append((a, ready, (r1 - r0) * (4 * self.Wd + 2)))
             self.copied_bytes += (r1 - r0) * (4 * self.Wd + 2)
             main.wait_event(ready)
             blocks = tuple(b[i0:i1] for b in self.blocks)
@@ -130,12 +144,18 @@ class SpaceX(EngineS):
         return pos, ok.bool()
 
     def _dense(self, Qb):
-        """Qr = Qb @ W1 (f32), QC = <Qb, c>, QM = fp16(Qr) @ meansR.T (fp16; the pair term and routing key add
-        QC), Zq = Qb @ VP (f32)."""
-        Qr = (Qb @ self.W1).contiguous()
-        _, _, QC, _, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
-        QM = (Qr.half() @ self.meansR.T).contiguous()
-        Zq = (Qb @ self.code["VP"]).contiguous()
+        """The dense products (space_x.py:33-38): Qr = Qb @ W1 and Zq = Qb @ VP (f32, or f32 of the fp16
+        products with vp16), QC = <Qb, c>, QM = fp16(Qb) @ means16.T (fp16), or fp16(Qr) @ meansR.T with proj
+        (the pair term and routing key then add QC)."""
+        Qh = Qb.half()
+        if self.vp16:
+            Qr = (Qh @ self.W1).float().contiguous()
+            Zq = (Qh @ self.code["VP"]).float().contiguous()
+        else:
+            Qr = (Qb @ self.W1).contiguous()
+            Zq = (Qb @ self.code["VP"]).contiguous()
+        _, _, QC, _, _ = _lib.query_prep(Qb, None, self.s1["c"], Qr)
+        QM = ((Qr.half() if self.proj else Qh) @ self.means.T).contiguous()
         return Qr, QC, QM, Zq
 
     def _finish(self, Qb, QC, Zq, pos, z, k):
@@ -145,8 +165,9 @@ class SpaceX(EngineS):
 
     def _run(self, Qb, K, z, nprobe, k, rho_override=None, M_override=None, dense=None):
         Qr, QC, QM, Zq = dense if dense is not None else self._dense(Qb)
-        probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe, qadd=QC)
-        pos, ok = self.stage1(Qr, QM, probe, K, rho_override, M_override, QC=QC)
+        qadd = QC if self.proj else None
+        probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe, qadd=qadd)
+        pos, ok = self.stage1(Qr, QM, probe, K, rho_override, M_override, QC=qadd)
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq)
 

@@ -24,20 +24,22 @@ def env(oracle_mod):
     s1, code = trellis.build_index(X, nlist=64)
     SpaceX.CHUNK = 2048  # several chunks, so the streaming path is exercised
     E = SpaceX(s1, code, X)
+    Ep = SpaceX(s1, code, X, proj=True, vp16=False)
     idx = oracle_mod.trellis_index_from_tables(s1, code, X)
     idx["Hs"] = npy(X[s1["order"].long()]).view(np.uint16)
-    return dict(X=X, Q=Q, s1=s1, E=E, idx=idx)
+    return dict(X=X, Q=Q, s1=s1, E=E, Ep=Ep, idx=idx)
 
 
-def test_streamed_engine_matches_oracle(env, oracle_mod):
-    E, Q = env["E"], env["Q"]
+@pytest.mark.parametrize("variant", ["E", "Ep"])
+def test_streamed_engine_matches_oracle(env, oracle_mod, variant):
+    E, Q = env[variant], env["Q"]
     assert len(E.chunks) > 4
     K, z, nprobe, k = 100, 2.0, 12, 10
     I, reads, ids = E.search(Q, K, z, nprobe, k, sorted_ids=True)
     torch.cuda.synchronize()
     Qr, QC, QM, Zq = E._dense(Q)
     out = oracle_mod.tr_pipeline(env["idx"], npy(Q), K, z, nprobe, k, Qr=npy(Qr), QM16=npy(QM).view(np.uint16),
-                                 Zq=npy(Zq), proj=True, order=False)
+                                 Zq=npy(Zq), proj=E.proj, order=False)
     assert np.array_equal(npy(I), out["I"])
     assert np.array_equal(npy(reads), out["reads"])
     assert np.array_equal(npy(ids), out["cand"])
@@ -51,7 +53,7 @@ def test_gpu_bytes_per_vector(env):
     shared tables of fixed size, so at the host-resident config's 1.28M vectors the total stays under 8 B."""
     E = env["E"]
     N = E.N
-    fixed = sum(t.numel() * t.element_size() for t in (E.meansR, E.W1, E.code["VP"], E.code["cb"], E.s1["tab"],
+    fixed = sum(t.numel() * t.element_size() for t in (E.means, E.W1, E.code["VP"], E.code["cb"], E.s1["tab"],
                                                        E.s1["off_t"], E.s1["inv_mnorm"], E.s1["c"]))
     fixed += sum(w.numel() * w.element_size() + s.numel() * s.element_size() for w, s in E.slots)
     per_vector = E.gpu_bytes() - fixed / N
