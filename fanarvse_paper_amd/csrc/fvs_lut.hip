@@ -1,12 +1,14 @@
 // Uniform tiered refinement code: nibble lookup tables and the LUT stage-2 scorer with error bars.
 //
-// Scorer mapping: one block (2 waves) per query. The query's LUT is converted once into 32-bit
+// Scorer mapping: one block (4 waves) per query. The query's LUT is converted once into 32-bit
 // fixed point in LDS, so every plane sum is an exact integer and the result does not depend on the
 // summation order (any lane/tile mapping gives the same bits). Each lane scores one candidate:
-// it streams the candidate's packed record (128 B in flight per iteration), looks up two LUT
-// entries per code byte, and folds the per-tier integer sums into the f32 estimate in tier order.
-// A per-dword descriptor table in LDS (LUT base, plane weight, end-of-tier flag) is shared by all
-// lanes, so control flow is uniform across the wave.
+// it streams the candidate's packed record in 128-byte units (the next unit in flight while one is
+// summed), looks up two LUT entries per code byte, and folds the per-tier integer sums into the f32
+// estimate in tier order. All lanes of a wave process the same record dword at the same time, so the
+// per-dword descriptor (LUT base, plane weight, end-of-tier flag) is wave-uniform: it is read from a
+// lane register into a scalar register, the lookups of one dword hit one 64-byte table (no LDS bank
+// conflicts), and the only branch, at a tier's end, is uniform.
 #include "fvs_common.h"
 
 namespace {
@@ -82,23 +84,44 @@ __global__ __launch_bounds__(256) void k_lut_build(const uint16_t *__restrict__ 
   }
 }
 
-constexpr int kScoreThreads = 128;
-constexpr int kUnit = 16;  // 16-byte chunks per pipeline unit (256 bytes of a record)
+constexpr int kScoreThreads = 256;
+constexpr int kUnit = 8;             // 16-byte chunks per pipeline unit (128 bytes of a record)
+constexpr int kUD = kUnit * 4;       // dwords per unit; lane l of a wave holds the descriptor of dword l % kUD
+constexpr int kZeroBytes = 512;      // zero table after the LUT: dwords past the planes look up zeros
 
-// Per-dword descriptors (LDS): planes carry the LUT byte offset, the plane weight, an end-of-tier flag
-// and the tier; the dwords after the planes carry the (scale, sigma) pair of tier t.
+// Per-dword descriptors (LDS, one per dword of every unit): the LUT byte offset of the dword's first table,
+// the plane weight (shift), the tier, and an end-of-tier flag.
 constexpr uint32_t kMetaLast = 1u << 24;
-constexpr uint32_t kMetaScale = 1u << 25;
 
 struct RecUnit {
   uint4 c[kUnit];
 };
 
-__device__ __forceinline__ void load_unit(RecUnit &b, const uint8_t *__restrict__ rec, int64_t row, int RB, int u,
-                                          int nchunk, bool live) {
-  const uint4 *rp = reinterpret_cast<const uint4 *>(rec + row * RB) + u * kUnit;
+// Unit u of record `row`. Every lane loads (dead lanes read row 0) and chunks past the record are clamped
+// to its last chunk, so the loads are unconditional and the pipeline's wait counts stay exact.
+__device__ __forceinline__ void load_unit(RecUnit &b, const uint8_t *__restrict__ rec, int64_t row, int RB16, int u) {
+  const uint4 *rp = reinterpret_cast<const uint4 *>(rec) + row * RB16;
 #pragma unroll
-  for (int c = 0; c < kUnit; c++) b.c[c] = (live && u * kUnit + c < nchunk) ? rp[c] : make_uint4(0, 0, 0, 0);
+  for (int c = 0; c < kUnit; c++) b.c[c] = rp[min(u * kUnit + c, RB16 - 1)];
+}
+
+__device__ __forceinline__ uint32_t unit_word(const RecUnit &b, int k) {
+  const uint4 &c = b.c[k >> 2];
+  return (k & 3) == 0 ? c.x : (k & 3) == 1 ? c.y : (k & 3) == 2 ? c.z : c.w;
+}
+
+// The 8 LUT entries of one record dword: byte j's high nibble indexes the table at lb + 128 j, its low
+// nibble the table at lb + 128 j + 64 (tables of 16 int32 = 64 bytes, nibble * 4 = byte offset).
+__device__ __forceinline__ void lookup8(const char *lutb, uint32_t x, uint32_t lb, int32_t (&v)[8]) {
+  uint32_t xh = (x >> 2) & 0x3c3c3c3cu, xl = (x << 2) & 0x3c3c3c3cu;
+  // opaque to the optimiser, so each byte stays a byte-select operand of the address add (SDWA) instead
+  // of being refolded into a shift and a mask per lookup
+  asm("" : "+v"(xh), "+v"(xl));
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    v[2 * j] = *reinterpret_cast<const int32_t *>(lutb + (lb + __builtin_amdgcn_ubfe(xh, 8 * j, 8)) + 128 * j);
+    v[2 * j + 1] = *reinterpret_cast<const int32_t *>(lutb + (lb + __builtin_amdgcn_ubfe(xl, 8 * j, 8)) + 128 * j + 64);
+  }
 }
 
 template <bool HALF>
@@ -108,14 +131,14 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     TierArgs ta, const int32_t *__restrict__ ncnt, int64_t N, int64_t B, int K, float *__restrict__ est,
     float *__restrict__ sdo) {
   extern __shared__ int32_t smem[];
-  int32_t *lut = smem;                                                 // [LW] fixed-point table
-  const int nw = soff / 4;
-  uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW);            // [nw + T], padded to even
-  float *tf = reinterpret_cast<float *>(meta + ((nw + FVS_MAX_TIERS + 1) & ~1));  // [T][4]: delta, mid, qsum, qn2
-  uint32_t *ssw = reinterpret_cast<uint32_t *>(tf + 4 * FVS_MAX_TIERS);  // [threads][T] (scale, sigma)
-  int64_t *acct = reinterpret_cast<int64_t *>(ssw + kScoreThreads * FVS_MAX_TIERS);  // [threads][T]
-  int32_t *rows = reinterpret_cast<int32_t *>(acct + kScoreThreads * FVS_MAX_TIERS);  // [K]
-  __shared__ float red[2];
+  int32_t *lut = smem;                                                  // [LW] fixed-point table + zero table
+  const int nw = soff / 4;                                              // plane dwords
+  const int U = (nw + kUD - 1) / kUD;                                   // units per record
+  uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW + kZeroBytes / 4);  // [U * kUD]
+  float *tf = reinterpret_cast<float *>(meta + U * kUD);                // [T][4]: delta, mid, qsum, qn2
+  int64_t *acct = reinterpret_cast<int64_t *>(tf + 4 * FVS_MAX_TIERS);  // [T][threads] tier sums
+  int32_t *rows = reinterpret_cast<int32_t *>(acct + ta.T * kScoreThreads);  // [K]
+  __shared__ float red[kScoreThreads / FVS_WAVE];
   __shared__ int sexp;
 
   const int64_t q = blockIdx.x;
@@ -126,7 +149,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   float m = 0.f;
   if (HALF) {
     const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
-#pragma unroll 8
+#pragma unroll 4
     for (int i = tid; i < LW / 8; i += kScoreThreads) {
       const uint4 v = L4[i];
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
@@ -136,7 +159,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     }
   } else {
     const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
-#pragma unroll 8
+#pragma unroll 4
     for (int i = tid; i < LW / 4; i += kScoreThreads) {
       const float4 v = L4[i];
       m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -149,17 +172,20 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   for (int i = tid; i < K; i += kScoreThreads) rows[i] = (int32_t)min(max((int64_t)pos[q * (int64_t)K + i], (int64_t)0), N - 1);
   __syncthreads();
   if (tid == 0) {
+    float mm = red[0];
+#pragma unroll
+    for (int w = 1; w < kScoreThreads / FVS_WAVE; w++) mm = fmaxf(mm, red[w]);
     int E = 0;
-    (void)frexpf(fmaxf(red[0], red[1]), &E);
+    (void)frexpf(mm, &E);
     sexp = max(0, E - 3);
   }
   __syncthreads();
   const int s = sexp;
 
-  // 2. integer LUT, per-dword descriptors, per-tier constants
+  // 2. integer LUT, zero table, per-dword descriptors, per-tier constants
   if (HALF) {
     const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
-#pragma unroll 8
+#pragma unroll 4
     for (int i = tid; i < LW / 8; i += kScoreThreads) {
       const uint4 v = L4[i];
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
@@ -171,7 +197,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     }
   } else {
     const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
-#pragma unroll 8
+#pragma unroll 4
     for (int i = tid; i < LW / 4; i += kScoreThreads) {
       const float4 v = L4[i];
       lut[4 * i + 0] = (int32_t)rintf(ldexpf(v.x, 24 - s));
@@ -180,11 +206,10 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
       lut[4 * i + 3] = (int32_t)rintf(ldexpf(v.w, 24 - s));
     }
   }
-  for (int w = tid; w < nw + T; w += kScoreThreads) {
-    uint32_t d = 0;
-    if (w >= nw) {
-      d = kMetaScale | (uint32_t)(w - nw);
-    } else {
+  for (int i = tid; i < kZeroBytes / 4; i += kScoreThreads) lut[LW + i] = 0;
+  for (int w = tid; w < U * kUD; w += kScoreThreads) {
+    uint32_t d = (uint32_t)LW * 4u;  // past the planes: the zero table, weight 1, never the end of a tier
+    if (w < nw) {
       const int byte = 4 * w;
       for (int t = 0; t < T; t++) {
         const int len = ta.bits[t] * ta.kb[t];
@@ -212,76 +237,75 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   }
   __syncthreads();
 
-  // 3. candidates: lane `tid` scores slots tid, tid + 128, ...; the record stream is cut into units of
-  //    256 bytes and double-buffered in registers, so the next unit is in flight while one is summed
-  const int nchunk = (soff + 4 * T + 15) / 16;  // chunks holding planes and (scale, sigma) pairs
-  const int U = (nchunk + kUnit - 1) / kUnit;
+  // 3. candidates: lane `tid` scores slots tid, tid + threads, ...; each record is streamed in units of
+  //    kUnit 16-byte chunks, double-buffered in registers, and the lookups of dword k + 1 are issued
+  //    before the entries of dword k are summed
+  const int RB16 = RB / 16;
   const int nround = (K + kScoreThreads - 1) / kScoreThreads;
   const int S = nround * U;
   const char *lutb = reinterpret_cast<const char *>(lut);
   const float qcq = qc[q];
+  const int lane = tid & (FVS_WAVE - 1);
   RecUnit ub0, ub1;
+  uint32_t ssv[FVS_MAX_TIERS];
   int64_t acc = 0;
-  // one pipeline step: `cur` holds unit sq, `nxt` receives unit sq + 1
+  auto load_pairs = [&](int64_t row) {
+    const uint32_t *rp = reinterpret_cast<const uint32_t *>(rec + row * (int64_t)RB);
+#pragma unroll
+    for (int t = 0; t < FVS_MAX_TIERS; t++) ssv[t] = rp[min(nw + t, RB / 4 - 1)];
+  };
   auto step = [&](int sq, const RecUnit &cur, RecUnit &nxt) {
     const int i = sq / U, u = sq - i * U;
     const int mm = tid + kScoreThreads * i;
-    const bool live = mm < lim;
+    const uint32_t mv = meta[u * kUD + (lane & (kUD - 1))];
     if (sq + 1 < S) {
       const int i1 = (sq + 1) / U, u1 = (sq + 1) - i1 * U;
       const int m1 = tid + kScoreThreads * i1;
-      load_unit(nxt, rec, m1 < lim ? rows[m1] : 0, RB, u1, nchunk, m1 < lim);
+      load_unit(nxt, rec, m1 < lim ? rows[m1] : 0, RB16, u1);
     }
-    if (live) {
+    if (u == 0) load_pairs(mm < lim ? rows[mm] : 0);
+    // wave-uniform: skip waves whose lanes are all past the candidate list
+    if (kScoreThreads * i + (tid & ~(FVS_WAVE - 1)) < lim) {
+      int32_t va[8], vb[8];
+      lookup8(lutb, unit_word(cur, 0), __builtin_amdgcn_readlane(mv, 0) & 0x1ffffu, va);
 #pragma unroll
-      for (int c = 0; c < kUnit; c++) {
-        const uint32_t xs[4] = {cur.c[c].x, cur.c[c].y, cur.c[c].z, cur.c[c].w};
-#pragma unroll
-        for (int ee = 0; ee < 4; ee++) {
-          const int w = (u * kUnit + c) * 4 + ee;
-          if (w < nw) {
-            const uint32_t mt = meta[w];
-            const char *lb = lutb + (mt & 0x1ffffu);
-            const uint32_t x = xs[ee];
-            const uint32_t xh = (x >> 2) & 0x3c3c3c3cu, xl = (x << 2) & 0x3c3c3c3cu;  // nibble * 4 per byte
-            int part = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              part += *reinterpret_cast<const int32_t *>(lb + 128 * j + ((xh >> (8 * j)) & 0xffu));
-              part += *reinterpret_cast<const int32_t *>(lb + 128 * j + 64 + ((xl >> (8 * j)) & 0xffu));
-            }
-            acc += (int64_t)part << ((mt >> 17) & 7u);
-            if (mt & kMetaLast) {
-              acct[tid * FVS_MAX_TIERS + ((mt >> 20) & 7u)] = acc;
-              acc = 0;
-            }
-          } else if (w < nw + T) {
-            ssw[tid * FVS_MAX_TIERS + (w - nw)] = xs[ee];
-          }
+      for (int k = 0; k < kUD; k++) {
+        int32_t(&vc)[8] = (k & 1) ? vb : va;
+        int32_t(&vn)[8] = (k & 1) ? va : vb;
+        if (k + 1 < kUD) lookup8(lutb, unit_word(cur, k + 1), __builtin_amdgcn_readlane(mv, k + 1) & 0x1ffffu, vn);
+        const uint32_t mt = __builtin_amdgcn_readlane(mv, k);
+        const int32_t part = vc[0] + vc[1] + vc[2] + vc[3] + vc[4] + vc[5] + vc[6] + vc[7];
+        acc += (int64_t)part << ((mt >> 17) & 7u);
+        if (mt & kMetaLast) {
+          acct[((mt >> 20) & 7u) * kScoreThreads + tid] = acc;
+          acc = 0;
         }
       }
     }
     if (u == U - 1 && mm < K) {
       const int64_t o = q * (int64_t)K + mm;
-      if (!live) {
+      if (mm >= lim) {
         est[o] = -1e30f;
         sdo[o] = 0.f;
       } else {
         float e = qcq, var = 0.f;
-        for (int t = 0; t < T; t++) {
-          float a = ldexpf((float)acct[tid * FVS_MAX_TIERS + t], s - 24);
-          a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
-          const uint32_t sw = ssw[tid * FVS_MAX_TIERS + t];
-          const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
-          e = __builtin_fmaf(a, sc, e);
-          var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
+#pragma unroll
+        for (int t = 0; t < FVS_MAX_TIERS; t++) {
+          if (t < T) {
+            float a = ldexpf((float)acct[t * kScoreThreads + tid], s - 24);
+            a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
+            const uint32_t sw = ssv[t];
+            const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
+            e = __builtin_fmaf(a, sc, e);
+            var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
+          }
         }
         est[o] = e;
         sdo[o] = sqrtf(var);
       }
     }
   };
-  load_unit(ub0, rec, tid < lim ? rows[tid] : 0, RB, 0, nchunk, tid < lim);
+  load_unit(ub0, rec, tid < lim ? rows[tid] : 0, RB16, 0);
   for (int sq = 0; sq < S; sq += 2) {
     step(sq, ub0, ub1);
     if (sq + 1 < S) step(sq + 1, ub1, ub0);
@@ -345,8 +369,9 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (B == 0) return FVS_OK;
   if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
   if (K > 4096) return FVS_E_CAPACITY;
-  const size_t shm = (size_t)LW * 4 + (size_t)((soff / 4 + FVS_MAX_TIERS + 1) & ~1) * 4 + 4 * FVS_MAX_TIERS * 4 +
-                     (size_t)kScoreThreads * FVS_MAX_TIERS * (4 + 8) + (size_t)K * 4;
+  const int units = (soff / 4 + kUD - 1) / kUD;
+  const size_t shm = (size_t)LW * 4 + kZeroBytes + (size_t)units * kUD * 4 + 4 * FVS_MAX_TIERS * 4 +
+                     (size_t)kScoreThreads * T * 8 + (size_t)K * 4;
   if (shm > 160 * 1024 - 64) return FVS_E_CAPACITY;
   hipStream_t st = (hipStream_t)stream;
   if (half)
