@@ -90,8 +90,9 @@ constexpr int kUD = kUnit * 4;       // dwords per unit; lane l of a wave holds 
 constexpr int kZeroBytes = 512;      // zero table after the LUT: dwords past the planes look up zeros
 
 // Per-dword descriptors (LDS, one per dword of every unit): the LUT byte offset of the dword's first table,
-// the plane weight (shift), the tier, and an end-of-tier flag.
+// the plane weight (shift), the tier, an end-of-tier flag, and a flag for the (scale, sigma) dword of tier t.
 constexpr uint32_t kMetaLast = 1u << 24;
+constexpr uint32_t kMetaPair = 1u << 25;
 
 struct RecUnit {
   uint4 c[kUnit];
@@ -133,11 +134,12 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   extern __shared__ int32_t smem[];
   int32_t *lut = smem;                                                  // [LW] fixed-point table + zero table
   const int nw = soff / 4;                                              // plane dwords
-  const int U = (nw + kUD - 1) / kUD;                                   // units per record
+  const int U = (nw + ta.T + kUD - 1) / kUD;                            // units per record (planes + pairs)
   uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW + kZeroBytes / 4);  // [U * kUD]
   float *tf = reinterpret_cast<float *>(meta + U * kUD);                // [T][4]: delta, mid, qsum, qn2
   int64_t *acct = reinterpret_cast<int64_t *>(tf + 4 * FVS_MAX_TIERS);  // [T][threads] tier sums
-  int32_t *rows = reinterpret_cast<int32_t *>(acct + ta.T * kScoreThreads);  // [K]
+  uint32_t *ssw = reinterpret_cast<uint32_t *>(acct + ta.T * kScoreThreads);  // [T][threads] (scale, sigma)
+  int32_t *rows = reinterpret_cast<int32_t *>(ssw + ta.T * kScoreThreads);  // [K]
   __shared__ float red[kScoreThreads / FVS_WAVE];
   __shared__ int sexp;
 
@@ -209,6 +211,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   for (int i = tid; i < kZeroBytes / 4; i += kScoreThreads) lut[LW + i] = 0;
   for (int w = tid; w < U * kUD; w += kScoreThreads) {
     uint32_t d = (uint32_t)LW * 4u;  // past the planes: the zero table, weight 1, never the end of a tier
+    if (w >= nw && w < nw + T) d |= kMetaPair | ((uint32_t)(w - nw) << 20);
     if (w < nw) {
       const int byte = 4 * w;
       for (int t = 0; t < T; t++) {
@@ -247,23 +250,22 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   const float qcq = qc[q];
   const int lane = tid & (FVS_WAVE - 1);
   RecUnit ub0, ub1;
-  uint32_t ssv[FVS_MAX_TIERS];
   int64_t acc = 0;
-  auto load_pairs = [&](int64_t row) {
-    const uint32_t *rp = reinterpret_cast<const uint32_t *>(rec + row * (int64_t)RB);
-#pragma unroll
-    for (int t = 0; t < FVS_MAX_TIERS; t++) ssv[t] = rp[min(nw + t, RB / 4 - 1)];
+  // every step issues the same unconditional loads (the last one reloads its own unit), so the wait
+  // before a unit is summed never has to drain the prefetch of the next one
+  auto row_of = [&](int m) {
+    const int r = rows[min(m, K - 1)];
+    return m < lim ? r : 0;
   };
   auto step = [&](int sq, const RecUnit &cur, RecUnit &nxt) {
     const int i = sq / U, u = sq - i * U;
     const int mm = tid + kScoreThreads * i;
     const uint32_t mv = meta[u * kUD + (lane & (kUD - 1))];
-    if (sq + 1 < S) {
-      const int i1 = (sq + 1) / U, u1 = (sq + 1) - i1 * U;
-      const int m1 = tid + kScoreThreads * i1;
-      load_unit(nxt, rec, m1 < lim ? rows[m1] : 0, RB16, u1);
+    {
+      const int sq1 = min(sq + 1, S - 1);
+      const int i1 = sq1 / U, u1 = sq1 - i1 * U;
+      load_unit(nxt, rec, row_of(tid + kScoreThreads * i1), RB16, u1);
     }
-    if (u == 0) load_pairs(mm < lim ? rows[mm] : 0);
     // wave-uniform: skip waves whose lanes are all past the candidate list
     if (kScoreThreads * i + (tid & ~(FVS_WAVE - 1)) < lim) {
       int32_t va[8], vb[8];
@@ -280,6 +282,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
           acct[((mt >> 20) & 7u) * kScoreThreads + tid] = acc;
           acc = 0;
         }
+        if (mt & kMetaPair) ssw[((mt >> 20) & 7u) * kScoreThreads + tid] = unit_word(cur, k);
       }
     }
     if (u == U - 1 && mm < K) {
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
           if (t < T) {
             float a = ldexpf((float)acct[t * kScoreThreads + tid], s - 24);
             a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
-            const uint32_t sw = ssv[t];
+            const uint32_t sw = ssw[t * kScoreThreads + tid];
             const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
             e = __builtin_fmaf(a, sc, e);
             var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
       }
     }
   };
-  load_unit(ub0, rec, tid < lim ? rows[tid] : 0, RB16, 0);
+  load_unit(ub0, rec, row_of(tid), RB16, 0);
   for (int sq = 0; sq < S; sq += 2) {
     step(sq, ub0, ub1);
     if (sq + 1 < S) step(sq + 1, ub1, ub0);
@@ -369,9 +372,9 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (B == 0) return FVS_OK;
   if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
   if (K > 4096) return FVS_E_CAPACITY;
-  const int units = (soff / 4 + kUD - 1) / kUD;
+  const int units = (soff / 4 + T + kUD - 1) / kUD;
   const size_t shm = (size_t)LW * 4 + kZeroBytes + (size_t)units * kUD * 4 + 4 * FVS_MAX_TIERS * 4 +
-                     (size_t)kScoreThreads * T * 8 + (size_t)K * 4;
+                     (size_t)kScoreThreads * T * (8 + 4) + (size_t)K * 4;
   if (shm > 160 * 1024 - 64) return FVS_E_CAPACITY;
   hipStream_t st = (hipStream_t)stream;
   if (half)
