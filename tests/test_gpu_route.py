@@ -1,0 +1,42 @@
+"""GPU routing (top-n_p cells per query) against the CPU oracle on adversarial fp16 score rows: heavy
+ties at the n_p-th value (taken lowest cells first), +-0 (equal), +-inf, and every shape class of the
+launcher: the wave-per-query kernel for each (cells per lane, sorted keys per lane) instantiation and
+the block-per-query kernel for rows it does not take (NC not a multiple of 8, NC > 8192, n_p > 2048).
+Results are bit-exact: the probe lists are sorted by (score desc, cell asc)."""
+import numpy as np
+import pytest
+import torch
+
+from fanarvse_paper_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(64, 1), (64, 12), (64, 64), (520, 65), (1024, 128), (4096, 256), (4096, 300), (4096, 512),
+          (4096, 768), (4096, 1024), (4096, 1025), (4096, 2048), (8192, 1), (8192, 768), (8192, 1536),
+          (8192, 2048), (100, 37), (16384, 768), (4096, 4096)]
+
+
+def rows(B, NC, seed):
+    rng = np.random.default_rng(seed)
+    levels = np.array([-np.inf, -2.0, -0.0, 0.0, 0.5, 1.0, 1.5, 3.0, np.inf], np.float16)
+    few = levels[rng.integers(0, len(levels), (B // 2, NC))]              # ties everywhere
+    many = rng.standard_normal((B - B // 2, NC)).astype(np.float16)      # fp16 rounding ties only
+    return np.concatenate([few, many]).view(np.uint16)
+
+
+@pytest.mark.parametrize("NC,npr", SHAPES)
+def test_route_topk_matches_oracle(oracle_mod, NC, npr):
+    print(f"\n[gpu route] NC={NC} nprobe={npr}", flush=True)
+    QM = rows(8, NC, NC * 7 + npr)
+    got = _lib.route_topk(torch.from_numpy(QM.view(np.float16)).cuda(), npr)
+    torch.cuda.synchronize()
+    want = oracle_mod.route_topk(QM, npr)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_route_topk_many_queries(oracle_mod):
+    """A batch that is not a multiple of the 4 queries per block, at the headline shape."""
+    QM = rows(1001, 4096, 5)
+    got = _lib.route_topk(torch.from_numpy(QM.view(np.float16)).cuda(), 768)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle_mod.route_topk(QM, 768))
