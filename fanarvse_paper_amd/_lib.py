@@ -28,6 +28,7 @@ SIGNATURES = {
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
     "fvs_pairs_scratch_bytes": [I64, I32],
+    "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P],
@@ -176,6 +177,31 @@ def pairs(probe, n, NC, QM, mnorm, scratch=None, qadd=None):
                            _dev(qid, torch.int32, "qid"), _dev(qrank, torch.int32, "qrank"),
                            _dev(qcp, torch.float32, "qcp"), _stream()), "fvs_pairs")
     return qid, qrank, coff, ccnt, qcp
+
+
+def pairs2(probe, n1, NC, QM, mnorm, scratch=None, qadd=None):
+    """The first-pass pairs (first n1 probe columns) and the emit pairs (all columns) of one batch, each as
+    pairs() returns them, from one pass (throughput/enginei8.py:48,55)."""
+    B, npr = probe.shape
+    dev = probe.device
+    if QM.shape != (B, NC):
+        raise ValueError("pairs2: QM shape")
+    if scratch is None:
+        scratch = pairs_scratch(B, NC, dev)
+    out = []
+    for n in (n1, npr):
+        out.append(dict(ccnt=_empty((NC,), torch.int32, dev), coff=_empty((NC,), torch.int32, dev),
+                        qid=_empty((B * n,), torch.int32, dev), qrank=_empty((B * n,), torch.int32, dev),
+                        qcp=_empty((B * n,), torch.float32, dev)))
+    args = []
+    for o in out:
+        args += [_dev(o["ccnt"], torch.int32, "ccnt"), _dev(o["coff"], torch.int32, "coff"),
+                 _dev(o["qid"], torch.int32, "qid"), _dev(o["qrank"], torch.int32, "qrank"),
+                 _dev(o["qcp"], torch.float32, "qcp")]
+    _check(lib().fvs_pairs2(_dev(probe, torch.int32, "probe"), B, npr, n1, NC, _dev(QM, torch.float16, "QM"),
+                            _opt(mnorm, torch.float32, "mnorm", (NC,)), _opt(qadd, torch.float32, "qadd", (B,)),
+                            _dev(scratch, torch.uint8, "scratch"), scratch.numel(), *args, _stream()), "fvs_pairs2")
+    return tuple((o["qid"], o["qrank"], o["coff"], o["ccnt"], o["qcp"]) for o in out)
 
 
 def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1, MB=1, n1=1):

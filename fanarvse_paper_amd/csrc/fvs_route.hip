@@ -12,8 +12,11 @@
 //
 // Pairs: instead of a global counting sort (atomics on popular cells serialise), the probe lists are
 // transposed into a cell-major rank matrix rank[c][q] (int16, -1 = not probed) in caller scratch.
-// Each cell's block then reads its row once to count and once to compact its queries in ascending
-// order -- the order of the reference's stable sort -- with no atomics and no per-cell sort.
+// The same pass copies each query's routing scores into a cell-major score matrix, so that the pair
+// constants are read row-wise. One wave per cell then reads its rank row once to count and its rank
+// and score rows once to compact its queries in ascending order -- the order of the reference's
+// stable sort -- with no atomics, no per-cell sort and no column gathers. The first-pass list (the
+// first n1 probe columns) and the full list come out of one matrix (fvs_pairs2).
 #include "fvs_common.h"
 
 namespace {
@@ -241,70 +244,256 @@ __global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__
 }
 
 // rank[c][q] = r for the first n probe columns (the matrix is pre-filled with 0xffff).
-__global__ void k_rank_scatter(const int32_t *__restrict__ probe, int64_t B, int npr, int n, uint16_t *__restrict__ rank) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= B * n) return;
-  const int64_t q = t / n;
-  const int r = (int)(t % n);
-  rank[(int64_t)probe[q * npr + r] * B + q] = (uint16_t)r;
-}
+// Rank and score matrices, row pitch Bp = B rounded up to 64 (one 128-byte line per 64 queries):
+// rank[c * Bp + q] = rank of cell c in query q's probe row (first n columns), 0xffff when q does not probe
+// c; score[c * Bp + q] = QM[q][c] (fp16 bits). One block per (64 queries, kTileC cells): the block's
+// probe entries inside its cell range are scattered into an LDS rank tile and its scores are read
+// row-wise into an LDS score tile (rows padded to 33 dwords, so neither the transposed writes nor the
+// row reads conflict on banks); both tiles are then written out as whole 128-byte rows. Probe entries
+// outside [0, NC) are ignored.
+constexpr int kTileQ = 64;
+constexpr int kTileC = 256;
+constexpr int kTileRow = kTileQ / 2 + 1;  // dwords per padded tile row
 
-// ccnt[c] = number of queries probing cell c.
-__global__ __launch_bounds__(256) void k_cell_count(const uint16_t *__restrict__ rank, int64_t B,
-                                                    int32_t *__restrict__ ccnt) {
-  __shared__ int sh[8];
-  const int c = blockIdx.x;
-  const uint16_t *rr = rank + (int64_t)c * B;
-  int m = 0;
-  for (int64_t q = threadIdx.x; q < B; q += 256) m += rr[q] != 0xffffu;
-  const int tot = fvs_block_scan256(m, sh);
-  if (threadIdx.x == 255) ccnt[c] = tot;
-}
-
-// Exclusive prefix sum of ccnt into coff. One block of 256 threads.
-__global__ __launch_bounds__(256) void k_cell_scan(const int32_t *__restrict__ ccnt, int NC, int32_t *__restrict__ coff) {
-  __shared__ int tmp[8];
-  int run = 0;
-  for (int base = 0; base < NC; base += 256) {
-    const int c = base + (int)threadIdx.x;
-    const int v = c < NC ? ccnt[c] : 0;
-    const int inc = fvs_block_scan256(v, tmp);
-    if (c < NC) coff[c] = run + inc - v;
-    if (threadIdx.x == 255) tmp[4] = inc;
-    __syncthreads();
-    run += tmp[4];
-    __syncthreads();
-  }
-}
-
-// One block per cell: its queries in ascending order, their probe ranks and pair constants.
-__global__ __launch_bounds__(256) void k_cell_emit(const uint16_t *__restrict__ rank, int64_t B,
-                                                   const int32_t *__restrict__ coff, const uint16_t *__restrict__ QM,
-                                                   const float *__restrict__ mnorm, const float *__restrict__ qadd,
-                                                   int NC, int32_t *__restrict__ qid,
-                                                   int32_t *__restrict__ qrank, float *__restrict__ qcp) {
-  __shared__ int sh[8];
-  const int c = blockIdx.x;
-  const uint16_t *rr = rank + (int64_t)c * B;
-  const float sc = mnorm ? mnorm[c] : 1.0f;
-  int run = coff[c];
-  for (int64_t base = 0; base < B; base += 256) {
-    const int64_t q = base + threadIdx.x;
-    const uint16_t r = q < B ? rr[q] : (uint16_t)0xffffu;
-    const bool f = r != 0xffffu;
-    const int inc = fvs_block_scan256(f ? 1 : 0, sh);
-    if (f) {
-      const int o = run + inc - 1;
-      qid[o] = (int32_t)q;
-      qrank[o] = (int32_t)r;
-      const float v = fvs_h2f(QM[q * NC + c]) * sc;
-      qcp[o] = qadd ? v + qadd[q] : v;
+__global__ __launch_bounds__(512) void k_rank_build(const int32_t *__restrict__ probe, const uint16_t *__restrict__ QM,
+                                                    int64_t B, int npr, int n, int NC, int64_t Bp,
+                                                    uint16_t *__restrict__ rank, uint16_t *__restrict__ score) {
+  __shared__ uint32_t rt[kTileC * kTileRow];
+  __shared__ uint32_t st[kTileC * kTileRow];
+  const int64_t q0 = (int64_t)blockIdx.y * kTileQ;
+  const int c0 = blockIdx.x * kTileC;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kTileC * kTileRow; i += 512) rt[i] = 0xffffffffu;
+  // scores: thread reads QM[q0 + qq][c0 + cc] along cc (coalesced), 16 loads in flight, and writes the
+  // transposed tile
+  constexpr int kSU = 16;
+  for (int i0 = 0; i0 < kTileQ * kTileC; i0 += 512 * kSU) {
+    uint16_t h[kSU];
+#pragma unroll
+    for (int u = 0; u < kSU; u++) {
+      const int i = i0 + u * 512 + tid;
+      const int qq = i / kTileC, cc = i - qq * kTileC;
+      const int64_t q = q0 + qq;
+      h[u] = (i < kTileQ * kTileC && q < B && c0 + cc < NC) ? QM[q * NC + c0 + cc] : (uint16_t)0;
     }
-    if (threadIdx.x == 255) sh[6] = inc;
-    __syncthreads();
-    run += sh[6];
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kSU; u++) {
+      const int i = i0 + u * 512 + tid;
+      const int qq = i / kTileC, cc = i - qq * kTileC;
+      if (i < kTileQ * kTileC) reinterpret_cast<uint16_t *>(st)[2 * (cc * kTileRow) + qq] = h[u];
+    }
   }
+  __syncthreads();
+  // ranks: one wave per query (8 at a time), its probe row read 64 entries per load with up to 16 loads in
+  // flight; entries that fall in [c0, c0 + kTileC) are scattered into the tile
+  constexpr int kPU = 16;
+  const int lane = tid & (FVS_WAVE - 1), wv = tid >> 6;
+  for (int qq = wv; qq < kTileQ; qq += 512 / FVS_WAVE) {
+    if (q0 + qq >= B) break;
+    const int32_t *pr = probe + (q0 + qq) * npr;
+    for (int r0 = 0; r0 < n; r0 += kPU * FVS_WAVE) {
+      int c[kPU];
+#pragma unroll
+      for (int u = 0; u < kPU; u++) {
+        const int r = r0 + u * FVS_WAVE + lane;
+        c[u] = r < n ? pr[r] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kPU; u++) {
+        const unsigned cc = (unsigned)(c[u] - c0);
+        if (cc < (unsigned)kTileC && c[u] < NC)
+          reinterpret_cast<uint16_t *>(rt)[2 * (cc * kTileRow) + qq] = (uint16_t)(r0 + u * FVS_WAVE + lane);
+      }
+    }
+  }
+  __syncthreads();
+  // out: 32 dwords per cell row, one row per 32 threads
+  for (int i = tid; i < kTileC * 32; i += 512) {
+    const int cc = i >> 5, j = i & 31;
+    if (c0 + cc < NC) {
+      const int64_t at = ((int64_t)(c0 + cc) * Bp + q0) / 2 + j;  // in dwords
+      reinterpret_cast<uint32_t *>(rank)[at] = rt[cc * kTileRow + j];
+      reinterpret_cast<uint32_t *>(score)[at] = st[cc * kTileRow + j];
+    }
+  }
+}
+
+// Entries of one 16-byte row piece (8 ranks) with rank < n.
+__device__ __forceinline__ int below8(const uint4 v, uint32_t n) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  int m = 0;
+#pragma unroll
+  for (int u = 0; u < 4; u++) m += ((w[u] & 0xffffu) < n) + ((w[u] >> 16) < n);
+  return m;
+}
+
+constexpr int kCellWaves = 4;  // cells per block in the count and emit kernels (one wave per cell)
+
+// ccnt_a[c] = number of queries probing cell c within their first na columns (and ccnt_b for nb).
+template <bool TWO>
+__global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_count(const uint16_t *__restrict__ rank, int NC,
+                                                                      int64_t Bp, uint32_t na, uint32_t nb,
+                                                                      int32_t *__restrict__ ccnt_a,
+                                                                      int32_t *__restrict__ ccnt_b) {
+  const int lane = threadIdx.x & (FVS_WAVE - 1);
+  const int c = blockIdx.x * kCellWaves + (threadIdx.x >> 6);
+  if (c >= NC) return;
+  const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
+  int ma = 0, mb = 0;
+  for (int64_t i = lane; i < Bp / 8; i += FVS_WAVE) {
+    const uint4 v = rr[i];
+    ma += below8(v, na);
+    if (TWO) mb += below8(v, nb);
+  }
+  ma = wave_sum_i32(ma);
+  if (TWO) mb = wave_sum_i32(mb);
+  if (lane == 0) {
+    ccnt_a[c] = ma;
+    if (TWO) ccnt_b[c] = mb;
+  }
+}
+
+// Exclusive prefix sum of ccnt into coff (block y = list). Thread t scans a run of consecutive cells,
+// then the run totals are scanned across the 1024 threads.
+__global__ __launch_bounds__(1024) void k_cell_scan(const int32_t *__restrict__ ccnt_a, int32_t *__restrict__ coff_a,
+                                                    const int32_t *__restrict__ ccnt_b, int32_t *__restrict__ coff_b,
+                                                    int NC) {
+  __shared__ int wsum[1024 / FVS_WAVE];
+  const int32_t *ccnt = blockIdx.x ? ccnt_b : ccnt_a;
+  int32_t *coff = blockIdx.x ? coff_b : coff_a;
+  const int t = threadIdx.x, lane = t & (FVS_WAVE - 1), w = t >> 6;
+  const int per = (NC + 1023) / 1024;
+  const int c0 = t * per, c1 = min(c0 + per, NC);
+  int run = 0;
+  for (int c = c0; c < c1; c++) run += ccnt[c];
+  const int inc = wave_incl_scan_i32(run, lane);
+  if (lane == FVS_WAVE - 1) wsum[w] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int i = 0; i < w; i++) base += wsum[i];
+  int o = base + inc - run;
+  for (int c = c0; c < c1; c++) {
+    coff[c] = o;
+    o += ccnt[c];
+  }
+}
+
+struct PairList {
+  int32_t *qid, *qrank;
+  float *qcp;
+  const int32_t *coff;
+  uint32_t n;  // columns of the probe rows in this list
+};
+
+// One wave per cell: its queries in ascending order, their probe ranks and pair constants, for one or
+// two lists. The rank and score rows are read kEmitU 16-byte pieces per lane at a time (2048 queries),
+// then wave prefix sums place each lane's pairs.
+constexpr int kEmitU = 4;
+
+template <bool TWO>
+__global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_emit(
+    const uint16_t *__restrict__ rank, const uint16_t *__restrict__ score, int64_t Bp, const float *__restrict__ mnorm,
+    const float *__restrict__ qadd, int NC, PairList la, PairList lb) {
+  const int lane = threadIdx.x & (FVS_WAVE - 1);
+  const int c = blockIdx.x * kCellWaves + (threadIdx.x >> 6);
+  if (c >= NC) return;
+  const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
+  const uint4 *ss = reinterpret_cast<const uint4 *>(score + (int64_t)c * Bp);
+  const float sc = mnorm ? mnorm[c] : 1.0f;
+  const int64_t nv = Bp / 8;
+  int runa = la.coff[c], runb = TWO ? lb.coff[c] : 0;
+  for (int64_t base = 0; base < nv; base += kEmitU * FVS_WAVE) {
+    uint4 v[kEmitU], sv[kEmitU];
+#pragma unroll
+    for (int u = 0; u < kEmitU; u++) {
+      const int64_t i = base + u * FVS_WAVE + lane;
+      v[u] = i < nv ? rr[i] : make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
+      sv[u] = i < nv ? ss[i] : make_uint4(0, 0, 0, 0);
+    }
+    int oa[kEmitU], ob[kEmitU];
+#pragma unroll
+    for (int u = 0; u < kEmitU; u++) {
+      const int ma = below8(v[u], la.n);
+      const int ia = wave_incl_scan_i32(ma, lane);
+      oa[u] = runa + ia - ma;
+      runa += __builtin_amdgcn_readlane(ia, FVS_WAVE - 1);
+      if (TWO) {
+        const int mb = below8(v[u], lb.n);
+        const int ib = wave_incl_scan_i32(mb, lane);
+        ob[u] = runb + ib - mb;
+        runb += __builtin_amdgcn_readlane(ib, FVS_WAVE - 1);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kEmitU; u++) {
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      const uint32_t hw[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const uint32_t r = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
+        const bool ina = r < la.n, inb = TWO && r < lb.n;
+        if (ina || inb) {
+          const int64_t q = (base + u * FVS_WAVE + lane) * 8 + e;
+          const uint32_t h = (e & 1) ? (hw[e >> 1] >> 16) : (hw[e >> 1] & 0xffffu);
+          float x = fvs_h2f((uint16_t)h) * sc;
+          if (qadd) x = x + qadd[q];
+          if (ina) {
+            la.qid[oa[u]] = (int32_t)q;
+            la.qrank[oa[u]] = (int32_t)r;
+            la.qcp[oa[u]] = x;
+            oa[u]++;
+          }
+          if (inb) {
+            lb.qid[ob[u]] = (int32_t)q;
+            lb.qrank[ob[u]] = (int32_t)r;
+            lb.qcp[ob[u]] = x;
+            ob[u]++;
+          }
+        }
+      }
+    }
+  }
+}
+
+int64_t pairs_pitch(int64_t B) { return (B + kTileQ - 1) / kTileQ * kTileQ; }
+
+int64_t matrix_bytes(int64_t B, int NC) { return ((int64_t)NC * pairs_pitch(B) * 2 + 255) / 256 * 256; }
+
+// One or two pair lists (first na columns, and first nb columns when lb is given) from one rank matrix.
+int pairs_impl(const int32_t *probe, int64_t B, int npr, int NC, const uint16_t *QM, const float *mnorm,
+               const float *qadd, void *scratch, int64_t scratch_bytes, int32_t *ccnt_a, PairList la,
+               int32_t *ccnt_b, const PairList *lb, hipStream_t st) {
+  if (scratch_bytes < 2 * matrix_bytes(B, NC)) return FVS_E_CAPACITY;
+  if (NC > kMaxNC) return FVS_E_CAPACITY;
+  if ((reinterpret_cast<uintptr_t>(scratch) & 15) != 0) return FVS_E_ARG;
+  const int64_t Bp = pairs_pitch(B);
+  uint16_t *rank = reinterpret_cast<uint16_t *>(scratch);
+  uint16_t *score = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(scratch) + matrix_bytes(B, NC));
+  const int n = (int)max(la.n, lb ? lb->n : 0u);
+  int e;
+  if (B > 0) {
+    const dim3 grid((unsigned)((NC + kTileC - 1) / kTileC), (unsigned)(Bp / kTileQ));
+    hipLaunchKernelGGL(k_rank_build, grid, dim3(512), 0, st, probe, QM, B, npr, n, NC, Bp, rank, score);
+    if ((e = fvs_launch_status())) return e;
+  }
+  const unsigned cg = (unsigned)((NC + kCellWaves - 1) / kCellWaves);
+  const dim3 cb(kCellWaves * FVS_WAVE);
+  if (lb) {
+    hipLaunchKernelGGL(k_cell_count<true>, dim3(cg), cb, 0, st, rank, NC, Bp, la.n, lb->n, ccnt_a, ccnt_b);
+    if ((e = fvs_launch_status())) return e;
+    hipLaunchKernelGGL(k_cell_scan, dim3(2), dim3(1024), 0, st, ccnt_a, const_cast<int32_t *>(la.coff), ccnt_b,
+                       const_cast<int32_t *>(lb->coff), NC);
+    if ((e = fvs_launch_status())) return e;
+    hipLaunchKernelGGL(k_cell_emit<true>, dim3(cg), cb, 0, st, rank, score, Bp, mnorm, qadd, NC, la, *lb);
+  } else {
+    hipLaunchKernelGGL(k_cell_count<false>, dim3(cg), cb, 0, st, rank, NC, Bp, la.n, 0u, ccnt_a, ccnt_a);
+    if ((e = fvs_launch_status())) return e;
+    hipLaunchKernelGGL(k_cell_scan, dim3(1), dim3(1024), 0, st, ccnt_a, const_cast<int32_t *>(la.coff), ccnt_a,
+                       const_cast<int32_t *>(la.coff), NC);
+    if ((e = fvs_launch_status())) return e;
+    hipLaunchKernelGGL(k_cell_emit<false>, dim3(cg), cb, 0, st, rank, score, Bp, mnorm, qadd, NC, la, la);
+  }
+  return fvs_launch_status();
 }
 
 }  // namespace
@@ -325,7 +514,7 @@ extern "C" int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t
 
 extern "C" int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC) {
   if (B < 0 || NC <= 0) return -1;
-  return ((int64_t)NC * B * 2 + 255) / 256 * 256;
+  return 2 * matrix_bytes(B, NC);  // rank matrix, then score matrix
 }
 
 extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
@@ -333,21 +522,22 @@ extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n
                          int64_t scratch_bytes,
                          int32_t *qid, int32_t *qrank, float *qcp, void *stream) {
   if (B < 0 || NC <= 0 || n <= 0 || n > npr || n > 65535) return FVS_E_ARG;
-  if (scratch_bytes < fvs_pairs_scratch_bytes(B, NC)) return FVS_E_CAPACITY;
   if (!probe || !QM || !ccnt || !coff || !scratch || !qid || !qrank || !qcp) return FVS_E_ARG;
-  hipStream_t st = (hipStream_t)stream;
-  uint16_t *rank = reinterpret_cast<uint16_t *>(scratch);
-  int e;
-  if (B > 0) {
-    if ((e = fvs_fill_u32(rank, ((int64_t)NC * B * 2 + 3) / 4, 0xffffffffu, stream))) return e;
-    const int64_t tot = B * (int64_t)n;
-    hipLaunchKernelGGL(k_rank_scatter, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, probe, B, npr, n, rank);
-    if ((e = fvs_launch_status())) return e;
-  }
-  hipLaunchKernelGGL(k_cell_count, dim3((unsigned)NC), dim3(256), 0, st, rank, B, ccnt);
-  if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_cell_scan, dim3(1), dim3(256), 0, st, ccnt, NC, coff);
-  if ((e = fvs_launch_status())) return e;
-  hipLaunchKernelGGL(k_cell_emit, dim3((unsigned)NC), dim3(256), 0, st, rank, B, coff, QM, mnorm, qadd, NC, qid, qrank, qcp);
-  return fvs_launch_status();
+  const PairList la{qid, qrank, qcp, coff, (uint32_t)n};
+  return pairs_impl(probe, B, npr, NC, QM, mnorm, qadd, scratch, scratch_bytes, ccnt, la, nullptr, nullptr,
+                    (hipStream_t)stream);
+}
+
+extern "C" int fvs_pairs2(const int32_t *probe, int64_t B, int32_t npr, int32_t n1, int32_t NC, const uint16_t *QM,
+                          const float *mnorm, const float *qadd, void *scratch, int64_t scratch_bytes,
+                          int32_t *ccnt1, int32_t *coff1, int32_t *qid1, int32_t *qrank1, float *qcp1,
+                          int32_t *ccnt, int32_t *coff, int32_t *qid, int32_t *qrank, float *qcp, void *stream) {
+  if (B < 0 || NC <= 0 || n1 <= 0 || n1 > npr || npr > 65535) return FVS_E_ARG;
+  if (!probe || !QM || !scratch || !ccnt1 || !coff1 || !qid1 || !qrank1 || !qcp1 || !ccnt || !coff || !qid ||
+      !qrank || !qcp)
+    return FVS_E_ARG;
+  const PairList la{qid1, qrank1, qcp1, coff1, (uint32_t)n1};
+  const PairList lb{qid, qrank, qcp, coff, (uint32_t)npr};
+  return pairs_impl(probe, B, npr, NC, QM, mnorm, qadd, scratch, scratch_bytes, ccnt1, la, ccnt, &lb,
+                    (hipStream_t)stream);
 }

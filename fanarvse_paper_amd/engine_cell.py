@@ -60,7 +60,7 @@ class EngineS:
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
         L = int(s1["L"])
         scratch = _lib.pairs_scratch(B, NC, dev)
-        pr = _lib.pairs(probe, n1, NC, QM, None, scratch)
+        pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
         _lib.tr_scan(0, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=self.MB, n1=n1)
         t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
@@ -68,7 +68,7 @@ class EngineS:
         _lib.fill_u32(cnt, 0)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
-        pr = _lib.pairs(probe, probe.shape[1], NC, QM, None, scratch)
+        pr = prn
         _lib.tr_scan(1, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, t0=t0, cnt=cnt, bval=bval,
                      bpos=bpos, CAP=M)
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)

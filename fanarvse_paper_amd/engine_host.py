@@ -129,7 +129,7 @@ class SpaceX(EngineS):
         dev = Qr.device
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
         scratch = _lib.pairs_scratch(B, NC, dev)
-        pr = _lib.pairs(probe, n1, NC, QM, None, scratch, qadd=QC)
+        pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch, qadd=QC)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
         self._scan_streamed(0, Qr, pr, bm=bm, MB=self.MB, n1=n1)
         t0 = _lib.threshold(bm, probe, self.s1["off_t"], n1, self.MB, r)
@@ -137,7 +137,7 @@ class SpaceX(EngineS):
         _lib.fill_u32(cnt, 0)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
-        pr = _lib.pairs(probe, probe.shape[1], NC, QM, None, scratch, qadd=QC)
+        pr = prn
         self._scan_streamed(1, Qr, pr, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
         self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M

@@ -97,7 +97,7 @@ class EngineI8:
         q8, qs = (qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"]))[:2]
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
         scratch = _lib.pairs_scratch(B, NC, Qb.device)
-        pr = _lib.pairs(probe, n1, NC, QM, self.mnorm, scratch)
+        pr, prn = _lib.pairs2(probe, n1, NC, QM, self.mnorm, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=Qb.device)
         _lib.i8_scan(0, self.blocks, q8, qs, pr, self.Z, self.zs, bm=bm, MB=self.MB, n1=n1)
         t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
@@ -105,7 +105,7 @@ class EngineI8:
         _lib.fill_u32(cnt, 0)
         bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
         bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
-        pr = _lib.pairs(probe, probe.shape[1], NC, QM, self.mnorm, scratch)
+        pr = prn
         _lib.i8_scan(1, self.blocks, q8, qs, pr, self.Z, self.zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
         pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, min(kd, K - 1), delta)
         self._est1, self._ncnt, self._t0, self._cnt = est1, ncnt, t0, cnt

@@ -86,7 +86,7 @@ int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t nprobe, in
  *   probe i32 [B, npr] (only the first n columns are used; a row holds distinct cells);
  *   QM fp16 [B, NC]; mnorm f32 [NC] or NULL (scale 1)
  *   ccnt i32 [NC]  number of pairs of each cell      coff i32 [NC]  exclusive prefix of ccnt
- *   scratch        at least fvs_pairs_scratch_bytes(B, NC) bytes (a cell-major probe-rank matrix)
+ *   scratch        at least fvs_pairs_scratch_bytes(B, NC) bytes, 16-byte aligned (cell-major probe-rank and score matrices)
  *   qid i32 [B*n]  query of each pair, cell-major, queries ascending inside a cell (the stable-sort order)
  *   qrank i32 [B*n] rank of the cell in the query's probe row     qcp f32 [B*n] = (float)QM[q][c] * mnorm[c]
  *   qadd f32 [B] or NULL: when given, qcp += qadd[q] (the projected-means variant of the host-resident engine,
@@ -96,6 +96,17 @@ int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC);
 int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
               const float *mnorm, const float *qadd, int32_t *ccnt, int32_t *coff, void *scratch, int64_t scratch_bytes,
               int32_t *qid, int32_t *qrank, float *qcp, void *stream);
+
+/*
+ * Both pair lists of one search batch from one pass: the first-pass list of the first n1 probe columns
+ * (ccnt1, coff1, qid1, qrank1, qcp1 over B*n1 pairs) and the emit list of all npr columns (ccnt, coff,
+ * qid, qrank, qcp over B*npr pairs), each exactly as fvs_pairs gives it. Replaces the two pairs_fast
+ * calls of stage1_i8 (throughput/enginei8.py:48,55); scratch as for fvs_pairs. npr <= 65535.
+ */
+int fvs_pairs2(const int32_t *probe, int64_t B, int32_t npr, int32_t n1, int32_t NC, const uint16_t *QM,
+               const float *mnorm, const float *qadd, void *scratch, int64_t scratch_bytes, int32_t *ccnt1,
+               int32_t *coff1, int32_t *qid1, int32_t *qrank1, float *qcp1, int32_t *ccnt, int32_t *coff,
+               int32_t *qid, int32_t *qrank, float *qcp, void *stream);
 
 /*
  * int8 stage-1 scan on MFMA (a9, a11). Same inputs and outputs as the reference's CUDA twin

@@ -40,3 +40,47 @@ def test_route_topk_many_queries(oracle_mod):
     got = _lib.route_topk(torch.from_numpy(QM.view(np.float16)).cuda(), 768)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy(), oracle_mod.route_topk(QM, 768))
+
+
+@pytest.mark.parametrize("B,NC,npr,n", [(1, 64, 12, 12), (7, 64, 24, 5), (2000, 4096, 768, 768), (2001, 4096, 768, 90),
+                                        (333, 5000, 300, 300), (129, 9000, 1024, 1000), (64, 16384, 64, 64)])
+def test_pairs_match_oracle(oracle_mod, B, NC, npr, n):
+    """Cell-major (query, cell) pairs of the first n probe columns: counts, offsets, queries ascending
+    inside a cell (the stable-sort order), probe ranks and the pair constants, bit-exact."""
+    print(f"\n[gpu pairs] B={B} NC={NC} npr={npr} n={n}", flush=True)
+    rng = np.random.default_rng(B + NC + n)
+    probe = np.stack([rng.permutation(NC)[:npr] for _ in range(B)]).astype(np.int32)
+    QM = rng.standard_normal((B, NC)).astype(np.float16)
+    mnorm = rng.uniform(0.5, 2.0, NC).astype(np.float32)
+    qadd = rng.standard_normal(B).astype(np.float32)
+    for qa in (None, qadd):
+        qid, qrank, coff, ccnt, qcp = _lib.pairs(torch.from_numpy(probe).cuda(), n, NC, torch.from_numpy(QM).cuda(),
+                                                 torch.from_numpy(mnorm).cuda(),
+                                                 qadd=None if qa is None else torch.from_numpy(qa).cuda())
+        torch.cuda.synchronize()
+        oq, oc, on, oqcp, o = oracle_mod.pairs(np.ascontiguousarray(probe[:, :n]), NC, QM.view(np.uint16), mnorm, qa)
+        assert np.array_equal(ccnt.cpu().numpy(), on)
+        assert np.array_equal(coff.cpu().numpy(), oc)
+        assert np.array_equal(qid.cpu().numpy(), oq)
+        assert np.array_equal(qrank.cpu().numpy(), (o % n).astype(np.int32))
+        assert np.array_equal(qcp.cpu().numpy().view(np.uint32), oqcp.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,NC,npr,n1", [(1, 64, 12, 3), (2001, 4096, 768, 52), (129, 9000, 1024, 1024)])
+def test_pairs2_is_two_pairs_calls(oracle_mod, B, NC, npr, n1):
+    """The fused first-pass and emit lists equal the oracle's pairs of the first n1 and of all columns."""
+    print(f"\n[gpu pairs2] B={B} NC={NC} npr={npr} n1={n1}", flush=True)
+    rng = np.random.default_rng(3 * B + n1)
+    probe = np.stack([rng.permutation(NC)[:npr] for _ in range(B)]).astype(np.int32)
+    QM = rng.standard_normal((B, NC)).astype(np.float16)
+    mnorm = rng.uniform(0.5, 2.0, NC).astype(np.float32)
+    lists = _lib.pairs2(torch.from_numpy(probe).cuda(), n1, NC, torch.from_numpy(QM).cuda(),
+                        torch.from_numpy(mnorm).cuda())
+    torch.cuda.synchronize()
+    for n, (qid, qrank, coff, ccnt, qcp) in zip((n1, npr), lists):
+        oq, oc, on, oqcp, o = oracle_mod.pairs(np.ascontiguousarray(probe[:, :n]), NC, QM.view(np.uint16), mnorm)
+        assert np.array_equal(ccnt.cpu().numpy(), on)
+        assert np.array_equal(coff.cpu().numpy(), oc)
+        assert np.array_equal(qid.cpu().numpy(), oq)
+        assert np.array_equal(qrank.cpu().numpy(), (o % n).astype(np.int32))
+        assert np.array_equal(qcp.cpu().numpy().view(np.uint32), oqcp.view(np.uint32))
