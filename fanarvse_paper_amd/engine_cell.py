@@ -20,6 +20,7 @@ import numpy as np
 import torch
 
 from . import _lib, index, s2lut
+from .enginei8 import _fresh
 
 
 class EngineS:
@@ -118,9 +119,10 @@ class EngineS:
         g, qs, (ok, I, nr, ids, sc, dense) = self.graphs[key]
         qs.copy_(Qb)
         g.replay()
-        I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
-        if not bool(ok.all()):
-            bad = torch.nonzero(~ok).flatten()
+        I, nr, ids, sc = _fresh(I, nr, ids, sc)
+        okh = ok.cpu()
+        if not bool(okh.all()):
+            bad = torch.nonzero(~okh).flatten().to(Qb.device)
             self.nbad += len(bad)
             a, b, c, s = self._fallback(Qb[bad], K, z, k, *[t[bad].contiguous() for t in dense])
             I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s

@@ -28,6 +28,17 @@ def pairs_fast(probe, NC, QM, scale=None):
     return qid, coff, ccnt, qcp, qrank
 
 
+def _fresh(*ts):
+    """Copies of the graph's output tensors (int32 / float32) for the caller, made by one gather kernel into
+    one new buffer instead of one copy per tensor."""
+    flat = torch.cat([t.reshape(-1).view(torch.int32) for t in ts])
+    out, at = [], 0
+    for t in ts:
+        out.append(flat[at:at + t.numel()].view(t.dtype).view(t.shape))
+        at += t.numel()
+    return out
+
+
 class EngineI8:
     BQ, BN = 32, 32
     PROJ = False
@@ -46,6 +57,7 @@ class EngineI8:
     NROUTE = True
     DELTA = 0.07
     LUTH = True
+    CB = 8  # 32-row blocks per stage-1 work item (the kernel stages 4 at a time in LDS)
 
     def __init__(self, s1, code, Z, zs, Vr, H=None):
         if self.BN != 32:
@@ -54,7 +66,7 @@ class EngineI8:
         self.H = H
         s2lut.prepare_u(code)
         _, self.MB = index.static_blocks(s1["off_t"], self.BN)
-        self.blocks = index.static_chunks(s1["off_t"], self.BN)
+        self.blocks = index.static_chunks(s1["off_t"], self.BN, self.CB)
         N = Z.shape[0]
         if int(s1["off_t"][-1]) != N or int(self.blocks[3].max()) > N:
             raise ValueError("EngineI8: cell offsets do not match the code rows")
@@ -162,9 +174,10 @@ class EngineI8:
         g, qs, (ok, I, nr, ids, sc, blas) = self.graphs[key]
         qs.copy_(Qb)
         g.replay()
-        I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
-        if not bool(ok.all()):
-            bad = torch.nonzero(~ok).flatten()
+        I, nr, ids, sc = _fresh(I, nr, ids, sc)
+        okh = ok.cpu()
+        if not bool(okh.all()):
+            bad = torch.nonzero(~okh).flatten().to(Qb.device)
             self.nbad += len(bad)
             a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, *[t[bad].contiguous() for t in blas])
             I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s

@@ -303,20 +303,30 @@ void or_emit(const int8_t *q8, const float *qs, const int32_t *probe, int npr, i
   emit_gen(est_i8_cb, &ctx, probe, npr, np, off, QM, NC, mnorm, t0, B, M, cnt, bval, bpos);
 }
 
+/* Selection (a12) and the delta rule (a14), throughput/enginei8.py:60 (t = bval.topk(K); pos = bpos[t];
+ * ok = K <= cnt <= M) and :87-88 (ncnt), with ties in est broken by the smaller position. */
 void or_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64_t B, int M, int K, int kd, float delta,
                int32_t *pos, float *est1, uint8_t *ok, int32_t *ncnt) {
 #pragma omp parallel for schedule(static)
   for (int64_t q = 0; q < B; q++) {
     const int n = cnt[q] < M ? cnt[q] : M;
+    /* top-K of the first n entries in the canonical order (est descending, pos ascending) */
+    uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * (n > 0 ? n : 1));
+    for (int i = 0; i < n; i++)
+      keys[i] = ((uint64_t)ord32(bval[q * M + i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)bpos[q * M + i]);
+    qsort(keys, (size_t)n, sizeof(uint64_t), cmp_u64_desc);
     for (int i = 0; i < K; i++) {
       if (i < n) {
-        est1[q * K + i] = bval[q * M + i];
-        pos[q * K + i] = bpos[q * M + i];
+        const uint32_t k = (uint32_t)(keys[i] >> 32);
+        const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+        memcpy(&est1[q * K + i], &u, 4);
+        pos[q * K + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
       } else {
         est1[q * K + i] = -1e30f;
         pos[q * K + i] = 0;
       }
     }
+    free(keys);
     ok[q] = (uint8_t)(cnt[q] >= K && cnt[q] <= M);
     if (delta >= 0.f) {
       const float thr = est1[q * K + kd] - delta;

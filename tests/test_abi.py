@@ -83,7 +83,7 @@ def test_no_packed_fp32_in_device_code():
         os.remove(out)
         return src, text
 
-    with ThreadPoolExecutor(4) as ex:
+    with ThreadPoolExecutor(8) as ex:
         for src, text in ex.map(asm, build.sources()):
             bad = re.findall(r"v_pk_(?:add|mul|fma)_f32", text)
             assert not bad, f"{os.path.basename(src)}: {len(bad)} packed-fp32 instructions"

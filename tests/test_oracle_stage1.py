@@ -142,10 +142,7 @@ def test_emit_is_threshold_set_and_lemma2(tiny, s1run):
 def test_select_canonical_order_fillers_and_delta(oracle_mod):
     bval = np.array([[0.5, 0.9, 0.5, 0.2, -1e30, -1e30], [0.3, 0.1, 0.0, 0.0, 0.0, 0.0]], np.float32)
     bpos = np.array([[7, 3, 2, 9, 0, 0], [5, 6, 0, 0, 0, 0]], np.int32)
-    # oracle buffers are kept in canonical order; reorder row 0 into it
-    o = sorted(range(4), key=lambda i: (-bval[0, i], bpos[0, i]))
-    bval[0, :4], bpos[0, :4] = bval[0, o], bpos[0, o]
-    cnt = np.array([4, 2], np.int32)
+    cnt = np.array([4, 2], np.int32)  # row 0 is not in canonical order: select sorts
     pos, est1, ok, ncnt = oracle_mod.select(bval, bpos, cnt, 3, 1, 0.3)
     assert pos[0].tolist() == [3, 2, 7] and est1[0].tolist() == [np.float32(0.9), np.float32(0.5), np.float32(0.5)]
     assert pos[1].tolist() == [5, 6, 0] and est1[1, 2] == np.float32(-1e30)
@@ -155,6 +152,30 @@ def test_select_canonical_order_fillers_and_delta(oracle_mod):
     assert ncnt2.tolist() == [3, 3] and ok2.tolist() == [1, 0]
     _, _, ok3, _ = oracle_mod.select(bval, bpos, np.array([7, 2], np.int32), 3, 1, None)
     assert ok3[0] == 0  # cnt > M overflows
+
+
+def test_select_is_sorted_topk_bruteforce(oracle_mod):
+    """Top-K of the first min(cnt, M) entries of unsorted buffers by (est desc, pos asc), against a numpy
+    lexsort; rows with long runs of equal estimates, short rows and overfull rows (cnt > M)."""
+    rng = np.random.default_rng(4)
+    B, M, K = 40, 64, 10
+    cnt = rng.integers(0, M + 20, B).astype(np.int32)
+    bval = np.where(np.arange(B)[:, None] % 2 == 1, rng.integers(-2, 3, (B, M)) * np.float32(0.5),
+                    rng.standard_normal((B, M))).astype(np.float32)
+    bpos = np.stack([rng.permutation(1000)[:M] for _ in range(B)]).astype(np.int32)
+    pos, est1, ok, _ = oracle_mod.select(bval, bpos, cnt, K, 0, None)
+    for q in range(B):
+        n = min(int(cnt[q]), M)
+        o = np.lexsort((bpos[q, :n], -bval[q, :n].astype(np.float64)))[:K]
+        want_p = np.concatenate([bpos[q, o], np.zeros(K - len(o), np.int32)])
+        want_e = np.concatenate([bval[q, o], np.full(K - len(o), -1e30, np.float32)])
+        assert np.array_equal(pos[q], want_p) and np.array_equal(est1[q], want_e), q
+    assert np.array_equal(ok, ((cnt >= K) & (cnt <= M)).astype(np.uint8))
+    # a planted mistake (ties broken by the larger position) fails the same check
+    q = next(q for q in range(1, B, 2) if min(cnt[q], M) > K)
+    n = min(int(cnt[q]), M)
+    bad = np.lexsort((-bpos[q, :n], -bval[q, :n].astype(np.float64)))[:K]
+    assert not np.array_equal(pos[q], bpos[q, bad])
 
 
 def test_pairs_against_bruteforce(oracle_mod):
