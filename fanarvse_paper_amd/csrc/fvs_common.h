@@ -38,6 +38,19 @@ __device__ __forceinline__ uint32_t fvs_ord16(uint16_t u) {
   return (u & 0x8000u) ? (uint32_t)((~u) & 0xffffu) : (uint32_t)(u | 0x8000u);
 }
 
+// Compute units of the current device (queried once per device; up to 64 devices).
+static inline int fvs_cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 // Workgroup barrier that orders LDS only: outstanding global loads stay in flight across it (a
 // plain __syncthreads() also waits for every outstanding global access of the wave).
 __device__ __forceinline__ void fvs_lds_barrier() {

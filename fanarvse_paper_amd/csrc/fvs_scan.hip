@@ -63,211 +63,258 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
     const int32_t *__restrict__ pcell, const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
-    const int32_t *__restrict__ pe, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
+    const int32_t *__restrict__ pe, int P, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
     const float *__restrict__ qcp, const float *__restrict__ t0, int32_t *__restrict__ cnt,
     float *__restrict__ bval, int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
   __shared__ __align__(16) Meta meta[kMeta];
   __shared__ __align__(16) float zsl[32 * kCB];
-  const int p = blockIdx.x;
-  const int c = pcell[p];
-  const int qn = ccnt[c];
-  if (qn == 0) return;
   EmitLds *E = nullptr;
   if constexpr (MODE == 1) {
     __shared__ EmitLds Es;
     E = &Es;
   }
-  const bool staged = MODE == 1 && qn <= kMaxQ;
-  const int qoff = coff[c];
-  const int blk0 = pblk[p];
-  const int cs = ps[p], ce = pe[p];
-  const int lastblk = (ce - 1) / 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int h = lane >> 5, li = lane & 31;
-  const int row0 = blk0 * 32;  // first row of the item
 
-  // the first chunk's pair ids are requested before the code block, so both latencies overlap
-  int pq[kMeta / 256];
+  // Items p = blockIdx.x, blockIdx.x + gridDim.x, ...: right after an item's tile loop the next item's
+  // pair ids, row scales and code blocks are requested, so their latency runs under the flush.
+  struct Item {
+    int p, c, qn, qoff, blk0, cs, ce;
+  };
+  auto item_at = [&](int p) {
+    Item it{p, 0, 0, 0, 0, 0, 0};
+    if (p < P) {
+      it.c = pcell[p];
+      it.blk0 = pblk[p];
+      it.cs = ps[p];
+      it.ce = pe[p];
+      it.qn = ccnt[it.c];
+      it.qoff = coff[it.c];
+    }
+    return it;
+  };
+  int pq[kMeta / 256];  // pair ids of the item's first chunk
+  float zr = 0.f;       // this thread's row scale of the item (thread < 32 * kCB)
+  v4i a[kNB][8];        // this wave's blocks: the A operands
+  auto prefetch = [&](const Item &it) {
+    if (it.qn == 0) return;
 #pragma unroll
-  for (int i = 0; i < kMeta / 256; i++) {
-    const int j = tid + 256 * i;
-    pq[i] = j < min(kMeta, qn) ? qid[qoff + j] : 0;
-  }
-  if (tid < 32 * kCB) {
-    const int r = row0 + tid;
-    zsl[tid] = (r >= cs && r < ce) ? zs[r] : __builtin_nanf("");
-  }
-  // this wave's blocks: the A operands
-  int bk[kNB];
-  bool act[kNB];
-  v4i a[kNB][8];
+    for (int i = 0; i < kMeta / 256; i++) {
+      const int j = tid + 256 * i;
+      pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
+    }
+    if (tid < 32 * kCB) {
+      const int r = it.blk0 * 32 + tid;
+      zr = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
+    }
+    const int lastblk = (it.ce - 1) / 32;
 #pragma unroll
-  for (int u = 0; u < kNB; u++) {
-    bk[u] = blk0 + kNB * w + u;
-    act[u] = bk[u] <= lastblk;
-    int64_t zr = (int64_t)bk[u] * 32 + li;
-    if (!act[u] || zr > N - 1) zr = N - 1;
-    const v4i *zp = reinterpret_cast<const v4i *>(Z + zr * kR + h * 16);
+    for (int u = 0; u < kNB; u++) {
+      const int bk = it.blk0 + kNB * w + u;
+      int64_t zr_ = (int64_t)bk * 32 + li;
+      if (bk > lastblk || zr_ > N - 1) zr_ = N - 1;
+      const v4i *zp = reinterpret_cast<const v4i *>(Z + zr_ * kR + h * 16);
 #pragma unroll
-    for (int s = 0; s < 8; s++) a[u][s] = zp[2 * s];
-  }
-  const bool any = act[0];
-  int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
+      for (int s = 0; s < 8; s++) a[u][s] = zp[2 * s];
+    }
+  };
 
-  auto scan = [&](const bool direct, bool first) {
-    for (int c0 = 0; c0 < qn; c0 += kMeta) {
-      const int nq = min(kMeta, qn - c0);
-      if (c0 > 0 || !first) {
+  // the emit pass takes one item per workgroup (stride = P): there the next item's state would only
+  // add register pressure to the flush
+  const int stride = MODE == 0 ? (int)gridDim.x : P;
+  int p = blockIdx.x;
+  Item cur = item_at(p);
+  if constexpr (MODE == 1) {
+    if (cur.qn == 0) return;
+  }
+  prefetch(cur);
+  while (p < P) {
+    const Item nxt = MODE == 0 ? item_at(p + stride) : Item{P, 0, 0, 0, 0, 0, 0};
+    if (cur.qn == 0) {
+      if constexpr (MODE == 0) prefetch(nxt);
+      cur = nxt;
+      p += stride;
+      continue;
+    }
+    const int qn = cur.qn, qoff = cur.qoff, blk0 = cur.blk0, cs = cur.cs;
+    const bool staged = MODE == 1 && qn <= kMaxQ;
+    const int row0 = blk0 * 32;  // first row of the item
+    const int lastblk = (cur.ce - 1) / 32;
+    if (tid < 32 * kCB) zsl[tid] = zr;
+    int bk[kNB];
+    bool act[kNB];
+#pragma unroll
+    for (int u = 0; u < kNB; u++) {
+      bk[u] = blk0 + kNB * w + u;
+      act[u] = bk[u] <= lastblk;
+    }
+    const bool any = act[0];
+    int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
+
+    auto scan = [&](const bool direct, bool first) {
+      for (int c0 = 0; c0 < qn; c0 += kMeta) {
+        const int nq = min(kMeta, qn - c0);
+        if (c0 > 0 || !first) {
+#pragma unroll
+          for (int i = 0; i < kMeta / 256; i++) {
+            const int j = tid + 256 * i;
+            pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
+          }
+        }
 #pragma unroll
         for (int i = 0; i < kMeta / 256; i++) {
           const int j = tid + 256 * i;
-          pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kMeta / 256; i++) {
-        const int j = tid + 256 * i;
-        if (j < nq) {
-          const int pidx = qoff + c0 + j;
-          const int q = pq[i];
-          Meta m;
-          m.qid = q;
-          m.qs = qs[q];
-          m.qcp = qcp[pidx];
-          m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
-          meta[j] = m;
-        }
-      }
-      __syncthreads();
-
-      if (any) {
-        const int ntiles = (nq + 31) / 32;
-        // B fragments of a tile: lane (li, h) reads bytes 32*s + 16*h of the code of the tile's query li
-        auto load = [&](v4i (&b)[8], int tile) {
-          const int jr = min(tile * 32 + li, nq - 1);
-          const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)meta[jr].qid * kR + h * 16);
-#pragma unroll
-          for (int s = 0; s < 8; s++) b[s] = src[2 * s];
-        };
-        auto compute = [&](const v4i (&b)[8], int t) {
-          v16i acc[kNB];
-#pragma unroll
-          for (int u = 0; u < kNB; u++) {
-            acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-            if (act[u]) {
-#pragma unroll
-              for (int s = 0; s < 8; s++) acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
-            }
+          if (j < nq) {
+            const int pidx = qoff + c0 + j;
+            const int q = pq[i];
+            Meta m;
+            m.qid = q;
+            m.qs = qs[q];
+            m.qcp = qcp[pidx];
+            m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
+            meta[j] = m;
           }
-          const int jl = t * 32 + li;  // pair index inside the chunk
-          const bool valid = jl < nq;
-          const Meta m = meta[valid ? jl : nq - 1];
-          const float th = MODE == 1 && valid ? m.x : __builtin_inff();
-          const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
+        }
+        __syncthreads();
+
+        if (any) {
+          const int ntiles = (nq + 31) / 32;
+          // B fragments of a tile: lane (li, h) reads bytes 32*s + 16*h of the code of the tile's query li
+          auto load = [&](v4i (&b)[8], int tile) {
+            const int jr = min(tile * 32 + li, nq - 1);
+            const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)meta[jr].qid * kR + h * 16);
 #pragma unroll
-          for (int u = 0; u < kNB; u++) {
-            if (MODE == 0 && !act[u]) continue;
-            // estimates of the block's 16 elements; the row scales are read from LDS up front
-            float ev[16];
+            for (int s = 0; s < 8; s++) b[s] = src[2 * s];
+          };
+          auto compute = [&](const v4i (&b)[8], int t) {
+            v16i acc[kNB];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
-              const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
+            for (int u = 0; u < kNB; u++) {
+              acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+              if (act[u]) {
 #pragma unroll
-              for (int i = 0; i < 4; i++) ev[4 * g + i] = __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp);
-            }
-            if (MODE == 0) {
-              float mx = -1e30f;
-#pragma unroll
-              for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
-              mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
-              if (h == 0 && valid) bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + (bk[u] - cs / 32)] = mx;
-            } else if (!direct) {
-              float *est = E->est[w];
-              uint32_t *tag = E->tag[w];
-#pragma unroll
-              for (int v = 0; v < 16; v++) {
-                const bool pass = ev[v] >= th;
-                const uint64_t bal = __ballot(pass);
-                if (bal) {
-                  const int slot = pass ? min(ebase + fvs_lane_prefix(bal), kCap - 1) : kCap + lane;
-                  est[slot] = ev[v];
-                  tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
-                  ebase += __popcll(bal);
-                }
+                for (int s = 0; s < 8; s++)
+                  acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
               }
-            } else {  // direct path
+            }
+            const int jl = t * 32 + li;  // pair index inside the chunk
+            const bool valid = jl < nq;
+            const Meta m = meta[valid ? jl : nq - 1];
+            const float th = MODE == 1 && valid ? m.x : __builtin_inff();
+            const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
 #pragma unroll
-              for (int v = 0; v < 16; v++) {
-                if (ev[v] >= th) {
-                  const int idx = atomicAdd(&cnt[m.qid], 1);
-                  if (idx < CAP) {
-                    bval[(int64_t)m.qid * CAP + idx] = ev[v];
-                    bpos[(int64_t)m.qid * CAP + idx] = bk[u] * 32 + acc_row(v, h);
+            for (int u = 0; u < kNB; u++) {
+              if (MODE == 0 && !act[u]) continue;
+              // estimates of the block's 16 elements; the row scales are read from LDS up front
+              float ev[16];
+#pragma unroll
+              for (int g = 0; g < 4; g++) {
+                const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
+                const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                  ev[4 * g + i] = __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp);
+              }
+              if (MODE == 0) {
+                float mx = -1e30f;
+#pragma unroll
+                for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
+                if (h == 0 && valid)
+                  bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + (bk[u] - cs / 32)] = mx;
+              } else if (!direct) {
+                float *est = E->est[w];
+                uint32_t *tag = E->tag[w];
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                  const bool pass = ev[v] >= th;
+                  const uint64_t bal = __ballot(pass);
+                  if (bal) {
+                    const int slot = pass ? min(ebase + fvs_lane_prefix(bal), kCap - 1) : kCap + lane;
+                    est[slot] = ev[v];
+                    tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
+                    ebase += __popcll(bal);
+                  }
+                }
+              } else {  // direct path
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                  if (ev[v] >= th) {
+                    const int idx = atomicAdd(&cnt[m.qid], 1);
+                    if (idx < CAP) {
+                      bval[(int64_t)m.qid * CAP + idx] = ev[v];
+                      bpos[(int64_t)m.qid * CAP + idx] = bk[u] * 32 + acc_row(v, h);
+                    }
                   }
                 }
               }
             }
+          };
+          v4i b0[8], b1[8];
+          load(b0, 0);
+          for (int t = 0; t < ntiles; t += 2) {
+            load(b1, min(t + 1, ntiles - 1));
+            compute(b0, t);
+            if (t + 1 >= ntiles) break;
+            load(b0, min(t + 2, ntiles - 1));
+            compute(b1, t + 1);
           }
-        };
-        v4i b0[8], b1[8];
-        load(b0, 0);
-        for (int t = 0; t < ntiles; t += 2) {
-          load(b1, min(t + 1, ntiles - 1));
-          compute(b0, t);
-          if (t + 1 >= ntiles) break;
-          load(b0, min(t + 2, ntiles - 1));
-          compute(b1, t + 1);
         }
+        __syncthreads();
       }
-      __syncthreads();
-    }
-  };
+    };
 
-  if constexpr (MODE == 0) {
-    scan(true, true);
-  } else {
-    scan(!staged, true);
-    if (!staged) return;
-    // a wave whose region overflowed: drop the staged candidates and redo the item on the direct path
-    if (lane == 0) E->n[w] = ebase;
-    __syncthreads();
-    if (E->n[0] > kCap || E->n[1] > kCap || E->n[2] > kCap || E->n[3] > kCap) {
-      __syncthreads();
-      scan(true, false);
-      return;
-    }
-    // flush the staged candidates: rank within the query, one global reservation per query, write out
-    for (int j = tid; j < qn; j += 256) E->qcount[j] = 0;
-    __syncthreads();
-    for (int i = tid; i < 4 * kCap; i += 256) {
-      const int ww = i / kCap, k = i - ww * kCap;
-      if (k < E->n[ww]) {
-        const uint32_t tg = E->tag[ww][k];
-        const int r = atomicAdd(&E->qcount[(tg >> 8) & 0xfffu], 1);  // < 256: a query has <= 256 rows here
-        E->tag[ww][k] = tg | ((uint32_t)r << 20);
-      }
-    }
-    __syncthreads();
-    for (int j = tid; j < qn; j += 256) {
-      const int m = E->qcount[j];
-      if (m) E->qcount[j] = atomicAdd(&cnt[qid[qoff + j]], m);  // now the query's base in its buffer
-    }
-    __syncthreads();
-    for (int i = tid; i < 4 * kCap; i += 256) {
-      const int ww = i / kCap, k = i - ww * kCap;
-      if (k < E->n[ww]) {
-        const uint32_t tg = E->tag[ww][k];
-        const int j = (tg >> 8) & 0xfffu;
-        const int idx = E->qcount[j] + (int)(tg >> 20);
-        if (idx < CAP) {
-          const int64_t q = qid[qoff + j];
-          bval[q * CAP + idx] = E->est[ww][k];
-          bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
+    if constexpr (MODE == 0) {
+      scan(true, true);
+      prefetch(nxt);
+    } else {
+      scan(!staged, true);
+      if (!staged) {
+      } else {
+        // a wave whose region overflowed: drop the staged candidates and redo the item on the direct path
+        if (lane == 0) E->n[w] = ebase;
+        __syncthreads();
+        if (E->n[0] > kCap || E->n[1] > kCap || E->n[2] > kCap || E->n[3] > kCap) {
+          __syncthreads();
+          scan(true, false);
+        } else {
+          // flush the staged candidates: rank within the query, one global reservation per query, write out
+          for (int j = tid; j < qn; j += 256) E->qcount[j] = 0;
+          __syncthreads();
+          for (int i = tid; i < 4 * kCap; i += 256) {
+            const int ww = i / kCap, k = i - ww * kCap;
+            if (k < E->n[ww]) {
+              const uint32_t tg = E->tag[ww][k];
+              const int r = atomicAdd(&E->qcount[(tg >> 8) & 0xfffu], 1);  // < 256: a query has <= 256 rows here
+              E->tag[ww][k] = tg | ((uint32_t)r << 20);
+            }
+          }
+          __syncthreads();
+          for (int j = tid; j < qn; j += 256) {
+            const int m = E->qcount[j];
+            if (m) E->qcount[j] = atomicAdd(&cnt[qid[qoff + j]], m);  // now the query's base in its buffer
+          }
+          __syncthreads();
+          for (int i = tid; i < 4 * kCap; i += 256) {
+            const int ww = i / kCap, k = i - ww * kCap;
+            if (k < E->n[ww]) {
+              const uint32_t tg = E->tag[ww][k];
+              const int j = (tg >> 8) & 0xfffu;
+              const int idx = E->qcount[j] + (int)(tg >> 20);
+              if (idx < CAP) {
+                const int64_t q = qid[qoff + j];
+                bval[q * CAP + idx] = E->est[ww][k];
+                bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
+              }
+            }
+          }
         }
       }
     }
+    if constexpr (MODE == 1) break;
+    cur = nxt;
+    p += stride;
   }
 }
 
@@ -285,14 +332,17 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
+  // first pass: two resident workgroups per CU, each looping over items with the next item's loads in
+  // flight during the current one; emit: one workgroup per item (its flush leaves no room to hide them)
+  const unsigned grid = mode == 0 ? (unsigned)min(P, 2 * fvs_cu_count()) : (unsigned)P;
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<0>, dim3((unsigned)P), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell,
-                       pblk, ps, pe, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+    hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, pblk, ps,
+                       pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<1>, dim3((unsigned)P), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell,
-                       pblk, ps, pe, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+    hipLaunchKernelGGL(k_i8_scan<1>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, pblk, ps,
+                       pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   }
   return fvs_launch_status();
 }
