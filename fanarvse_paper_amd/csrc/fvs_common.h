@@ -145,12 +145,48 @@ __host__ __device__ __forceinline__ int fvs_pow2_ceil(int n) {
   return p;
 }
 
+// A bound T with #{i : key(i) >= T} == kk for n UNIQUE keys, 1 <= kk <= n: the MSD radix select of
+// fvs_block_kth, stopped as soon as the chosen bucket holds exactly the keys still wanted (then every
+// key of the bucket is in and T is the bucket's smallest possible key). Block of 256 threads.
+template <typename KT, typename F>
+__device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
+  KT prefix = 0, pmask = 0;
+  for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
+    hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+      KT x = key(i);
+      if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
+    }
+    __syncthreads();
+    const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
+    const int h = hist[b];
+    const int inc = fvs_block_scan256(h, sh);
+    const int exc = inc - h;
+    if (exc < k && k <= inc) {
+      sh[4] = b;
+      sh[5] = k - exc;
+      sh[6] = h;
+    }
+    __syncthreads();
+    prefix |= (KT)sh[4] << shift;
+    pmask |= (KT)0xff << shift;
+    k = sh[5];
+    const bool whole = sh[6] == k;
+    __syncthreads();
+    if (whole) break;
+  }
+  return prefix;
+}
+
 // Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
-// Requires kk <= n. Block of 256 threads; cnt: 1 int of LDS.
+// Requires kk <= n. The kk keys above the radix bound are gathered, then each is stored at its rank
+// among them (kk <= 1024: a count of the larger keys; above, a bitonic sort). Block of 256 threads;
+// cnt: 1 int of LDS.
 template <typename F>
 __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
   const int P = fvs_pow2_ceil(kk);
-  const uint64_t kth = fvs_block_kth<uint64_t>(key, n, kk, hist, sh);
+  const uint64_t kth = fvs_block_kth_set<uint64_t>(key, n, kk, hist, sh);
   if (threadIdx.x == 0) *cnt = 0;
   for (int i = threadIdx.x; i < P; i += 256) s[i] = 0;
   __syncthreads();
@@ -162,5 +198,25 @@ __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist,
     }
   }
   __syncthreads();
-  fvs_block_bitonic<uint64_t, true>(s, P);
+  if (kk <= 1024) {
+    uint64_t mine[4];
+    int rank[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      mine[u] = threadIdx.x + 256 * u < kk ? s[threadIdx.x + 256 * u] : 0ull;
+      rank[u] = 0;
+    }
+    for (int t = 0; t < kk; t++) {
+      const uint64_t y = s[t];  // the same address for every lane: a broadcast read
+#pragma unroll
+      for (int u = 0; u < 4; u++) rank[u] += y > mine[u] ? 1 : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (threadIdx.x + 256 * u < kk) s[rank[u]] = mine[u];
+    __syncthreads();
+  } else {
+    fvs_block_bitonic<uint64_t, true>(s, P);
+  }
 }
