@@ -73,6 +73,7 @@ class EngineI8:
         self.meansN = (s1["means16"].float() * s1["inv_mnorm"][:, None]).half().contiguous()
         self.mnorm = (1.0 / s1["inv_mnorm"]).float().contiguous()
         self.graphs = {}
+        self._side = None  # stream for the stage-2 tables (default priority)
         self.nbad = 0
         self.nbad2 = 0
 
@@ -137,16 +138,28 @@ class EngineI8:
         s1 = self.s1
         qp = _lib.query_prep(Qb, self.Vr, s1["c"])
         q8, qs, QC, Qh, zq = qp
+        # the stage-2 tables depend only on the fp16 queries: a side stream builds them while stage 1 runs
+        main = torch.cuda.current_stream()
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=Qb.device)
+        self._side.wait_stream(main)
+        half = self.LUTF and self.LUTH
+        with torch.cuda.stream(self._side):
+            Zq = s2lut.rotate(self.code, Qh)
+            pre = _lib.lut_build(Zq, self.code["TS"], half)
+        for t in (Zq, *pre):  # made on the side stream, used on this one
+            t.record_stream(main)
         QM, probe = self._route(Qh, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
-        Zq = s2lut.rotate(self.code, Qh)
-        ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=self.LUTF and self.LUTH,
-                                                 ncnt=self._ncnt if self.DELTA is not None else None)
+        main.wait_stream(self._side)
+        ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=half,
+                                                 ncnt=self._ncnt if self.DELTA is not None else None, pre=pre)
         return ok, I, reads, ids, scores, (zq, QM, Zq)
 
-    def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt):
+    def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt, pre=None):
         """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95)."""
-        pre = _lib.lut_build(Zq, self.code["TS"], half)
+        if pre is None:
+            pre = _lib.lut_build(Zq, self.code["TS"], half)
         est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
         self._est, self._sd = est, sd
         ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
