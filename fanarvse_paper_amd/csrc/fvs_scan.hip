@@ -28,8 +28,11 @@
 // lanes write to a private dummy slot, so the store needs no divergent branch. If a wave's region
 // overflows, the item's staged candidates are dropped and the item is redone on the direct path
 // (one global atomic per candidate), which is also the path of cells probed by more than kMaxQ
-// queries. At the end of the item one global atomic per (item, query) reserves the query's buffer
-// range and the staged candidates are written out.
+// queries. Each pair of the item falls in exactly one tile, so while it emits, a lane numbers its own
+// candidates (the query of its column, its half of the rows); the per-(query, wave, half) counts go to
+// LDS at the end of the tile. At the end of the item one global atomic per (item, query) reserves the
+// query's buffer range, the counts are prefix-summed, and every staged candidate is written out at
+// base + prefix + its own number, with no per-candidate atomics.
 #include "fvs_common.h"
 
 namespace {
@@ -53,8 +56,10 @@ struct Meta {  // one (query, cell) pair of the item
 
 struct EmitLds {
   float est[4][kEW];
-  uint32_t tag[4][kEW];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | rank (20-27)
-  int qcount[kMaxQ];
+  uint32_t tag[4][kEW];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | number (20-27)
+  uint8_t cnt8[kMaxQ][8];  // candidates of (pair, wave, half); then their exclusive prefix over (wave, half)
+  int qids[kMaxQ];         // the pair's query
+  int qbase[kMaxQ];        // the pair's base in its query's buffer
   int n[4];
 };
 
@@ -151,6 +156,10 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
     }
     const bool any = act[0];
     int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
+    if constexpr (MODE == 1) {
+      if (staged)
+        for (int j = tid; j < qn; j += 256) *reinterpret_cast<uint2 *>(E->cnt8[j]) = make_uint2(0u, 0u);
+    }
 
     auto scan = [&](const bool direct, bool first) {
       for (int c0 = 0; c0 < qn; c0 += kMeta) {
@@ -174,6 +183,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
             m.qcp = qcp[pidx];
             m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
             meta[j] = m;
+            if (MODE == 1 && !direct) E->qids[c0 + j] = q;
           }
         }
         __syncthreads();
@@ -203,6 +213,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
             const Meta m = meta[valid ? jl : nq - 1];
             const float th = MODE == 1 && valid ? m.x : __builtin_inff();
             const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
+            int nmine = 0;  // this lane's candidates of the tile (its query, its half of the rows)
 #pragma unroll
             for (int u = 0; u < kNB; u++) {
               if (MODE == 0 && !act[u]) continue;
@@ -233,7 +244,8 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
                   if (bal) {
                     const int slot = pass ? min(ebase + fvs_lane_prefix(bal), kCap - 1) : kCap + lane;
                     est[slot] = ev[v];
-                    tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
+                    tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3)) + ((uint32_t)nmine << 20);
+                    nmine += pass ? 1 : 0;
                     ebase += __popcll(bal);
                   }
                 }
@@ -250,6 +262,7 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
                 }
               }
             }
+            if (MODE == 1 && !direct && valid) E->cnt8[c0 + jl][2 * w + h] = (uint8_t)nmine;
           };
           v4i b0[8], b1[8];
           load(b0, 0);
@@ -279,31 +292,34 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
           __syncthreads();
           scan(true, false);
         } else {
-          // flush the staged candidates: rank within the query, one global reservation per query, write out
-          for (int j = tid; j < qn; j += 256) E->qcount[j] = 0;
-          __syncthreads();
-          for (int i = tid; i < 4 * kCap; i += 256) {
-            const int ww = i / kCap, k = i - ww * kCap;
-            if (k < E->n[ww]) {
-              const uint32_t tg = E->tag[ww][k];
-              const int r = atomicAdd(&E->qcount[(tg >> 8) & 0xfffu], 1);  // < 256: a query has <= 256 rows here
-              E->tag[ww][k] = tg | ((uint32_t)r << 20);
-            }
-          }
-          __syncthreads();
+          // flush: per pair, the exclusive prefix of its (wave, half) counts and one global reservation of
+          // the total in its query's buffer; then every staged candidate goes to base + prefix + number
           for (int j = tid; j < qn; j += 256) {
-            const int m = E->qcount[j];
-            if (m) E->qcount[j] = atomicAdd(&cnt[qid[qoff + j]], m);  // now the query's base in its buffer
+            const uint2 c2 = *reinterpret_cast<const uint2 *>(E->cnt8[j]);
+            uint32_t run = 0, lo = 0, hi = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+              const uint32_t c = ((k < 4 ? c2.x : c2.y) >> (8 * (k & 3))) & 0xffu;
+              if (k < 4)
+                lo |= run << (8 * k);
+              else
+                hi |= run << (8 * (k - 4));
+              run += c;  // <= 8 * 32: every exclusive prefix fits a byte
+            }
+            *reinterpret_cast<uint2 *>(E->cnt8[j]) = make_uint2(lo, hi);
+            E->qbase[j] = run ? atomicAdd(&cnt[E->qids[j]], (int)run) : 0;
           }
           __syncthreads();
-          for (int i = tid; i < 4 * kCap; i += 256) {
-            const int ww = i / kCap, k = i - ww * kCap;
-            if (k < E->n[ww]) {
+#pragma unroll
+          for (int ww = 0; ww < 4; ww++) {
+            const int nn = E->n[ww];
+            for (int k = tid; k < nn; k += 256) {
               const uint32_t tg = E->tag[ww][k];
               const int j = (tg >> 8) & 0xfffu;
-              const int idx = E->qcount[j] + (int)(tg >> 20);
+              const int hh = (int)(tg >> 2) & 1;  // the half of the rows: bit 2 of the row offset
+              const int idx = E->qbase[j] + (int)E->cnt8[j][2 * ww + hh] + (int)(tg >> 20);
               if (idx < CAP) {
-                const int64_t q = qid[qoff + j];
+                const int64_t q = E->qids[j];
                 bval[q * CAP + idx] = E->est[ww][k];
                 bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
               }
