@@ -181,8 +181,8 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
 
 // Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
 // Requires kk <= n. The kk keys above the radix bound are gathered, then each is stored at its rank
-// among them (kk <= 1024: a count of the larger keys; above, a bitonic sort). Block of 256 threads;
-// cnt: 1 int of LDS.
+// among them (kk <= 128: a count of the larger keys; above, a bitonic sort, which measures faster
+// there). Block of 256 threads; cnt: 1 int of LDS.
 template <typename F>
 __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
   const int P = fvs_pow2_ceil(kk);
@@ -198,23 +198,12 @@ __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist,
     }
   }
   __syncthreads();
-  if (kk <= 1024) {
-    uint64_t mine[4];
-    int rank[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      mine[u] = threadIdx.x + 256 * u < kk ? s[threadIdx.x + 256 * u] : 0ull;
-      rank[u] = 0;
-    }
-    for (int t = 0; t < kk; t++) {
-      const uint64_t y = s[t];  // the same address for every lane: a broadcast read
-#pragma unroll
-      for (int u = 0; u < 4; u++) rank[u] += y > mine[u] ? 1 : 0;
-    }
+  if (kk <= 128) {
+    const uint64_t mine = threadIdx.x < kk ? s[threadIdx.x] : 0ull;
+    int rank = 0;
+    for (int t = 0; t < kk; t++) rank += s[t] > mine ? 1 : 0;  // one address for every lane: a broadcast read
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (threadIdx.x + 256 * u < kk) s[rank[u]] = mine[u];
+    if (threadIdx.x < kk) s[rank] = mine;
     __syncthreads();
   } else {
     fvs_block_bitonic<uint64_t, true>(s, P);
