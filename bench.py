@@ -300,7 +300,9 @@ def cpu_baseline(E, Q, K, args, nprobe, np, torch):
 def latency_mode(args):
     """the trellis cell-residual default engine on the same 1M x 1536 set, searched
     with batches of 1, 16 and 64 at z in {1.5, 2, 3}; per batch the median and p99 wall time of one search
-    call (host to host: queries already on the GPU, ids copied back), as src/v19_final.py:51-59 times it."""
+    call (host to host: queries already on the GPU, ids copied back), as src/v19_final.py:51-59 times it,
+    and the same for the lean path search_host (src/engine_cell.py:152-165). fallback_queries: flagged
+    queries in one pass over the timed batches (3 warm-up batches included)."""
     import numpy as np
     import torch
 
@@ -329,17 +331,26 @@ def latency_mode(args):
             rec = metrics.recall(I.cpu().numpy(), GT, args.k)
             for B in (int(v) for v in args.lat_batches.split(",")):
                 nb = max(20, min(args.lat_reps, 2000 // B))
-                ts = []
-                for i in range(nb + 3):
-                    Qb = Q[(i * B) % 2000:(i * B) % 2000 + B]
-                    torch.cuda.synchronize()
-                    t0 = time.perf_counter()
-                    E.search(Qb, K, z, nprobe, args.k)[0].cpu()
-                    ts.append(time.perf_counter() - t0)
-                ts = np.array(ts[3:]) * 1000
+                nbad0 = E.nbad
+
+                def timed(call):
+                    ts = []
+                    for i in range(nb + 3):
+                        Qb = Q[(i * B) % 2000:(i * B) % 2000 + B]
+                        torch.cuda.synchronize()
+                        t0 = time.perf_counter()
+                        call(Qb)
+                        ts.append(time.perf_counter() - t0)
+                    return np.array(ts[3:]) * 1000
+
+                # the reference's timing (src/v19_final.py:55-57), then the lean path (one replay, one sync)
+                ts = timed(lambda Qb: E.search(Qb, K, z, nprobe, args.k)[0].cpu())
+                tl = timed(lambda Qb: E.search_host(Qb, K, z, nprobe, args.k))
                 row = dict(nprobe=nprobe, K=K, z=z, batch=B, recall=rec, median_ms=round(float(np.median(ts)), 3),
                            p99_ms=round(float(np.percentile(ts, 99)), 3),
-                           qps=round(B / float(np.median(ts)) * 1000, 1), fallback=E.nbad)
+                           qps=round(B / float(np.median(ts)) * 1000, 1),
+                           lean_median_ms=round(float(np.median(tl)), 3), lean_p99_ms=round(float(np.percentile(tl, 99)), 3),
+                           fallback_queries=(E.nbad - nbad0) // 2, timed_queries=nb * B)
                 rows.append(row)
                 log(f"latency {row}")
     out = {"metric": "search latency per batch (median / p99 ms), trellis default engine, 1M x 1536",

@@ -8,7 +8,9 @@
 // (score << 16 | 0xffff - cell) are sorted by a bitonic network held in registers (element
 // lane * R + r; partners within a lane are registers, the others one lane shuffle away). The wave
 // never waits at a block barrier. Larger rows take the block-per-query kernel below, which stages
-// the keys in LDS, finds v* with two 8-bit histogram passes and sorts in LDS.
+// the keys in LDS, finds v* with two 8-bit histogram passes and sorts in LDS. Routing on fp32 keys
+// (fvs_route_topk_scaled, the trellis engine's scaled cell scores) follows the same two designs with
+// 32-bit keys, a 32-step bisection and (key, cell) pairs sorted as 64-bit values.
 //
 // Pairs: instead of a global counting sort (atomics on popular cells serialise), the probe lists are
 // transposed into a cell-major rank matrix rank[c][q] (int16, -1 = not probed) in caller scratch.
@@ -179,6 +181,176 @@ int route_wave_r(const uint16_t *QM, int64_t B, int NC, int np, int32_t *probe, 
   if (np <= 512) return launch_route_wave<C, 8>(QM, B, NC, np, probe, st);
   if (np <= 1024) return launch_route_wave<C, 16>(QM, B, NC, np, probe, st);
   return launch_route_wave<C, 32>(QM, B, NC, np, probe, st);
+}
+
+// ------------------------------------------------------------------------------------ routing
+// Top-n_p cells by the fp32 key (float)QM[q][c] * scale[c] (or ((float)QM[q][c] + qadd[q]) * scale[c]),
+// sorted by (key descending, cell ascending).
+__global__ __launch_bounds__(256) void k_route_f32(const uint16_t *__restrict__ QM, const float *__restrict__ scale,
+                                                   const float *__restrict__ qadd, int NC, int np,
+                                                   int32_t *__restrict__ probe) {
+  extern __shared__ uint64_t rk[];  // [NC] keys, then [pow2(np)] the sorted top
+  __shared__ int hist[256];
+  __shared__ int sh[8];
+  __shared__ int gcnt;
+  const int64_t q = blockIdx.x;
+  uint64_t *top = rk + NC;
+  const float add = qadd ? qadd[q] : 0.f;
+  for (int i = threadIdx.x; i < NC; i += 256) {
+    const float key = qadd ? (fvs_h2f(QM[q * NC + i]) + add) * scale[i] : fvs_h2f(QM[q * NC + i]) * scale[i];
+    rk[i] = ((uint64_t)fvs_ord32(key) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  }
+  __syncthreads();
+  fvs_block_topk_u64([&](int i) { return rk[i]; }, NC, np, top, hist, sh, &gcnt);
+  for (int i = threadIdx.x; i < np; i += 256) probe[q * np + i] = (int32_t)(0xffffffffu - (uint32_t)(top[i] & 0xffffffffu));
+}
+
+// The same selection with one wave per query (fvs_route_topk_scaled when NC % 8 == 0, NC <= 8192 and
+// n_p <= 1024): 32-bit ordered keys in registers, v* = the n_p-th largest by bisection over the 32 bits,
+// ties at v* taken lowest cells first, then a bitonic sort of the (key << 32 | ~cell) pairs, n_p <= 64 R.
+template <int C, int R, bool ADD>
+__global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave_f32(const uint16_t *__restrict__ QM,
+                                                                          const float *__restrict__ scale,
+                                                                          const float *__restrict__ qadd, int NC,
+                                                                          int np, int64_t B,
+                                                                          int32_t *__restrict__ probe) {
+  __shared__ uint64_t sbuf[kRouteWaves][FVS_WAVE * R];
+  const int lane = threadIdx.x & (FVS_WAVE - 1), wv = threadIdx.x >> 6;
+  const int64_t q = (int64_t)blockIdx.x * kRouteWaves + wv;
+  if (q >= B) return;  // wave-uniform, and no block barrier follows
+  uint64_t *s = sbuf[wv];
+  const uint4 *row = reinterpret_cast<const uint4 *>(QM + q * (int64_t)NC);
+  const float4 *sc4 = reinterpret_cast<const float4 *>(scale);
+  const float add = ADD ? qadd[q] : 0.f;
+
+  // 1. keys, computed as in k_route_f32; cells past NC get key 0 and are excluded by their index
+  uint32_t k[8 * C];
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int ch = c * FVS_WAVE + lane;
+    const bool ok = ch * 8 < NC;
+    const uint4 v = ok ? row[ch] : make_uint4(0, 0, 0, 0);
+    const float4 s0 = ok ? sc4[2 * ch] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 s1 = ok ? sc4[2 * ch + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float x = fvs_h2f((uint16_t)((e & 1) ? (w4[e >> 1] >> 16) : (w4[e >> 1] & 0xffffu)));
+      if (ADD) x = x + add;
+      x = x * sc[e];
+      k[8 * c + e] = ok ? fvs_ord32(x) : 0u;
+    }
+  }
+
+  // 2. v* = the largest t with #{keys >= t} >= n_p
+  uint32_t vstar = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; bit--) {
+    const uint32_t cand = vstar | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 8 * C; i++) cnt += k[i] >= cand ? 1 : 0;
+    if (wave_sum_i32(cnt) >= np) vstar = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < 8 * C; i++) gt += k[i] > vstar ? 1 : 0;
+  const int want = np - wave_sum_i32(gt);
+
+  // 3. compaction in cell order
+  int sbase = 0, tbase = 0;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int ch = c * FVS_WAVE + lane;
+    const bool ok = ch * 8 < NC;
+    int nt = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) nt += (ok && k[8 * c + e] == vstar) ? 1 : 0;
+    const int tin = wave_incl_scan_i32(nt, lane);
+    int tie = tbase + tin - nt;
+    uint32_t selm = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint32_t x = k[8 * c + e];
+      const bool eq = ok && x == vstar;
+      const bool sel = ok && (x > vstar || (eq && tie < want));
+      tie += eq ? 1 : 0;
+      selm |= sel ? (1u << e) : 0u;
+    }
+    const int ns = __builtin_popcount(selm);
+    const int sin = wave_incl_scan_i32(ns, lane);
+    int at = sbase + sin - ns;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      if (selm & (1u << e))
+        s[at++] = ((uint64_t)k[8 * c + e] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(ch * 8 + e));
+    }
+    sbase += __builtin_amdgcn_readlane(sin, FVS_WAVE - 1);
+    tbase += __builtin_amdgcn_readlane(tin, FVS_WAVE - 1);
+  }
+  for (int i = np + lane; i < FVS_WAVE * R; i += FVS_WAVE) s[i] = 0ull;  // below every selected pair
+  wave_lds_sync();
+
+  // 4. bitonic sort, descending, of element lane * R + r
+  uint64_t x[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) x[r] = s[lane * R + r];
+#pragma unroll
+  for (int kk = 2; kk <= FVS_WAVE * R; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      if (j >= R) {
+        const int lo = lane * R;
+        const bool desc = (lo & kk) == 0, first = (lo & j) == 0;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint64_t y = __shfl_xor(x[r], j / R, FVS_WAVE);
+          x[r] = (desc == first) ? (x[r] > y ? x[r] : y) : (x[r] < y ? x[r] : y);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          if ((r & j) == 0) {
+            const bool desc = ((lane * R + r) & kk) == 0;
+            const uint64_t a = x[r], b = x[r | j];
+            const uint64_t hi = a > b ? a : b, lo = a < b ? a : b;
+            x[r] = desc ? hi : lo;
+            x[r | j] = desc ? lo : hi;
+          }
+        }
+      }
+    }
+  }
+  int32_t *out = probe + q * (int64_t)np;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int i = lane * R + r;
+    if (i < np) out[i] = (int32_t)(0xffffffffu - (uint32_t)(x[r] & 0xffffffffu));
+  }
+}
+
+template <int C, int R>
+int launch_route_wave_f32(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int NC, int np,
+                          int32_t *probe, hipStream_t st) {
+  const unsigned grid = (unsigned)((B + kRouteWaves - 1) / kRouteWaves);
+  if (qadd)
+    hipLaunchKernelGGL((k_route_wave_f32<C, R, true>), dim3(grid), dim3(kRouteWaves * FVS_WAVE), 0, st, QM, scale,
+                       qadd, NC, np, B, probe);
+  else
+    hipLaunchKernelGGL((k_route_wave_f32<C, R, false>), dim3(grid), dim3(kRouteWaves * FVS_WAVE), 0, st, QM, scale,
+                       qadd, NC, np, B, probe);
+  return fvs_launch_status();
+}
+
+template <int C>
+int route_wave_f32_r(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int NC, int np,
+                     int32_t *probe, hipStream_t st) {
+  if (np <= 64) return launch_route_wave_f32<C, 1>(QM, scale, qadd, B, NC, np, probe, st);
+  if (np <= 128) return launch_route_wave_f32<C, 2>(QM, scale, qadd, B, NC, np, probe, st);
+  if (np <= 256) return launch_route_wave_f32<C, 4>(QM, scale, qadd, B, NC, np, probe, st);
+  if (np <= 512) return launch_route_wave_f32<C, 8>(QM, scale, qadd, B, NC, np, probe, st);
+  return launch_route_wave_f32<C, 16>(QM, scale, qadd, B, NC, np, probe, st);
 }
 
 __global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__ QM, int NC, int np,
@@ -509,6 +681,22 @@ extern "C" int fvs_route_topk(const uint16_t *QM, int64_t B, int32_t NC, int32_t
     if (NC <= 8192) return route_wave_r<16>(QM, B, NC, nprobe, probe, st);
   }
   hipLaunchKernelGGL(k_route_topk, dim3((unsigned)B), dim3(256), 0, st, QM, NC, nprobe, probe);
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC,
+                                     int32_t nprobe, int32_t *probe, void *stream) {
+  if (B < 0 || NC <= 0 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
+  if (NC > 8192 || nprobe > 4096) return FVS_E_CAPACITY;
+  if (B == 0) return FVS_OK;
+  if (!QM || !scale || !probe) return FVS_E_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (NC % 8 == 0 && nprobe <= 1024 && ((reinterpret_cast<uintptr_t>(QM) | reinterpret_cast<uintptr_t>(scale)) & 15) == 0) {
+    if (NC <= 4096) return route_wave_f32_r<8>(QM, scale, qadd, B, NC, nprobe, probe, st);
+    return route_wave_f32_r<16>(QM, scale, qadd, B, NC, nprobe, probe, st);
+  }
+  const size_t shm = 8 * ((size_t)NC + (size_t)fvs_pow2_ceil(nprobe));
+  hipLaunchKernelGGL(k_route_f32, dim3((unsigned)B), dim3(256), shm, st, QM, scale, qadd, NC, nprobe, probe);
   return fvs_launch_status();
 }
 

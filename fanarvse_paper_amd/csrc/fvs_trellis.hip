@@ -1,10 +1,12 @@
 // The trellis cell-residual engine of the latency mode: bitshift-trellis encoder (Viterbi), stage-1
-// scan over the decoded codes, routing on fp32 keys, and the Lloyd-Max tiered stage 2.
+// scan over the decoded codes and the Lloyd-Max tiered stage 2 (its fp32-key routing is in fvs_route.hip).
 //
 // Trellis code (L-bit states, one bit per coordinate): a vector's bit stream is the L bits of its
 // first state (MSB first) followed by the newest bit of every later state; state_j is the window
 // bits[j .. j+L) read MSB first and the decoded coordinate j is tab[state_j]. The stream is stored
 // as W = ceil((R + L - 1) / 32) 32-bit words, first bit in the most significant position.
+#include <algorithm>
+
 #include "fvs_common.h"
 
 namespace {
@@ -208,27 +210,6 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
   }
 }
 
-// ------------------------------------------------------------------------------------ routing
-// Top-n_p cells by the fp32 key (float)QM[q][c] * scale[c] (or ((float)QM[q][c] + qadd[q]) * scale[c]),
-// sorted by (key descending, cell ascending).
-__global__ __launch_bounds__(256) void k_route_f32(const uint16_t *__restrict__ QM, const float *__restrict__ scale,
-                                                   const float *__restrict__ qadd, int NC, int np,
-                                                   int32_t *__restrict__ probe) {
-  extern __shared__ uint64_t rk[];  // [NC] keys, then [pow2(np)] the sorted top
-  __shared__ int hist[256];
-  __shared__ int sh[8];
-  __shared__ int gcnt;
-  const int64_t q = blockIdx.x;
-  uint64_t *top = rk + NC;
-  const float add = qadd ? qadd[q] : 0.f;
-  for (int i = threadIdx.x; i < NC; i += 256) {
-    const float key = qadd ? (fvs_h2f(QM[q * NC + i]) + add) * scale[i] : fvs_h2f(QM[q * NC + i]) * scale[i];
-    rk[i] = ((uint64_t)fvs_ord32(key) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-  }
-  __syncthreads();
-  fvs_block_topk_u64([&](int i) { return rk[i]; }, NC, np, top, hist, sh, &gcnt);
-  for (int i = threadIdx.x; i < np; i += 256) probe[q * np + i] = (int32_t)(0xffffffffu - (uint32_t)(top[i] & 0xffffffffu));
-}
 
 // ------------------------------------------------------------------------------------ stage 2
 struct LmTiers {
@@ -236,7 +217,9 @@ struct LmTiers {
   int start[kMaxT], width[kMaxT], bits[kMaxT], toff[kMaxT];
 };
 
-// One workgroup per query, one wave per candidate at a time. Canonical arithmetic:
+// A query's K candidates are split over `nchunk` workgroups of 4 waves; workgroup (q, c) takes candidates
+// 4*cpw*c .. 4*cpw*(c+1)-1 and each wave one candidate at a time, so a batch of one query still fills the
+// chip while a large batch keeps one staging of Zq and the codebooks per 4*cpw candidates. Canonical arithmetic:
 //   a_t = (xor butterfly over 64 lanes of) the lane sums, lane l summing fmaf(cb_t[code_k], Zq[s_t + k], .)
 //   over the tier's coordinates k = l, l + 64, ... in order;
 //   est = fmaf(a_t, scale_t, est) and var = fmaf(qn2_t * sig_t, sig_t, var) for t = 0..T-1 from
@@ -245,15 +228,16 @@ struct LmTiers {
 __global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict__ pos, const float *__restrict__ qc,
                                                       const float *__restrict__ Zq, int D, const uint8_t *__restrict__ rec,
                                                       int RB, int soff, LmTiers tiers, const float *__restrict__ cb,
-                                                      const int32_t *__restrict__ ncnt, int K, float *__restrict__ est,
-                                                      float *__restrict__ sd) {
+                                                      const int32_t *__restrict__ ncnt, int K, int nchunk, int cpw,
+                                                      float *__restrict__ est, float *__restrict__ sd) {
   extern __shared__ __align__(16) uint8_t dyn[];
   float *zq = reinterpret_cast<float *>(dyn);                  // [D]
   float *cbs = zq + D;                                         // [T][256]
   uint8_t *recs = reinterpret_cast<uint8_t *>(cbs + 256 * tiers.T);  // [4][RB]
   __shared__ float qn2[kMaxT];
-  const int64_t q = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t q = blockIdx.x / nchunk;
+  const int m0 = (int)(blockIdx.x % nchunk) * 4 * cpw, m1 = min(K, m0 + 4 * cpw);
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int i = tid; i < D; i += 256) zq[i] = Zq[q * D + i];
   for (int i = tid; i < 256 * tiers.T; i += 256) cbs[i] = cb[i];
   __syncthreads();
@@ -273,7 +257,7 @@ __global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict_
   __syncthreads();
   const int nc = ncnt ? min(ncnt[q], K) : K;
   uint8_t *rw = recs + w * RB;
-  for (int m = w; m < K; m += 4) {
+  for (int m = m0 + w; m < m1; m += 4) {
     if (m >= nc) {
       if (lane == 0) {
         est[q * K + m] = -1e30f;
@@ -362,17 +346,6 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
   return fvs_launch_status();
 }
 
-extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC,
-                                     int32_t nprobe, int32_t *probe, void *stream) {
-  if (B < 0 || NC <= 0 || nprobe <= 0 || nprobe > NC) return FVS_E_ARG;
-  if (NC > 8192 || nprobe > 4096) return FVS_E_CAPACITY;
-  if (B == 0) return FVS_OK;
-  if (!QM || !scale || !probe) return FVS_E_ARG;
-  const size_t shm = 8 * ((size_t)NC + (size_t)fvs_pow2_ceil(nprobe));
-  hipLaunchKernelGGL(k_route_f32, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, QM, scale, qadd, NC, nprobe, probe);
-  return fvs_launch_status();
-}
-
 extern "C" int fvs_tiered_score(const int32_t *pos, const float *qc, const float *Zq, int32_t D, const uint8_t *rec,
                                 int64_t N, int32_t RB, int32_t soff, int32_t T, const int32_t *tiers, const int32_t *toff,
                                 const float *cb, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
@@ -394,7 +367,12 @@ extern "C" int fvs_tiered_score(const int32_t *pos, const float *qc, const float
   }
   const size_t shm = 4 * (size_t)D + 4 * 256 * (size_t)T + 4 * (size_t)RB;
   if (shm > 160 * 1024) return FVS_E_CAPACITY;
-  hipLaunchKernelGGL(k_tiered_score, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, pos, qc, Zq, D, rec, RB,
-                     soff, ta, cb, ncnt, K, est, sd);
+  // about 2048 workgroups when the batch is small, one per query when it is large
+  const int groups = (K + 3) / 4;
+  const int nchunk = (int)std::min<int64_t>(groups, std::max<int64_t>(1, (2048 + B - 1) / B));
+  const int cpw = (groups + nchunk - 1) / nchunk;
+  if (B * nchunk > 0x7fffffff) return FVS_E_CAPACITY;
+  hipLaunchKernelGGL(k_tiered_score, dim3((unsigned)(B * nchunk)), dim3(256), shm, (hipStream_t)stream, pos, qc, Zq,
+                     D, rec, RB, soff, ta, cb, ncnt, K, nchunk, cpw, est, sd);
   return fvs_launch_status();
 }

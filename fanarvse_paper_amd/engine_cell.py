@@ -6,7 +6,10 @@ stage 3, src/engine3.py:135-175):
     E = EngineS(s1, code, H=X16)
     I, reads, cand_ids = E.search(Qb, K, z, nprobe, k)
 A batch is one hipGraph replay per (B, K, z, nprobe, k) and one host synchronisation on the exactness
-flags; flagged queries are redone with rho = 1, beta = 1.5 and a 65,536-entry buffer.
+flags; flagged queries are redone with rho = 1, beta = 1.5 and a 65,536-entry buffer, by a captured
+graph too (flagged rows padded to a power of two). search_host is the lean latency path
+(src/engine_cell.py:130-165, EngineT.search_host): the graph itself copies the flags and the top-k ids
+into pinned host memory, so a search is one replay and one stream synchronisation.
 
 Stage 1 is the static work-list scan (src/s1cell.py:176-195) for every batch size. The reference
 switches to per-(query, cell) programs for B <= 8 and to a dense probe mask for B <= 32
@@ -25,8 +28,12 @@ from .enginei8 import _fresh
 
 class EngineS:
     BN = 32
-    M = None          # emit buffer size; None = max(4096, 16 K) (src/s1cell.py:180)
-    SMALL, TINY = 32, 8
+    M = None          # emit buffer size; None = max(4096, 16 K) (src/s1cell.py:180), or M_SMALL for small batches
+    # Batches of at most SMALL_B queries get a 65,536-entry emit buffer, the size of the fallback's. Results
+    # are unchanged: a query that emits cnt >= K candidates above its threshold t0 holds the global top-K
+    # (by estimate, then position) of its probed rows whatever t0 was, so the reference's overflow fallback
+    # returns the same top-K; only the second stage-1 pass is saved. Underflows (cnt < K) still fall back.
+    M_SMALL, SMALL_B = 65536, 64
 
     def __init__(self, s1, code, H=None):
         self.s1, self.code, self.H = s1, code, H
@@ -42,10 +49,10 @@ class EngineS:
         if int(s1["off_t"][-1]) != s1["words"].shape[0]:
             raise ValueError("EngineS: cell offsets do not match the code rows")
 
-    def _params(self, K, nprobe, rho_override=None, M_override=None):
+    def _params(self, K, nprobe, rho_override=None, M_override=None, B=None):
         NC = len(self.s1["off"]) - 1
         N = self.s1["words"].shape[0]
-        M = M_override or self.M or max(4096, 16 * K)
+        M = M_override or self.M or (self.M_SMALL if B is not None and B <= self.SMALL_B else max(4096, 16 * K))
         beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
         if rho_override:
             beta, rho = 1.5, rho_override
@@ -58,7 +65,7 @@ class EngineS:
         NC = len(s1["off"]) - 1
         B = Qr.shape[0]
         dev = Qr.device
-        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
+        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override, B)
         L = int(s1["L"])
         scratch = _lib.pairs_scratch(B, NC, dev)
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch)
@@ -99,34 +106,103 @@ class EngineS:
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq, probe)
 
+    @staticmethod
+    def _capture(fn):
+        """Run fn three times on a side stream (allocations and lazy set-up happen there), then capture
+        one more run into a hipGraph. Returns (graph, fn's outputs)."""
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(st)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs = fn()
+        return g, outs
+
+    def _main(self, Qb, K, z, nprobe, k, host=False):
+        """The captured search of a (B, K, z, nprobe, k) batch. host: the graph also copies
+        [ok | top-k ids] (int64) into pinned host memory."""
+        B = len(Qb)
+        key = ("host" if host else "dev", B, K, float(z), nprobe, k)
+        if key not in self.graphs:
+            qs = Qb.clone()
+            hb = torch.empty((B, k + 1), dtype=torch.int64, pin_memory=True) if host else None
+
+            def run():
+                outs = self._gpu(qs, K, z, nprobe, k)
+                if host:
+                    hb.copy_(torch.cat([outs[0].to(torch.int64)[:, None], outs[1].to(torch.int64)], 1),
+                             non_blocking=True)
+                return outs
+
+            g, outs = self._capture(run)
+            self.graphs[key] = (key, g, qs, outs, hb)
+            self._fallback_graph(self.graphs[key], 1)  # a lone flagged query needs no capture later
+        return self.graphs[key]
+
+    def _fallback_graph(self, entry, nbp):
+        """The captured fallback of nbp rows gathered from the static inputs of the main graph `entry`."""
+        key, _, qs, (ok, I, nr, ids, sc, dense), _ = entry
+        fkey = ("fb", key, nbp)
+        if fkey not in self.graphs:
+            sel = torch.zeros(nbp, dtype=torch.int64, device=qs.device)
+            K, z, k = key[2], key[3], key[5]
+
+            def run():
+                a = [t.index_select(0, sel) for t in (qs,) + tuple(dense)]
+                return self._fallback(a[0], K, z, k, *a[1:])
+
+            g, outs = self._capture(run)
+            self.graphs[fkey] = (g, sel, outs)
+        return self.graphs[fkey]
+
+    def _fallback_rows(self, entry, bad):
+        """Flagged rows `bad` (host int64) of the batch last replayed in `entry`, recomputed by a captured
+        fallback graph over a power-of-two padding of the rows (the last row repeated). Returns the
+        device tensors (I, reads, ids, scores) of the len(bad) rows."""
+        nb = len(bad)
+        nbp = 1 << (nb - 1).bit_length()
+        g, sel, outs = self._fallback_graph(entry, nbp)
+        pad = np.concatenate([bad, np.full(nbp - nb, bad[-1], np.int64)])
+        sel.copy_(torch.from_numpy(pad), non_blocking=False)
+        g.replay()
+        self.nbad += nb
+        return [t[:nb] for t in outs]
+
     def search(self, Qb, K, z, nprobe, k, ret_scores=False):
         """(I [B,k], reads [B], cand_ids [B,K]) (+ scores) as src/engine_cell.py:85-102."""
         Qb = Qb.float().contiguous()
-        B = len(Qb)
-        key = (B, K, float(z), nprobe, k)
-        if key not in self.graphs:
-            qs = Qb.clone()
-            st = torch.cuda.Stream()
-            st.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(st):
-                for _ in range(3):
-                    self._gpu(qs, K, z, nprobe, k)
-            torch.cuda.current_stream().wait_stream(st)
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                outs = self._gpu(qs, K, z, nprobe, k)
-            self.graphs[key] = (g, qs, outs)
-        g, qs, (ok, I, nr, ids, sc, dense) = self.graphs[key]
+        entry = self._main(Qb, K, z, nprobe, k)
+        _, g, qs, (ok, I, nr, ids, sc, dense), _ = entry
         qs.copy_(Qb)
         g.replay()
         I, nr, ids, sc = _fresh(I, nr, ids, sc)
-        okh = ok.cpu()
-        if not bool(okh.all()):
-            bad = torch.nonzero(~okh).flatten().to(Qb.device)
-            self.nbad += len(bad)
-            a, b, c, s = self._fallback(Qb[bad], K, z, k, *[t[bad].contiguous() for t in dense])
-            I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
+        okh = ok.cpu().numpy()
+        if not okh.all():
+            bad = np.nonzero(~okh)[0].astype(np.int64)
+            a, b, c, s = self._fallback_rows(entry, bad)
+            bd = torch.from_numpy(bad).to(Qb.device)
+            I[bd], nr[bd], ids[bd], sc[bd] = a, b, c, s
         return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
+
+    def search_host(self, Qb, K, z, nprobe, k):
+        """Top-k ids [B, k] as an int64 numpy array: the latency path of src/engine_cell.py:152-165. One
+        graph replay, which ends by copying the exactness flags and the ids into pinned host memory, and
+        one stream synchronisation; flagged queries go through the captured fallback."""
+        Qb = Qb.float().contiguous()
+        entry = self._main(Qb, K, z, nprobe, k, host=True)
+        _, g, qs, _, hb = entry
+        qs.copy_(Qb)
+        g.replay()
+        torch.cuda.current_stream().synchronize()
+        h = hb.numpy()
+        out = h[:, 1:].copy()
+        if not h[:, 0].all():
+            bad = np.nonzero(h[:, 0] == 0)[0].astype(np.int64)
+            out[bad] = self._fallback_rows(entry, bad)[0].cpu().numpy()
+        return out
 
     def _fallback(self, Qb, K, z, k, Qr, QC, QM, Zq, probe):
         """Flagged queries again with rho = 1, beta = 1.5 and M = 65,536 (the reference recomputes them with

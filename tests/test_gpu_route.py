@@ -2,7 +2,9 @@
 ties at the n_p-th value (taken lowest cells first), +-0 (equal), +-inf, and every shape class of the
 launcher: the wave-per-query kernel for each (cells per lane, sorted keys per lane) instantiation and
 the block-per-query kernel for rows it does not take (NC not a multiple of 8, NC > 8192, n_p > 2048).
-Results are bit-exact: the probe lists are sorted by (score desc, cell asc)."""
+Routing on fp32 keys (QM * scale, or (QM + qadd) * scale: the trellis engines) is checked the same way
+over its wave kernel (32-bit keys) and its block kernel. Results are bit-exact: the probe lists are
+sorted by (score desc, cell asc)."""
 import numpy as np
 import pytest
 import torch
@@ -40,6 +42,44 @@ def test_route_topk_many_queries(oracle_mod):
     got = _lib.route_topk(torch.from_numpy(QM.view(np.float16)).cuda(), 768)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy(), oracle_mod.route_topk(QM, 768))
+
+
+SCALED = [(64, 1), (64, 12), (104, 64), (520, 65), (1024, 128), (4096, 256), (4096, 384), (4096, 512),
+          (4096, 1024), (4096, 1025), (8192, 1), (8192, 768), (8192, 1024), (100, 37), (4100, 300)]
+
+
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("NC,npr", SCALED)
+def test_route_topk_scaled_matches_oracle(oracle_mod, NC, npr, add):
+    print(f"\n[gpu route scaled] NC={NC} nprobe={npr} qadd={add}", flush=True)
+    B = 9
+    QM = rows(B, NC, NC * 5 + npr)
+    rng = np.random.default_rng(npr)
+    # repeated scales keep exact key ties; some zeros and negatives
+    scale = rng.choice(np.array([0.0, 0.5, 1.0, 1.0, 2.0, -1.0, 3.0], np.float32), NC)
+    qadd = rng.choice(np.array([0.0, -1.5, 2.0], np.float32), B) if add else None
+    QMd = torch.from_numpy(QM.view(np.float16)).cuda()
+    got = _lib.route_topk_scaled(QMd, torch.from_numpy(scale).cuda(), npr,
+                                 None if qadd is None else torch.from_numpy(qadd).cuda())
+    torch.cuda.synchronize()
+    want = oracle_mod.route_topk_scaled(QM, scale, npr, qadd)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_route_topk_scaled_batches(oracle_mod):
+    """Batch 1 and a batch that is not a multiple of the 4 queries per block, at the latency shape; a
+    misaligned scale vector takes the block kernel."""
+    for B in (1, 1001):
+        QM = rows(B, 4096, B)
+        scale = np.random.default_rng(B).uniform(0.5, 2.0, 4096).astype(np.float32)
+        QMd = torch.from_numpy(QM.view(np.float16)).cuda()
+        got = _lib.route_topk_scaled(QMd, torch.from_numpy(scale).cuda(), 384)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), oracle_mod.route_topk_scaled(QM, scale, 384))
+    buf = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), scale])).cuda()  # 4-byte offset
+    got = _lib.route_topk_scaled(QMd, buf[1:], 384)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle_mod.route_topk_scaled(QM, scale, 384))
 
 
 @pytest.mark.parametrize("B,NC,npr,n", [(1, 64, 12, 12), (7, 64, 24, 5), (2000, 4096, 768, 768), (2001, 4096, 768, 90),

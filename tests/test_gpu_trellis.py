@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from fanarvse_paper_amd import datagen, metrics, trellis
+from fanarvse_paper_amd import _lib, datagen, metrics, trellis
 from fanarvse_paper_amd.engine_cell import EngineS
 
 pytestmark = pytest.mark.gpu
@@ -43,7 +43,7 @@ def traced(env, oracle_mod):
     torch.cuda.synchronize()
     tr = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in tr.items()}
     out = oracle_mod.tr_pipeline(env["idx"], npy(env["Q"]), K, Z_, NPROBE, KK, Qr=npy(tr["Qr"]), QM16=u16(tr["QM"]),
-                                 Zq=npy(tr["Zq"]), fallback=False)
+                                 Zq=npy(tr["Zq"]), M=tr["M"], fallback=False)
     return tr, out
 
 
@@ -106,6 +106,28 @@ def test_stage2_and_refine_bit_exact(traced):
     assert np.allclose(npy(tr["scores"])[ok], out["scores"][ok], rtol=1e-3)
 
 
+@pytest.mark.parametrize("B,K2", [(1, 400), (3, 1000), (16, 7), (64, 100), (700, 200), (5000, 64)])
+def test_tiered_score_launch_shapes(env, oracle_mod, B, K2):
+    """Stage 2 alone over every split of a query's candidates across workgroups (one workgroup per 4
+    candidates at batch 1 up to one per query at large batches), with slots past a query's count."""
+    print(f"\n[gpu trellis] tiered score B={B} K={K2}", flush=True)
+    code = env["code"]
+    N = code["rec"].shape[0]
+    D = code["VP"].shape[1]
+    g = torch.Generator(device="cuda").manual_seed(B * 7 + K2)
+    pos = torch.randint(0, N, (B, K2), device="cuda", generator=g, dtype=torch.int32)
+    qc = torch.randn(B, device="cuda", generator=g)
+    Zq = torch.randn(B, D, device="cuda", generator=g)
+    ncnt = torch.randint(0, K2 + 5, (B,), device="cuda", generator=g, dtype=torch.int32)
+    for nc in (None, ncnt):
+        est, sd = _lib.tiered_score(pos, qc, Zq, code, nc)
+        torch.cuda.synchronize()
+        we, ws = oracle_mod.tiered_score(npy(pos), npy(qc), npy(Zq), npy(code["rec"]), code["soff"], code["TS"],
+                                         code["toff"], npy(code["cb"]), None if nc is None else npy(nc))
+        assert np.array_equal(npy(est).view(np.uint32), we.view(np.uint32))
+        assert np.array_equal(npy(sd).view(np.uint32), ws.view(np.uint32))
+
+
 @pytest.mark.parametrize("B", [1, 16, 64])
 def test_search_batch_sizes_match_oracle(env, oracle_mod, B):
     E = env["E"]
@@ -122,3 +144,69 @@ def test_search_batch_sizes_match_oracle(env, oracle_mod, B):
     if B >= 16:  # one query's recall is too coarse a statistic
         rec = metrics.recall(npy(I), env["GT"][:B], 10)
         assert rec >= 0.85, rec
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+def test_lean_path_matches_search(env, B):
+    """search_host (one replay that copies flags and ids to pinned host memory, one synchronisation)
+    returns search's top-k ids."""
+    E = env["E"]
+    Q = env["Q"][:B].contiguous()
+    I = npy(E.search(Q, K, Z_, NPROBE, KK)[0])
+    for _ in range(2):
+        h = E.search_host(Q, K, Z_, NPROBE, KK)
+        assert h.dtype == np.int64 and h.shape == (B, KK)
+        assert np.array_equal(h, I)
+
+
+@pytest.mark.parametrize("B", [1, 5, 64])
+def test_fallback_graph_matches_oracle(env, oracle_mod, B):
+    """A buffer of K+8 entries overflows for most queries: the flagged rows go through the captured
+    fallback graph (rows padded to a power of two), from search and from search_host, twice each (graph
+    replays), and agree with the oracle's fallback on the same shared BLAS inputs."""
+    print(f"\n[gpu trellis] fallback graph B={B}", flush=True)
+    E = env["E"]
+    Q = env["Q"][:B].contiguous()
+    old = E.M
+    E.M = K + 8
+    E.graphs.clear()
+    try:
+        res = [E.search(Q, K, Z_, NPROBE, KK, ret_scores=True) for _ in range(2)]
+        hs = [E.search_host(Q, K, Z_, NPROBE, KK) for _ in range(2)]
+        torch.cuda.synchronize()
+        Qr, QC, QM, Zq = E._dense(Q)
+        out = oracle_mod.tr_pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, Qr=npy(Qr), QM16=u16(QM), Zq=npy(Zq),
+                                     M=K + 8)
+    finally:
+        E.M = old
+        E.graphs.clear()
+    assert len(out["bad"]) > 0
+    for I, reads, ids, sc in res:
+        assert np.array_equal(npy(I), out["I"])
+        assert np.array_equal(npy(reads), out["reads"])
+        assert np.array_equal(npy(ids), out["cand"])
+        assert np.allclose(npy(sc), out["scores"], rtol=1e-3)
+    for h in hs:
+        assert np.array_equal(h, out["I"])
+
+
+@pytest.mark.parametrize("B", [1, 64])
+def test_small_batch_buffer_equals_overflow_fallback(env, oracle_mod, B):
+    """Batches of at most 64 queries get a 65,536-entry emit buffer, so their queries do not overflow.
+    The results equal the oracle's with a K+8-entry buffer, where most queries overflow and are redone by
+    the fallback: the top-K of any emitted set with cnt >= K is the top-K of all probed rows."""
+    E = env["E"]
+    Q = env["Q"][:B].contiguous()
+    E.graphs.clear()
+    nb0 = E.nbad
+    I, reads, ids, sc = E.search(Q, K, Z_, NPROBE, KK, ret_scores=True)
+    torch.cuda.synchronize()
+    Qr, QC, QM, Zq = E._dense(Q)
+    out = oracle_mod.tr_pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, Qr=npy(Qr), QM16=u16(QM), Zq=npy(Zq),
+                                 M=K + 8)
+    assert E.nbad == nb0                       # no query of this set underflows
+    assert len(out["bad"]) >= (B + 1) // 2     # the oracle's buffer overflows for most queries
+    assert np.array_equal(npy(I), out["I"])
+    assert np.array_equal(npy(reads), out["reads"])
+    assert np.array_equal(npy(ids), out["cand"])
+    assert np.array_equal(npy(sc).view(np.uint32), out["scores"].view(np.uint32))
