@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
   const float s1 = fvs_h2f(scale1[(int64_t)rr - row0]);
   for (int i = 0; i < qn; i++) {
     const int pidx = qoff + i;
-    const int q = qid[pidx];
+    const int q = __builtin_amdgcn_readfirstlane(qid[pidx]);  // one query per wave and step
     const float4 *qv = reinterpret_cast<const float4 *>(Qr + (int64_t)q * kTrR + 128 * h);
     float acc = 0.f;
 #pragma unroll
@@ -199,9 +199,16 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
       for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, FVS_WAVE));
       if (lane == 0) bm[((int64_t)q * n1 + qrank[pidx]) * MB + (blk - cs / 32)] = m;
     } else {
-      if (h == 0 && valid && est >= t0[q]) {
-        const int idx = atomicAdd(&cnt[q], 1);
-        if (idx < CAP) {
+      // one counter update per wave: slot = base + rank of the lane among the passing lanes
+      const bool pass = h == 0 && valid && est >= t0[q];
+      const uint64_t m = __ballot(pass);
+      if (m) {
+        const int lead = __builtin_ctzll(m);
+        int base = 0;
+        if (lane == lead) base = atomicAdd(&cnt[q], __builtin_popcountll(m));
+        base = __builtin_amdgcn_readlane(base, lead);
+        const int idx = base + __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        if (pass && idx < CAP) {
           bval[(int64_t)q * CAP + idx] = est;
           bpos[(int64_t)q * CAP + idx] = r;
         }

@@ -139,7 +139,10 @@ class EngineS:
 
             g, outs = self._capture(run)
             self.graphs[key] = (key, g, qs, outs, hb)
-            self._fallback_graph(self.graphs[key], 1)  # a lone flagged query needs no capture later
+            # a lone flagged query needs no capture later. The fallback's warm-up runs read the main graph's
+            # static outputs (probe lists included), which a capture leaves unwritten: replay it first.
+            g.replay()
+            self._fallback_graph(self.graphs[key], 1)
         return self.graphs[key]
 
     def _fallback_graph(self, entry, nbp):
