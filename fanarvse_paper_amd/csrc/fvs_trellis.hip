@@ -148,7 +148,8 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
                                                  int32_t *__restrict__ cnt, float *__restrict__ bval,
                                                  int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
   __shared__ float stab[1 << kMaxL];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ float4 qbuf[4][kTrR / 4];  // per wave: the query vector of the current step
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int S = 1 << L;
   for (int i = tid; i < S; i += 256) stab[i] = tab[i];
   __syncthreads();
@@ -178,10 +179,21 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
     v[i] = stab[(uint32_t)(comb >> (64 - L - (i & 31))) & mask];
   }
   const float s1 = fvs_h2f(scale1[(int64_t)rr - row0]);
+  // The query vectors (kTrR floats = one float4 per lane) are read one step ahead and staged in LDS, so
+  // a step waits for one LDS round trip instead of a chain of global ones.
+  const float4 *Qr4 = reinterpret_cast<const float4 *>(Qr);
+  float4 nxt = Qr4[(int64_t)__builtin_amdgcn_readfirstlane(qid[qoff]) * (kTrR / 4) + lane];
   for (int i = 0; i < qn; i++) {
     const int pidx = qoff + i;
     const int q = __builtin_amdgcn_readfirstlane(qid[pidx]);  // one query per wave and step
-    const float4 *qv = reinterpret_cast<const float4 *>(Qr + (int64_t)q * kTrR + 128 * h);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the previous step's reads of qbuf are issued
+    __builtin_amdgcn_wave_barrier();
+    qbuf[w][lane] = nxt;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (i + 1 < qn) nxt = Qr4[(int64_t)__builtin_amdgcn_readfirstlane(qid[pidx + 1]) * (kTrR / 4) + lane];
+    const float4 *qv = &qbuf[w][32 * h];
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < 32; g++) {
