@@ -330,6 +330,140 @@ __global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave_f32(const
   }
 }
 
+// The same selection with one 1024-thread block per query, for small batches (fvs_route_topk_scaled when
+// NC % 8 == 0, NC <= 8192, n_p <= 1024 and B <= kRouteBlkMaxB). Thread t holds the keys of cells
+// [KPT t, KPT t + KPT) in registers; v* = the n_p-th largest key comes from an MSD radix select over
+// 8-bit digits with one LDS histogram per wave (so same-bucket atomics of different waves do not
+// collide), stopped early when the chosen bucket is taken whole; ties at v* are taken lowest cells first
+// by a block prefix sum in cell order. The n_p selected (key << 32 | ~cell) pairs are compacted into LDS
+// and each is stored at its rank among them (a count of the larger pairs).
+constexpr int kRouteBlk = 1024;
+constexpr int kRouteBlkMaxB = 256;
+
+template <int KPT, bool ADD>
+__global__ __launch_bounds__(kRouteBlk) void k_route_blk_f32(const uint16_t *__restrict__ QM,
+                                                            const float *__restrict__ scale,
+                                                            const float *__restrict__ qadd, int NC, int np,
+                                                            int32_t *__restrict__ probe) {
+  constexpr int NW = kRouteBlk / FVS_WAVE;
+  __shared__ int hist[NW][256];
+  __shared__ uint64_t s[1024];
+  __shared__ int wsum[NW];
+  __shared__ int sh[4];
+  const int tid = threadIdx.x, lane = tid & (FVS_WAVE - 1), wv = tid >> 6;
+  const int64_t q = blockIdx.x;
+  const int c0 = tid * KPT;
+  const float add = ADD ? qadd[q] : 0.f;
+
+  // 1. keys, computed as in k_route_f32; cells past NC get key 0 and are never selected
+  uint32_t k[KPT];
+  {
+    uint16_t hv[KPT];
+    float sc[KPT];
+    if (c0 < NC) {
+      if constexpr (KPT == 4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(QM + q * (int64_t)NC + c0);
+        const float4 f = *reinterpret_cast<const float4 *>(scale + c0);
+        hv[0] = (uint16_t)(v.x & 0xffffu); hv[1] = (uint16_t)(v.x >> 16);
+        hv[2] = (uint16_t)(v.y & 0xffffu); hv[3] = (uint16_t)(v.y >> 16);
+        sc[0] = f.x; sc[1] = f.y; sc[2] = f.z; sc[3] = f.w;
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4 *>(QM + q * (int64_t)NC + c0);
+        const float4 f0 = *reinterpret_cast<const float4 *>(scale + c0);
+        const float4 f1 = *reinterpret_cast<const float4 *>(scale + c0 + 4);
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) hv[e] = (uint16_t)((e & 1) ? (w4[e >> 1] >> 16) : (w4[e >> 1] & 0xffffu));
+        sc[0] = f0.x; sc[1] = f0.y; sc[2] = f0.z; sc[3] = f0.w;
+        sc[4] = f1.x; sc[5] = f1.y; sc[6] = f1.z; sc[7] = f1.w;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < KPT; e++) {
+      float x = c0 < NC ? fvs_h2f(hv[e]) : 0.f;
+      if (ADD) x = x + add;
+      x = x * (c0 < NC ? sc[e] : 0.f);
+      k[e] = c0 < NC ? fvs_ord32(x) : 0u;
+    }
+  }
+
+  // 2. radix select: after the loop, the selected keys are those with (key & mask) > prefix, plus, with
+  //    (key & mask) == prefix, all of them (whole) or the `want` lowest cells
+  uint32_t prefix = 0, mask = 0;
+  int want = np;
+  bool whole = false;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < NW * 256; i += kRouteBlk) (&hist[0][0])[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < KPT; e++)
+      if (c0 + e < NC && (k[e] & mask) == prefix) atomicAdd(&hist[wv][(k[e] >> shift) & 0xff], 1);
+    __syncthreads();
+    int h = 0, inc = 0;
+    if (tid < 256) {  // thread order = descending digit 255 - tid; waves 0..3
+#pragma unroll
+      for (int j = 0; j < NW; j++) h += hist[j][255 - tid];
+      inc = wave_incl_scan_i32(h, lane);
+      if (lane == FVS_WAVE - 1) wsum[wv] = inc;
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int before = 0;
+      for (int j = 0; j < wv; j++) before += wsum[j];
+      const int hi = before + inc, lo = hi - h;
+      if (lo < want && want <= hi) {
+        sh[0] = 255 - tid;
+        sh[1] = want - lo;
+        sh[2] = h;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sh[0] << shift;
+    mask |= 0xffu << shift;
+    want = sh[1];
+    whole = sh[2] == want;
+    if (whole) break;  // uniform: every thread read the same sh
+  }
+
+  // 3. ties in cell order (only when the last bucket is not taken whole)
+  int tie0 = 0;
+  if (!whole) {
+    int nt = 0;
+#pragma unroll
+    for (int e = 0; e < KPT; e++) nt += (c0 + e < NC && k[e] == prefix) ? 1 : 0;
+    const int inc = wave_incl_scan_i32(nt, lane);
+    if (lane == FVS_WAVE - 1) wsum[wv] = inc;
+    __syncthreads();
+    int before = 0;
+    for (int j = 0; j < wv; j++) before += wsum[j];
+    tie0 = before + inc - nt;
+  }
+
+  // 4. compaction
+  if (tid == 0) sh[3] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < KPT; e++) {
+    const uint32_t x = k[e] & mask;
+    const bool eq = c0 + e < NC && x == prefix;
+    const bool sel = c0 + e < NC && (x > prefix || (eq && (whole || tie0 < want)));
+    tie0 += (eq && !whole) ? 1 : 0;
+    if (sel) {
+      const int slot = atomicAdd(&sh[3], 1);  // exactly n_p <= 1024 keys are selected
+      if (slot < 1024) s[slot] = ((uint64_t)k[e] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(c0 + e));
+    }
+  }
+  __syncthreads();
+
+  // 5. rank of each selected pair among them (keys are unique), one pair per thread
+  if (tid < np) {
+    const uint64_t mine = s[tid];
+    int rank = 0;
+    for (int j = 0; j < np; j++) rank += s[j] > mine ? 1 : 0;  // one address per wave: a broadcast read
+    probe[q * (int64_t)np + rank] = (int32_t)(0xffffffffu - (uint32_t)(mine & 0xffffffffu));
+  }
+}
+
 template <int C, int R>
 int launch_route_wave_f32(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int NC, int np,
                           int32_t *probe, hipStream_t st) {
@@ -692,6 +826,17 @@ extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, con
   if (!QM || !scale || !probe) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
   if (NC % 8 == 0 && nprobe <= 1024 && ((reinterpret_cast<uintptr_t>(QM) | reinterpret_cast<uintptr_t>(scale)) & 15) == 0) {
+    if (B <= kRouteBlkMaxB) {
+      const dim3 g((unsigned)B), b(kRouteBlk);
+      if (NC <= 4096) {
+        if (qadd) hipLaunchKernelGGL((k_route_blk_f32<4, true>), g, b, 0, st, QM, scale, qadd, NC, nprobe, probe);
+        else hipLaunchKernelGGL((k_route_blk_f32<4, false>), g, b, 0, st, QM, scale, qadd, NC, nprobe, probe);
+      } else {
+        if (qadd) hipLaunchKernelGGL((k_route_blk_f32<8, true>), g, b, 0, st, QM, scale, qadd, NC, nprobe, probe);
+        else hipLaunchKernelGGL((k_route_blk_f32<8, false>), g, b, 0, st, QM, scale, qadd, NC, nprobe, probe);
+      }
+      return fvs_launch_status();
+    }
     if (NC <= 4096) return route_wave_f32_r<8>(QM, scale, qadd, B, NC, nprobe, probe, st);
     return route_wave_f32_r<16>(QM, scale, qadd, B, NC, nprobe, probe, st);
   }

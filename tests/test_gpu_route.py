@@ -3,7 +3,8 @@ ties at the n_p-th value (taken lowest cells first), +-0 (equal), +-inf, and eve
 launcher: the wave-per-query kernel for each (cells per lane, sorted keys per lane) instantiation and
 the block-per-query kernel for rows it does not take (NC not a multiple of 8, NC > 8192, n_p > 2048).
 Routing on fp32 keys (QM * scale, or (QM + qadd) * scale: the trellis engines) is checked the same way
-over its wave kernel (32-bit keys) and its block kernel. Results are bit-exact: the probe lists are
+over its three kernels: 1024 threads per query (small batches), one wave per query, and the block
+kernel for the rows neither takes. Results are bit-exact: the probe lists are
 sorted by (score desc, cell asc)."""
 import numpy as np
 import pytest
@@ -48,11 +49,11 @@ SCALED = [(64, 1), (64, 12), (104, 64), (520, 65), (1024, 128), (4096, 256), (40
           (4096, 1024), (4096, 1025), (8192, 1), (8192, 768), (8192, 1024), (100, 37), (4100, 300)]
 
 
+@pytest.mark.parametrize("B", [9, 300])    # the block-per-query kernel (small batches), the wave kernel
 @pytest.mark.parametrize("add", [False, True])
 @pytest.mark.parametrize("NC,npr", SCALED)
-def test_route_topk_scaled_matches_oracle(oracle_mod, NC, npr, add):
-    print(f"\n[gpu route scaled] NC={NC} nprobe={npr} qadd={add}", flush=True)
-    B = 9
+def test_route_topk_scaled_matches_oracle(oracle_mod, NC, npr, add, B):
+    print(f"\n[gpu route scaled] B={B} NC={NC} nprobe={npr} qadd={add}", flush=True)
     QM = rows(B, NC, NC * 5 + npr)
     rng = np.random.default_rng(npr)
     # repeated scales keep exact key ties; some zeros and negatives
