@@ -70,8 +70,13 @@ __device__ __forceinline__ float fvs_wave_max(float v) {
   return v;
 }
 
-// Inclusive prefix sum over threadIdx.x for a 256-thread block. tmp: 4 ints of LDS.
-__device__ __forceinline__ int fvs_block_scan256(int v, int *tmp) {
+// Ints of LDS the block helpers below need for their `sh` argument with NT threads: NT / 64 for the scan,
+// then three results.
+__host__ __device__ constexpr int fvs_sh_ints(int NT) { return NT / 64 + 4; }
+
+// Inclusive prefix sum over threadIdx.x for a block of NT threads (a multiple of 64). tmp: NT/64 ints.
+template <int NT = 256>
+__device__ __forceinline__ int fvs_block_scan(int v, int *tmp) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -85,33 +90,36 @@ __device__ __forceinline__ int fvs_block_scan256(int v, int *tmp) {
   __syncthreads();
   return v + add;
 }
+__device__ __forceinline__ int fvs_block_scan256(int v, int *tmp) { return fvs_block_scan<256>(v, tmp); }
 
 // k-th largest (1-based, counted with multiplicity) of n keys key(i), 1 <= k <= n, by an MSD radix
-// select of 8 bits per pass. Block of 256 threads; hist: 256 ints of LDS, sh: 8 ints of LDS.
-// Every thread returns the same key.
-template <typename KT, typename F>
+// select of 8 bits per pass. Block of NT >= 256 threads; hist: 256 ints of LDS, sh: fvs_sh_ints(NT)
+// ints of LDS. Every thread returns the same key.
+template <typename KT, int NT = 256, typename F>
 __device__ KT fvs_block_kth(F key, int n, int k, int *hist, int *sh) {
+  static_assert(NT >= 256 && NT % 64 == 0, "block of at least 256 threads");
+  constexpr int R = NT / 64;
   KT prefix = 0, pmask = 0;
   for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
-    hist[threadIdx.x] = 0;
+    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) {
+    for (int i = threadIdx.x; i < n; i += NT) {
       KT x = key(i);
       if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
     }
     __syncthreads();
     const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
-    const int h = hist[b];
-    const int inc = fvs_block_scan256(h, sh);
+    const int h = threadIdx.x < 256 ? hist[b] : 0;
+    const int inc = fvs_block_scan<NT>(h, sh);
     const int exc = inc - h;
-    if (exc < k && k <= inc) {
-      sh[4] = b;
-      sh[5] = k - exc;
+    if (threadIdx.x < 256 && exc < k && k <= inc) {
+      sh[R] = b;
+      sh[R + 1] = k - exc;
     }
     __syncthreads();
-    prefix |= (KT)sh[4] << shift;
+    prefix |= (KT)sh[R] << shift;
     pmask |= (KT)0xff << shift;
-    k = sh[5];
+    k = sh[R + 1];
     __syncthreads();
   }
   return prefix;
@@ -147,32 +155,34 @@ __host__ __device__ __forceinline__ int fvs_pow2_ceil(int n) {
 
 // A bound T with #{i : key(i) >= T} == kk for n UNIQUE keys, 1 <= kk <= n: the MSD radix select of
 // fvs_block_kth, stopped as soon as the chosen bucket holds exactly the keys still wanted (then every
-// key of the bucket is in and T is the bucket's smallest possible key). Block of 256 threads.
-template <typename KT, typename F>
+// key of the bucket is in and T is the bucket's smallest possible key). Block of NT >= 256 threads.
+template <typename KT, int NT = 256, typename F>
 __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
+  static_assert(NT >= 256 && NT % 64 == 0, "block of at least 256 threads");
+  constexpr int R = NT / 64;
   KT prefix = 0, pmask = 0;
   for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
-    hist[threadIdx.x] = 0;
+    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) {
+    for (int i = threadIdx.x; i < n; i += NT) {
       KT x = key(i);
       if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
     }
     __syncthreads();
     const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
-    const int h = hist[b];
-    const int inc = fvs_block_scan256(h, sh);
+    const int h = threadIdx.x < 256 ? hist[b] : 0;
+    const int inc = fvs_block_scan<NT>(h, sh);
     const int exc = inc - h;
-    if (exc < k && k <= inc) {
-      sh[4] = b;
-      sh[5] = k - exc;
-      sh[6] = h;
+    if (threadIdx.x < 256 && exc < k && k <= inc) {
+      sh[R] = b;
+      sh[R + 1] = k - exc;
+      sh[R + 2] = h;
     }
     __syncthreads();
-    prefix |= (KT)sh[4] << shift;
+    prefix |= (KT)sh[R] << shift;
     pmask |= (KT)0xff << shift;
-    k = sh[5];
-    const bool whole = sh[6] == k;
+    k = sh[R + 1];
+    const bool whole = sh[R + 2] == k;
     __syncthreads();
     if (whole) break;
   }
@@ -181,16 +191,16 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
 
 // Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
 // Requires kk <= n. The kk keys above the radix bound are gathered, then each is stored at its rank
-// among them (kk <= 128: a count of the larger keys; above, a bitonic sort, which measures faster
-// there). Block of 256 threads; cnt: 1 int of LDS.
-template <typename F>
+// among them: a count of the larger keys when kk <= 128 (256 threads) or kk <= NT (larger blocks), a
+// bitonic sort above, which measures faster there. Block of NT threads; cnt: 1 int of LDS.
+template <int NT = 256, typename F>
 __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
   const int P = fvs_pow2_ceil(kk);
-  const uint64_t kth = fvs_block_kth_set<uint64_t>(key, n, kk, hist, sh);
+  const uint64_t kth = fvs_block_kth_set<uint64_t, NT>(key, n, kk, hist, sh);
   if (threadIdx.x == 0) *cnt = 0;
-  for (int i = threadIdx.x; i < P; i += 256) s[i] = 0;
+  for (int i = threadIdx.x; i < P; i += NT) s[i] = 0;
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += 256) {
+  for (int i = threadIdx.x; i < n; i += NT) {
     const uint64_t x = key(i);
     if (x >= kth) {
       const int slot = atomicAdd(cnt, 1);
@@ -198,10 +208,11 @@ __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist,
     }
   }
   __syncthreads();
-  if (kk <= 128) {
+  if (kk <= (NT > 256 ? NT : 128)) {
     const uint64_t mine = threadIdx.x < kk ? s[threadIdx.x] : 0ull;
     int rank = 0;
-    for (int t = 0; t < kk; t++) rank += s[t] > mine ? 1 : 0;  // one address for every lane: a broadcast read
+    if (threadIdx.x < kk)
+      for (int t = 0; t < kk; t++) rank += s[t] > mine ? 1 : 0;  // one address for every lane: a broadcast read
     __syncthreads();
     if (threadIdx.x < kk) s[rank] = mine;
     __syncthreads();

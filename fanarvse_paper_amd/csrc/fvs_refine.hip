@@ -1,9 +1,9 @@
 // Error-bar classification, exact scoring of the ambiguous candidates and the final top-k.
 //
-// One block (4 waves) per query. est/sd are staged once into LDS as the lower/upper interval keys;
-// the two order statistics (k+1-th largest upper bound, k-th largest lower bound) come from radix
-// selects over LDS. Ambiguous slots and their ids are compacted in LDS and the waves take them in
-// groups of four rows, so four fp16 rows (coalesced 16-byte lane loads, from HBM or pinned host
+// One block (4 waves, or 16 for small batches) per query. est/sd are staged once into LDS as the
+// lower/upper interval keys; the two order statistics (k+1-th largest upper bound, k-th largest lower
+// bound) come from radix selects over LDS. Ambiguous slots and their ids are compacted in LDS and the
+// waves take them in groups of four rows, so four fp16 rows (coalesced 16-byte lane loads, from HBM or pinned host
 // memory over PCIe) are in flight per wave; each lane keeps its slice of the query in registers,
 // and every row's partial sums are reduced with the same fixed butterfly.
 #include "fvs_common.h"
@@ -14,11 +14,12 @@ constexpr int kMaxK = 4096;
 constexpr int kMaxk = 1024;
 constexpr int kRows = 4;       // rows in flight per wave
 constexpr int kMaxG = 8;       // 8-element groups per lane: d <= 8 * 64 * kMaxG = 4096
+constexpr int kSmallB = 64;    // batches up to this size use 1024-thread blocks
 
 struct RefineLds {  // fixed part; the per-slot arrays follow in dynamic LDS
   uint64_t s[kMaxk];
   int hist[256];
-  int sh[8];
+  int sh[fvs_sh_ints(1024)];
   int namb, gcnt;
 };
 
@@ -58,8 +59,8 @@ __device__ __forceinline__ void dot_rows(const uint16_t *__restrict__ H, int d, 
   }
 }
 
-template <int NG>
-__global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, const float *__restrict__ sd,
+template <int NG, int NT>
+__global__ __launch_bounds__(NT) void k_refine(const float *__restrict__ est, const float *__restrict__ sd,
                                                 const int32_t *__restrict__ pos, const int32_t *__restrict__ order,
                                                 const uint16_t *__restrict__ H, const float *__restrict__ Q, int K,
                                                 int d, float z, int k, int32_t *__restrict__ ids,
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, c
   const float *e = est + q * (int64_t)K;
   const float *g = sd + q * (int64_t)K;
   const int32_t *pq = pos + q * (int64_t)K;
-  for (int i = tid; i < K; i += 256) {
+  for (int i = tid; i < K; i += NT) {
     const float t = z * g[i];
     lo[i] = e[i] - t;
     hi[i] = e[i] + t;
@@ -90,9 +91,9 @@ __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, c
   }
   if (tid == 0) L.namb = 0;
   __syncthreads();
-  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(hi[i]); }, K, k + 1, L.hist, L.sh));
-  const float lk = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(lo[i]); }, K, k, L.hist, L.sh));
-  for (int i = tid; i < K; i += 256) {
+  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t, NT>([&](int i) { return fvs_ord32(hi[i]); }, K, k + 1, L.hist, L.sh));
+  const float lk = fvs_unord32(fvs_block_kth<uint32_t, NT>([&](int i) { return fvs_ord32(lo[i]); }, K, k, L.hist, L.sh));
+  for (int i = tid; i < K; i += NT) {
     const bool sure = lo[i] > hk1;
     const bool am = (hi[i] >= lk) && !sure;
     flag[i] = sure ? 1 : (am ? 2 : 0);
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, c
 #pragma unroll
       for (int u = 0; u < 8; u++) qv[gg][u] = gi * 8 < d ? qr[gi * 8 + u] : 0.f;
     }
-    for (int a0 = w * kRows; a0 < na; a0 += 4 * kRows) dot_rows<NG>(H, d, aid, amb, a0, na, qv, score, lane);
+    for (int a0 = w * kRows; a0 < na; a0 += (NT / 64) * kRows) dot_rows<NG>(H, d, aid, amb, a0, na, qv, score, lane);
   }
   __syncthreads();
   if (tid == 0) reads[q] = na;
@@ -126,8 +127,8 @@ __global__ __launch_bounds__(256) void k_refine(const float *__restrict__ est, c
   auto key = [&](int i) -> uint64_t {
     return ((uint64_t)fvs_ord32(score[i]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   };
-  fvs_block_topk_u64(key, K, k, L.s, L.hist, L.sh, &L.gcnt);
-  for (int j = tid; j < k; j += 256) {
+  fvs_block_topk_u64<NT>(key, K, k, L.s, L.hist, L.sh, &L.gcnt);
+  for (int j = tid; j < k; j += NT) {
     const int slot = (int)(0xffffffffu - (uint32_t)(L.s[j] & 0xffffffffu));
     Iout[q * (int64_t)k + j] = sid[slot];
     scores[q * (int64_t)k + j] = flag[slot] == 1 ? e[slot] : score[slot];
@@ -146,19 +147,23 @@ extern "C" int fvs_refine(const float *est, const float *sd, const int32_t *pos,
   const size_t shm = (size_t)K * (4 * 5 + 2 + 1);
   hipStream_t st = (hipStream_t)stream;
   const int ng = (d / 8 + 63) / 64;
-#define FVS_REFINE_LAUNCH(NG)                                                                                     \
-  hipLaunchKernelGGL(k_refine<NG>, dim3((unsigned)B), dim3(256), shm, st, est, sd, pos, order, H, Q, K, d, z, k, ids, \
-                     I, scores, reads)
-  if (ng <= 1)
-    FVS_REFINE_LAUNCH(1);
-  else if (ng <= 2)
-    FVS_REFINE_LAUNCH(2);
-  else if (ng <= 3)
-    FVS_REFINE_LAUNCH(3);
-  else if (ng <= 4)
-    FVS_REFINE_LAUNCH(4);
-  else
-    FVS_REFINE_LAUNCH(8);
+  // batches of at most kSmallB queries: 1024 threads per query (16 waves, 64 rows in flight) when the
+  // query slice fits the 128 registers a thread of such a block has (d <= 1536)
+  const bool big = B <= kSmallB && ng <= 3;
+#define FVS_REFINE_LAUNCH(NG, NT)                                                                                \
+  hipLaunchKernelGGL((k_refine<NG, NT>), dim3((unsigned)B), dim3(NT), shm, st, est, sd, pos, order, H, Q, K, d, z, k, \
+                     ids, I, scores, reads)
+  if (ng <= 1) {
+    if (big) FVS_REFINE_LAUNCH(1, 1024); else FVS_REFINE_LAUNCH(1, 256);
+  } else if (ng <= 2) {
+    if (big) FVS_REFINE_LAUNCH(2, 1024); else FVS_REFINE_LAUNCH(2, 256);
+  } else if (ng <= 3) {
+    if (big) FVS_REFINE_LAUNCH(3, 1024); else FVS_REFINE_LAUNCH(3, 256);
+  } else if (ng <= 4) {
+    FVS_REFINE_LAUNCH(4, 256);
+  } else {
+    FVS_REFINE_LAUNCH(8, 256);
+  }
 #undef FVS_REFINE_LAUNCH
   return fvs_launch_status();
 }

@@ -11,24 +11,29 @@ __device__ __forceinline__ int cell_blocks(const int32_t *off, int c) {
   return e > s ? (e - 1) / 32 - s / 32 + 1 : 0;
 }
 
-// One block per query. Valid values: bm[q][j][b], j < n1, b < blocks(probe[q][j]).
-__global__ __launch_bounds__(256) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
-                                                   int npr, const int32_t *__restrict__ off, int n1, int MB, int r,
-                                                   float *__restrict__ t0) {
+// Batches of at most kSmallB queries run the per-query kernels below with 1024 threads per block: a batch
+// of one query then spreads its radix passes over 16 waves instead of 4.
+constexpr int kSmallB = 64;
+
+// One block of NT threads per query. Valid values: bm[q][j][b], j < n1, b < blocks(probe[q][j]).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
+                                                  int npr, const int32_t *__restrict__ off, int n1, int MB, int r,
+                                                  float *__restrict__ t0) {
   __shared__ int nb[kMaxN1];
   __shared__ int hist[256];
-  __shared__ int sh[8];
+  __shared__ int sh[fvs_sh_ints(NT)];
   const int64_t q = blockIdx.x;
   int mine = 0;
-  for (int j = threadIdx.x; j < n1; j += 256) {
+  for (int j = threadIdx.x; j < n1; j += NT) {
     nb[j] = cell_blocks(off, probe[q * npr + j]);
     mine += nb[j];
   }
   // block sum of the valid counts
-  const int tot = fvs_block_scan256(mine, sh);
-  if (threadIdx.x == 255) sh[6] = tot;
+  const int tot = fvs_block_scan<NT>(mine, sh);
+  if (threadIdx.x == NT - 1) sh[NT / 64 + 2] = tot;
   __syncthreads();
-  const int nv = sh[6];
+  const int nv = sh[NT / 64 + 2];
   __syncthreads();
   const int n = n1 * MB;
   const float *row = bm + q * (int64_t)n;
@@ -38,7 +43,7 @@ __global__ __launch_bounds__(256) void k_threshold(const float *__restrict__ bm,
   };
   const int kk = min(min(r, n), nv);
   float out = 1e30f;
-  if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t>(key, n, kk, hist, sh));
+  if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t, NT>(key, n, kk, hist, sh));
   if (threadIdx.x == 0) t0[q] = out;
 }
 
@@ -47,7 +52,8 @@ __global__ __launch_bounds__(256) void k_threshold(const float *__restrict__ bm,
 // radix passes run over LDS; larger ones (the fallback's 65,536-entry buffers) are read from global.
 constexpr int kStage = 4096;
 
-__global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, const int32_t *__restrict__ bpos,
+template <int NT>
+__global__ __launch_bounds__(NT) void k_select(const float *__restrict__ bval, const int32_t *__restrict__ bpos,
                                                 const int32_t *__restrict__ cntp, int M, int K, int kd, float delta,
                                                 int32_t *__restrict__ pos, float *__restrict__ est1,
                                                 uint8_t *__restrict__ ok, int32_t *__restrict__ ncnt) {
@@ -56,7 +62,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, 
   uint64_t *s = dyn64;           // [P] the sorted top-K
   uint64_t *keys = dyn64 + P;    // [min(M, kStage)] staged buffer
   __shared__ int hist[256];
-  __shared__ int sh[8];
+  __shared__ int sh[fvs_sh_ints(NT)];
   __shared__ int gcnt;
   const int64_t q = blockIdx.x;
   const int cq = cntp[q];
@@ -73,7 +79,7 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, 
       const float4 *bv4 = reinterpret_cast<const float4 *>(bv);
       const int4 *bp4 = reinterpret_cast<const int4 *>(bp);
 #pragma unroll 4
-      for (int i = threadIdx.x; i < (n + 3) / 4; i += 256) {
+      for (int i = threadIdx.x; i < (n + 3) / 4; i += NT) {
         const float4 v = bv4[i];
         const int4 p = bp4[i];
         const float vv[4] = {v.x, v.y, v.z, v.w};
@@ -83,27 +89,27 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, 
           if (4 * i + u < n) keys[4 * i + u] = ((uint64_t)fvs_ord32(vv[u]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)pp[u]);
       }
     } else {
-      for (int i = threadIdx.x; i < n; i += 256) keys[i] = gkey(i);
+      for (int i = threadIdx.x; i < n; i += NT) keys[i] = gkey(i);
     }
     __syncthreads();
   }
   int have;
   if (n >= K) {
     if (staged)
-      fvs_block_topk_u64([&](int i) { return keys[i]; }, n, K, s, hist, sh, &gcnt);
+      fvs_block_topk_u64<NT>([&](int i) { return keys[i]; }, n, K, s, hist, sh, &gcnt);
     else
-      fvs_block_topk_u64(gkey, n, K, s, hist, sh, &gcnt);
+      fvs_block_topk_u64<NT>(gkey, n, K, s, hist, sh, &gcnt);
     have = K;
   } else {
     const int Pn = fvs_pow2_ceil(n > 0 ? n : 1);
-    for (int i = threadIdx.x; i < Pn; i += 256) s[i] = i < n ? (staged ? keys[i] : gkey(i)) : 0ull;
+    for (int i = threadIdx.x; i < Pn; i += NT) s[i] = i < n ? (staged ? keys[i] : gkey(i)) : 0ull;
     __syncthreads();
     fvs_block_bitonic<uint64_t, true>(s, Pn);
     have = n;
   }
   float *e1 = est1 + q * (int64_t)K;
   int32_t *po = pos + q * (int64_t)K;
-  for (int i = threadIdx.x; i < K; i += 256) {
+  for (int i = threadIdx.x; i < K; i += NT) {
     if (i < have) {
       const uint64_t x = s[i];
       e1[i] = fvs_unord32((uint32_t)(x >> 32));
@@ -118,9 +124,9 @@ __global__ __launch_bounds__(256) void k_select(const float *__restrict__ bval, 
     auto est_at = [&](int i) -> float { return i < have ? fvs_unord32((uint32_t)(s[i] >> 32)) : -1e30f; };
     const float thr = est_at(kd) - delta;
     int mine = 0;
-    for (int i = threadIdx.x; i < K; i += 256) mine += (est_at(i) >= thr) ? 1 : 0;
-    const int tot = fvs_block_scan256(mine, sh);
-    if (threadIdx.x == 255) ncnt[q] = tot;
+    for (int i = threadIdx.x; i < K; i += NT) mine += (est_at(i) >= thr) ? 1 : 0;
+    const int tot = fvs_block_scan<NT>(mine, sh);
+    if (threadIdx.x == NT - 1) ncnt[q] = tot;
   } else if (threadIdx.x == 0) {
     ncnt[q] = K;
   }
@@ -135,8 +141,12 @@ extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr,
   if ((int64_t)n1 * MB > (int64_t)1 << 30) return FVS_E_ARG;
   if (B == 0) return FVS_OK;
   if (!bm || !probe || !off || !t0) return FVS_E_ARG;
-  hipLaunchKernelGGL(k_threshold, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, n1, MB, r,
-                     t0);
+  if (B <= kSmallB)
+    hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
+                       MB, r, t0);
+  else
+    hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
+                       MB, r, t0);
   return fvs_launch_status();
 }
 
@@ -148,7 +158,11 @@ extern "C" int fvs_select(const float *bval, const int32_t *bpos, const int32_t 
   if (B == 0) return FVS_OK;
   if (!bval || !bpos || !cnt || !pos || !est1 || !ok || !ncnt) return FVS_E_ARG;
   const size_t shm = 8 * ((size_t)fvs_pow2_ceil(K) + (size_t)(M < kStage ? M : kStage));
-  hipLaunchKernelGGL(k_select, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, bval, bpos, cnt, M, K, kd,
-                     delta, pos, est1, ok, ncnt);
+  if (B <= kSmallB)
+    hipLaunchKernelGGL(k_select<1024>, dim3((unsigned)B), dim3(1024), shm, (hipStream_t)stream, bval, bpos, cnt, M, K,
+                       kd, delta, pos, est1, ok, ncnt);
+  else
+    hipLaunchKernelGGL(k_select<256>, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, bval, bpos, cnt, M, K,
+                       kd, delta, pos, est1, ok, ncnt);
   return fvs_launch_status();
 }

@@ -32,10 +32,10 @@ def buffers(B, M, K, seed):
     return bval, bpos, cnt
 
 
+@pytest.mark.parametrize("B", [37, 80])     # 1024-thread blocks (batches <= 64), 256-thread blocks
 @pytest.mark.parametrize("K,M", CASES)
-def test_select_matches_oracle(oracle_mod, K, M):
-    print(f"\n[gpu select] K={K} M={M}", flush=True)
-    B = 37
+def test_select_matches_oracle(oracle_mod, K, M, B):
+    print(f"\n[gpu select] B={B} K={K} M={M}", flush=True)
     bval, bpos, cnt = buffers(B, M, K, K * 13 + M)
     for kd, delta in ((0, None), (min(9, K - 1), 0.07)):
         got = _lib.select(torch.from_numpy(bval).cuda(), torch.from_numpy(bpos).cuda(), torch.from_numpy(cnt).cuda(),
