@@ -28,12 +28,7 @@ from .enginei8 import _fresh
 
 class EngineS:
     BN = 32
-    M = None          # emit buffer size; None = max(4096, 16 K) (src/s1cell.py:180), or M_SMALL for small batches
-    # Batches of at most SMALL_B queries get a 65,536-entry emit buffer, the size of the fallback's. Results
-    # are unchanged: a query that emits cnt >= K candidates above its threshold t0 holds the global top-K
-    # (by estimate, then position) of its probed rows whatever t0 was, so the reference's overflow fallback
-    # returns the same top-K; only the second stage-1 pass is saved. Underflows (cnt < K) still fall back.
-    M_SMALL, SMALL_B = 65536, 64
+    M = None          # emit buffer size; None = index.emit_buffer(B, K)
 
     def __init__(self, s1, code, H=None):
         self.s1, self.code, self.H = s1, code, H
@@ -52,7 +47,7 @@ class EngineS:
     def _params(self, K, nprobe, rho_override=None, M_override=None, B=None):
         NC = len(self.s1["off"]) - 1
         N = self.s1["words"].shape[0]
-        M = M_override or self.M or (self.M_SMALL if B is not None and B <= self.SMALL_B else max(4096, 16 * K))
+        M = M_override or self.M or index.emit_buffer(B, K)
         beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
         if rho_override:
             beta, rho = 1.5, rho_override

@@ -69,7 +69,9 @@ class SpaceX(EngineS):
 
     def _params(self, K, nprobe, rho_override=None, M_override=None):
         NC = len(self.s1["off"]) - 1
-        M = M_override or self.M or max(4096, 16 * K)
+        # the reference's size: at batch 2000 a larger buffer (index.emit_buffer) avoids most overflow
+        # fallbacks but measured no faster, the batch being bound by the zero-copy stage-2 reads
+        M = M_override or self.M or index.emit_buffer(None, K)
         beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
         if rho_override:
             beta, rho = 1.5, rho_override

@@ -74,6 +74,19 @@ def build_codes(s1, X16, Vr):
     return _lib.build_codes(X16, s1["order"], s1["cell"], s1["means16"], Vr.contiguous())
 
 
+def emit_buffer(B, K, budget=1 << 29):
+    """Emit buffer entries per query of the trellis engines' stage 1: the reference's max(4096, 16 K)
+    (src/s1cell.py:180), raised towards the fallback's 65,536 while B * M * 8 bytes stay within `budget`.
+    Results do not depend on it: a query that emits cnt >= K candidates above its threshold t0 holds the
+    top-K (by estimate, then position) of all its probed rows, whatever t0 was, so the fallback the
+    reference runs for an overflowing query (cnt > M) returns the same top-K. A larger buffer only saves
+    that second stage-1 pass; underflows (cnt < K) still take it. B=None: the reference's size."""
+    ref = max(4096, 16 * K)
+    if B is None or B <= 0:
+        return ref
+    return max(ref, min(65536, budget // (8 * B)))
+
+
 def static_blocks(off_t, BN=32):
     """All (cell, block) items of the index: cell, global block id, cell start and end, and MB = max blocks
     per cell + 1 (src/s1cell.py:161-168)."""

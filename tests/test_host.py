@@ -121,3 +121,15 @@ def test_generator_properties():
     assert np.allclose(Rm @ Rm.T, np.eye(64), atol=1e-5)
     GT = datagen.ground_truth(X, X[:5].float(), 3)
     assert GT[:, 0].tolist() == list(range(5))
+
+
+def test_emit_buffer_rule():
+    """The trellis engines' emit buffer: the reference's max(4096, 16 K) without a batch size, raised
+    towards 65,536 entries while the batch's buffers stay within 512 MB."""
+    from fanarvse_paper_amd.index import emit_buffer
+
+    assert emit_buffer(None, 200) == 4096 and emit_buffer(None, 400) == 6400
+    assert emit_buffer(1, 200) == emit_buffer(1024, 200) == 65536
+    assert emit_buffer(2000, 200) == (1 << 29) // 16000
+    assert emit_buffer(1 << 20, 400) == 6400            # never below the reference's size
+    assert emit_buffer(2000, 5000) == 80000             # nor capped below it for large K
