@@ -49,10 +49,12 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("throughput", "latency", "host", "largek"), default="throughput",
+    ap.add_argument("--mode", choices=("throughput", "latency", "host", "largek", "tier"), default="throughput",
                     help="throughput: the headline config (EngineI8, batch 2000); latency: the trellis default "
                          "engine at batches 1/16/64 (BASELINE.json configs[2]); host: the host-resident engine "
-                         "(configs[4]); largek: k=100 with the z sweep (configs[3])")
+                         "(configs[4]); largek: k=100 with the z sweep (configs[3]); tier: the default engine with "
+                         "its fp16 rows in a file on the local drive (the reference's NVMe tier)")
+    ap.add_argument("--tier-dir", default=None, help="directory of the tier file (default: $TMPDIR or /tmp)")
     ap.add_argument("--lat-points", default="256:200,384:400", help="n_p:K points of the latency mode")
     ap.add_argument("--lat-batches", default="1,16,64")
     ap.add_argument("--lat-z", default="1.5,2,3")
@@ -80,6 +82,8 @@ def main():
         return latency_mode(args)
     if args.mode == "host":
         return host_mode(args)
+    if args.mode == "tier":
+        return tier_mode(args)
     if args.mode == "largek":
         return largek_mode(args)
     _lib.lib()
@@ -359,6 +363,88 @@ def latency_mode(args):
                                   f"k={args.k}", "nlist": args.nlist, "build_s": round(build_s, 1),
                       "gpu_bytes_per_vector": round(E.gpu_bytes(), 1)},
            "rows": rows}
+    print(json.dumps(out), flush=True)
+
+
+def tier_mode(args):
+    """The default engine with its fp16 rows on the local drive instead of in HBM (the reference's NVMe
+    tier, src/engine3.py:204-233): the 1M x 1536 set of the latency mode written as a tier file (4096-byte
+    row slots), read with O_DIRECT through io_uring or the pread pool. Reports the reader's random-read
+    rate at several queue depths, then batch-1 latency and pipelined batch-500 throughput of
+    EngineSTier next to EngineS with the same rows in HBM."""
+    import numpy as np
+    import torch
+
+    from fanarvse_paper_amd import datagen, metrics, tier, trellis
+    from fanarvse_paper_amd.engine_cell import EngineS
+    from fanarvse_paper_amd.engine_tier import EngineSTier
+
+    dev = "cuda"
+    X = datagen.gen(args.n, args.d, args.clusters, 0.7, seed=0, device=dev)
+    Q = datagen.gen(2000, args.d, args.clusters, 0.7, seed=1, device=dev, dtype=torch.float32)
+    GT = datagen.ground_truth(X, Q, args.k).cpu().numpy()
+    s1, code = trellis.build_index(X, nlist=args.nlist)
+    torch.cuda.synchronize()
+    d = args.tier_dir or os.environ.get("TMPDIR", "/tmp")
+    path = os.path.join(d, f"fvs_tier_{os.getpid()}.bin")
+    t = time.time()
+    stride = tier.write_tier(path, X)
+    os.sync()
+    log(f"tier file {path}: {os.path.getsize(path) / 1e9:.2f} GB written in {time.time() - t:.1f}s")
+    rows = []
+    try:
+        rng = np.random.default_rng(0)
+        ids = rng.integers(0, args.n, 100_000)
+        reader = []
+        for backend in (None, "threads"):
+            for qd in (32, 128, 512):
+                with tier.RowTier(path, args.d, qd=qd, backend=backend) as T:
+                    out = np.empty((len(ids), args.d), np.float16)
+                    T.read_into(ids[:2000], out[:2000])
+                    t = time.perf_counter()
+                    T.read_into(ids, out)
+                    dt = time.perf_counter() - t
+                    reader.append(dict(backend=T.backend, qd=qd, rows_per_s=round(len(ids) / dt),
+                                       GBps=round(len(ids) * stride / dt / 1e9, 3)))
+                    log(f"reader {reader[-1]}")
+        E = EngineS(s1, code, H=X)
+        for p in args.lat_points.split(","):
+            nprobe, K = (int(v) for v in p.split(":"))
+            z = 2.0
+            with tier.RowTier(path, args.d, qd=128) as T:
+                Et = EngineSTier(s1, code, T)
+                I, reads, _ = Et.run(Q, K, z, nprobe, args.k, B=500)  # warm-up and recall
+                rec = metrics.recall(I, GT, args.k)
+                t = time.perf_counter()
+                Et.run(Q, K, z, nprobe, args.k, B=500)
+                qps = 2000 / (time.perf_counter() - t)
+                lat = []
+                for i in range(203):
+                    torch.cuda.synchronize()
+                    t = time.perf_counter()
+                    Et.search_host(Q[i:i + 1], K, z, nprobe, args.k)
+                    lat.append(time.perf_counter() - t)
+                lat = np.array(lat[3:]) * 1e3
+                lh = []
+                for i in range(203):
+                    torch.cuda.synchronize()
+                    t = time.perf_counter()
+                    E.search_host(Q[i:i + 1], K, z, nprobe, args.k)
+                    lh.append(time.perf_counter() - t)
+                lh = np.array(lh[3:]) * 1e3
+                row = dict(nprobe=nprobe, K=K, z=z, recall=rec, backend=T.backend, reads_per_query=float(reads.mean()),
+                           run_qps_B500=round(qps, 1), B1_median_ms=round(float(np.median(lat)), 3),
+                           B1_p99_ms=round(float(np.percentile(lat, 99)), 3),
+                           hbm_B1_median_ms=round(float(np.median(lh)), 3),
+                           hbm_B1_p99_ms=round(float(np.percentile(lh, 99)), 3))
+                rows.append(row)
+                log(f"tier {row}")
+    finally:
+        os.remove(path)
+    out = {"metric": "NVMe row tier: random-read rate of the reader, and search with the fp16 rows on the drive",
+           "unit": "queries/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"row tier, {args.n}x{args.d} fp16 synthetic, tier file of {stride}-byte slots",
+                      "k": args.k}, "reader": reader, "rows": rows}
     print(json.dumps(out), flush=True)
 
 

@@ -36,6 +36,8 @@ SIGNATURES = {
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
     "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
+    "fvs_classify": [P, P, P, P, I64, I32, F32, I32, P, P, P, P, P],
+    "fvs_refine_rows": [P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "fvs_trellis_encode": [P, P, I64, I32, P, I32, P, I32, P, P, P],
     "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, I32, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_route_topk_scaled": [P, P, P, I64, I32, I32, P, P],
@@ -313,6 +315,44 @@ def refine(est, sd, pos, order, H, Q, z, k):
                             _dev(scores, torch.float32, "scores"), _dev(reads, torch.int32, "reads"), _stream()),
            "fvs_refine")
     return ids, I, scores, reads
+
+
+def classify(est, sd, pos, order, z, k):
+    """(ids [B,K], flag u8 [B,K], namb [B], aslot [B,K]): the first half of refine for rows read by the
+    host (src/engine3.py:204-216): flags 1 sure / 2 ambiguous, ambiguous slots in ascending order
+    (entries of aslot past namb are 0)."""
+    B, K = est.shape
+    dev = est.device
+    ids = _empty((B, K), torch.int32, dev)
+    flag = _empty((B, K), torch.uint8, dev)
+    namb = _empty((B,), torch.int32, dev)
+    aslot = torch.zeros((B, K), dtype=torch.int32, device=dev)  # entries past namb stay 0 (a valid slot)
+    _check(lib().fvs_classify(_dev(est, torch.float32, "est"), _dev(sd, torch.float32, "sd", (B, K)),
+                              _dev(pos, torch.int32, "pos", (B, K)), _opt(order, torch.int32, "order"), B, K, F32(z), k,
+                              _dev(ids, torch.int32, "ids"), _dev(flag, torch.uint8, "flag"),
+                              _dev(namb, torch.int32, "namb"), _dev(aslot, torch.int32, "aslot"), _stream()),
+           "fvs_classify")
+    return ids, flag, namb, aslot
+
+
+def refine_rows(est, flag, aslot, namb, roff, ids, rows, Q, k):
+    """(I [B,k], scores [B,k], reads [B]): the second half (src/engine3.py:218-223): exact scores of the
+    ambiguous slots from rows [sum namb, d] fp16 (device or pinned host), query q's at roff[q] + j."""
+    B, K = est.shape
+    d = Q.shape[1]
+    if rows.dim() != 2 or rows.shape[1] != d:
+        raise ValueError("refine_rows: rows width")
+    dev = est.device
+    I = _empty((B, k), torch.int32, dev)
+    scores = _empty((B, k), torch.float32, dev)
+    reads = _empty((B,), torch.int32, dev)
+    _check(lib().fvs_refine_rows(_dev(est, torch.float32, "est"), _dev(flag, torch.uint8, "flag", (B, K)),
+                                 _dev(aslot, torch.int32, "aslot", (B, K)), _dev(namb, torch.int32, "namb", (B,)),
+                                 _dev(roff, torch.int64, "roff", (B,)), _dev(ids, torch.int32, "ids", (B, K)),
+                                 _dev(rows, torch.float16, "rows", host_ok=True), _dev(Q, torch.float32, "Q", (B, d)),
+                                 B, K, d, k, _dev(I, torch.int32, "I"), _dev(scores, torch.float32, "scores"),
+                                 _dev(reads, torch.int32, "reads"), _stream()), "fvs_refine_rows")
+    return I, scores, reads
 
 
 # ------------------------------------------------------------------------------ trellis engine

@@ -1,4 +1,5 @@
-"""Build libfvs.so (the gfx950 HIP kernels behind include/fvs.h) in-tree with hipcc.
+"""Build libfvs.so (the gfx950 HIP kernels behind include/fvs.h) in-tree with hipcc, and the host-only
+row tier reader libfvs_tier.so (include/fvs_tier.h) with the host compiler.
 
 Each .hip translation unit is compiled to an object in parallel, then linked into
 fanarvse_paper_amd/libfvs.so. Floating-point contraction is disabled (every fma in the kernels is
@@ -25,8 +26,24 @@ FLAGS = [
 ]
 
 
+TIER_SRC = os.path.join(CSRC, "fvs_tier.cpp")
+TIER_LIB = os.path.join(HERE, "libfvs_tier.so")
+CXX = os.environ.get("CXX", "g++")
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build_tier():
+    """The host-only row tier reader (include/fvs_tier.h) with the host compiler."""
+    tmp = TIER_LIB + ".tmp"
+    r = subprocess.run([CXX, "-O2", "-std=c++17", "-Wall", "-fPIC", "-shared", TIER_SRC, "-o", tmp, "-lpthread"],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{CXX} failed for {TIER_SRC}:\n{r.stderr}")
+    os.replace(tmp, TIER_LIB)
+    return TIER_LIB
 
 
 def _compile(src):
@@ -50,8 +67,9 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_tier()
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources, and {TIER_LIB}")
     return LIB
 
 

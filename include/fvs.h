@@ -202,6 +202,21 @@ int fvs_refine(const float *est, const float *sd, const int32_t *pos, const int3
                const float *Q, int64_t B, int32_t K, int32_t d, float z, int32_t k, int32_t *ids, int32_t *I,
                float *scores, int32_t *reads, void *stream);
 
+/*
+ * Stage 3 split for rows outside GPU-visible memory (the NVMe row tier of the reference's Engine12,
+ * src/engine3.py:204-233, which classifies on the GPU, reads the ambiguous rows with its asynchronous
+ * reader and scores them). Together the two calls give the results of fvs_refine over the same rows.
+ * fvs_classify: ids [B,K] (order[pos] or pos), flag u8 [B,K] (1 sure, 2 ambiguous, 0 neither, by the
+ *   bounds of fvs_refine), namb [B], aslot [B,K]: the ambiguous slots in ascending slot order.
+ * fvs_refine_rows: rows fp16 [sum namb, d] (device or pinned host) hold the row of ambiguous slot
+ *   aslot[q][j] at roff[q] + j (roff i64 [B]); outputs I, scores, reads as fvs_refine.
+ */
+int fvs_classify(const float *est, const float *sd, const int32_t *pos, const int32_t *order, int64_t B, int32_t K,
+                 float z, int32_t k, int32_t *ids, uint8_t *flag, int32_t *namb, int32_t *aslot, void *stream);
+int fvs_refine_rows(const float *est, const uint8_t *flag, const int32_t *aslot, const int32_t *namb,
+                    const int64_t *roff, const int32_t *ids, const uint16_t *rows, const float *Q, int64_t B,
+                    int32_t K, int32_t d, int32_t k, int32_t *I, float *scores, int32_t *reads, void *stream);
+
 /* ============================================================ trellis engine (latency mode)
  * The default engine of the reference (src/engine_cell.py:70-102 EngineS, src/engine3.py:135-175 Engine8):
  * cell-residual bitshift-trellis codes in stage 1 and the Lloyd-Max tiered code in stage 2. */
