@@ -138,18 +138,23 @@ class EngineI8:
         s1 = self.s1
         qp = _lib.query_prep(Qb, self.Vr, s1["c"])
         q8, qs, QC, Qh, zq = qp
-        # the stage-2 tables depend only on the fp16 queries: a side stream builds them while stage 1 runs
+        # the stage-2 tables depend only on the fp16 queries: a side stream builds them while stage 1 runs.
+        # The routing product is issued before the side branch: it heads the critical path, and a branch
+        # issued ahead of it was measured to hold it back until the branch's first node had finished.
         main = torch.cuda.current_stream()
         if self._side is None:
             self._side = torch.cuda.Stream(device=Qb.device)
-        self._side.wait_stream(main)
+        prepped = torch.cuda.Event()
+        prepped.record(main)
+        QM = Qh @ self.meansN.T
+        self._side.wait_event(prepped)
         half = self.LUTF and self.LUTH
         with torch.cuda.stream(self._side):
             Zq = s2lut.rotate(self.code, Qh)
             pre = _lib.lut_build(Zq, self.code["TS"], half)
         for t in (Zq, *pre):  # made on the side stream, used on this one
             t.record_stream(main)
-        QM, probe = self._route(Qh, nprobe)
+        probe = _lib.route_topk(QM, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         main.wait_stream(self._side)
         ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=half,
