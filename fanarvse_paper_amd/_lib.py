@@ -31,7 +31,7 @@ SIGNATURES = {
     "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
-    "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P],
+    "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
@@ -232,12 +232,13 @@ def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=
                              _stream()), "fvs_i8_scan")
 
 
-def threshold(bm, probe, off, n1, MB, r):
+def threshold(bm, probe, off, n1, MB, r, cnt=None):
+    """t0 [B] from the first-pass block maxima; with cnt, also zeroes the emit pass's counters."""
     B, npr = probe.shape
     t0 = _empty((B,), torch.float32, probe.device)
     _check(lib().fvs_threshold(_dev(bm, torch.float32, "bm"), _dev(probe, torch.int32, "probe"), npr,
-                               _dev(off, torch.int32, "off"), B, n1, MB, r, _dev(t0, torch.float32, "t0"), _stream()),
-           "fvs_threshold")
+                               _dev(off, torch.int32, "off"), B, n1, MB, r, _dev(t0, torch.float32, "t0"),
+                               _opt(cnt, torch.int32, "cnt", (B,)), _stream()), "fvs_threshold")
     return t0
 
 

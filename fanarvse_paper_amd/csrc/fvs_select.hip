@@ -19,7 +19,7 @@ constexpr int kSmallB = 64;
 template <int NT>
 __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
                                                   int npr, const int32_t *__restrict__ off, int n1, int MB, int r,
-                                                  float *__restrict__ t0) {
+                                                  float *__restrict__ t0, int32_t *__restrict__ cnt) {
   __shared__ int nb[kMaxN1];
   __shared__ int hist[256];
   __shared__ int sh[fvs_sh_ints(NT)];
@@ -44,7 +44,10 @@ __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, 
   const int kk = min(min(r, n), nv);
   float out = 1e30f;
   if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t, NT>(key, n, kk, hist, sh));
-  if (threadIdx.x == 0) t0[q] = out;
+  if (threadIdx.x == 0) {
+    t0[q] = out;
+    if (cnt) cnt[q] = 0;  // the emit pass's counter, zeroed here instead of by a fill launch
+  }
 }
 
 // One block per query: top-K of the first min(cnt, M) buffer entries by (est desc, pos asc).
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(NT) void k_select(const float *__restrict__ bval, c
 }  // namespace
 
 extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
-                             int32_t n1, int32_t MB, int32_t r, float *t0, void *stream) {
+                             int32_t n1, int32_t MB, int32_t r, float *t0, int32_t *cnt, void *stream) {
   if (B < 0 || n1 <= 0 || n1 > npr || MB <= 0 || r <= 0) return FVS_E_ARG;
   if (n1 > kMaxN1) return FVS_E_CAPACITY;
   if ((int64_t)n1 * MB > (int64_t)1 << 30) return FVS_E_ARG;
@@ -143,10 +146,10 @@ extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr,
   if (!bm || !probe || !off || !t0) return FVS_E_ARG;
   if (B <= kSmallB)
     hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
-                       MB, r, t0);
+                       MB, r, t0, cnt);
   else
     hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
-                       MB, r, t0);
+                       MB, r, t0, cnt);
   return fvs_launch_status();
 }
 

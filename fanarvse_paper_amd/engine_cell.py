@@ -66,9 +66,8 @@ class EngineS:
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
         _lib.tr_scan(0, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=self.MB, n1=n1)
-        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
-        cnt = torch.empty((B,), dtype=torch.int32, device=dev)
-        _lib.fill_u32(cnt, 0)
+        cnt = torch.empty((B,), dtype=torch.int32, device=dev)  # zeroed by the threshold kernel
+        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r, cnt)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
         pr = prn
@@ -76,7 +75,7 @@ class EngineS:
                      bpos=bpos, CAP=M)
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
         self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
-        return pos, ok.bool()
+        return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
 
     def _dense(self, Qb):
         """The dense products: Qr = Qb @ W1 (f32), QM = fp16(Qb) @ means16.T (fp16), Zq = Qb @ VP (f32);

@@ -134,16 +134,15 @@ class SpaceX(EngineS):
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch, qadd=QC)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
         self._scan_streamed(0, Qr, pr, bm=bm, MB=self.MB, n1=n1)
-        t0 = _lib.threshold(bm, probe, self.s1["off_t"], n1, self.MB, r)
-        cnt = torch.empty((B,), dtype=torch.int32, device=dev)
-        _lib.fill_u32(cnt, 0)
+        cnt = torch.empty((B,), dtype=torch.int32, device=dev)  # zeroed by the threshold kernel
+        t0 = _lib.threshold(bm, probe, self.s1["off_t"], n1, self.MB, r, cnt)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
         pr = prn
         self._scan_streamed(1, Qr, pr, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
         self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
-        return pos, ok.bool()
+        return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
 
     def _dense(self, Qb):
         """The dense products (space_x.py:33-38): Qr = Qb @ W1 and Zq = Qb @ VP (f32, or f32 of the fp16

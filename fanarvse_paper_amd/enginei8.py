@@ -113,9 +113,8 @@ class EngineI8:
         pr, prn = _lib.pairs2(probe, n1, NC, QM, self.mnorm, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=Qb.device)
         _lib.i8_scan(0, self.blocks, q8, qs, pr, self.Z, self.zs, bm=bm, MB=self.MB, n1=n1)
-        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r)
-        cnt = torch.empty((B,), dtype=torch.int32, device=Qb.device)
-        _lib.fill_u32(cnt, 0)
+        cnt = torch.empty((B,), dtype=torch.int32, device=Qb.device)  # zeroed by the threshold kernel
+        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r, cnt)
         bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
         bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
         pr = prn
@@ -123,7 +122,7 @@ class EngineI8:
         pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, min(kd, K - 1), delta)
         self._est1, self._ncnt, self._t0, self._cnt = est1, ncnt, t0, cnt
         self._bm, self._bval, self._bpos, self._n1, self._M = bm, bval, bpos, n1, M
-        return pos, ok.bool()
+        return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
 
     def _route(self, Qh, nprobe):
         QM = Qh @ self.meansN.T

@@ -137,9 +137,10 @@ int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, cons
  *   bm f32 [B, n1, MB] written by fvs_i8_scan mode 0; probe i32 [B, npr]; off i32 [NC+1] cell offsets.
  *   Valid values of query q: bm[q][j][b] for j < n1 and b < blocks(cell probe[q][j]).
  *   t0[q] = the min(r, n1*MB, #valid)-th largest valid value, or 1e30 if none is valid.
+ *   cnt i32 [B] (may be NULL): set to 0, the emit pass's candidate counters (saves a fill launch).
  */
 int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
-                  int32_t n1, int32_t MB, int32_t r, float *t0, void *stream);
+                  int32_t n1, int32_t MB, int32_t r, float *t0, int32_t *cnt, void *stream);
 
 /*
  * Final stage-1 selection (a12) and the delta rule (a14). Replaces throughput/enginei8.py:60
