@@ -41,6 +41,7 @@ class EngineS:
         self.means16 = s1["means16"].contiguous()
         self.graphs = {}
         self.nbad = 0
+        self._done = torch.cuda.Event() if torch.cuda.is_available() else None
         if int(s1["off_t"][-1]) != s1["words"].shape[0]:
             raise ValueError("EngineS: cell offsets do not match the code rows")
 
@@ -122,13 +123,16 @@ class EngineS:
         key = ("host" if host else "dev", B, K, float(z), nprobe, k)
         if key not in self.graphs:
             qs = Qb.clone()
-            hb = torch.empty((B, k + 1), dtype=torch.int64, pin_memory=True) if host else None
+            # host: [ok | top-k ids] as int64; otherwise the flags alone (bool) reach the host in the graph
+            hb = torch.empty((B, k + 1) if host else (B,), dtype=torch.int64 if host else torch.bool, pin_memory=True)
 
             def run():
                 outs = self._gpu(qs, K, z, nprobe, k)
                 if host:
                     hb.copy_(torch.cat([outs[0].to(torch.int64)[:, None], outs[1].to(torch.int64)], 1),
                              non_blocking=True)
+                else:
+                    hb.copy_(outs[0], non_blocking=True)
                 return outs
 
             g, outs = self._capture(run)
@@ -172,11 +176,14 @@ class EngineS:
         """(I [B,k], reads [B], cand_ids [B,K]) (+ scores) as src/engine_cell.py:85-102."""
         Qb = Qb.float().contiguous()
         entry = self._main(Qb, K, z, nprobe, k)
-        _, g, qs, (ok, I, nr, ids, sc, dense), _ = entry
+        _, g, qs, (ok, I, nr, ids, sc, dense), hb = entry
         qs.copy_(Qb)
         g.replay()
-        I, nr, ids, sc = _fresh(I, nr, ids, sc)
-        okh = ok.cpu().numpy()
+        done = self._done
+        done.record()
+        I, nr, ids, sc = _fresh(I, nr, ids, sc)  # runs while the host reads the flags
+        done.synchronize()
+        okh = hb.numpy()
         if not okh.all():
             bad = np.nonzero(~okh)[0].astype(np.int64)
             a, b, c, s = self._fallback_rows(entry, bad)

@@ -184,17 +184,20 @@ class EngineI8:
                 for _ in range(3):
                     self._gpu(qs, K, z, nprobe, k)
             torch.cuda.current_stream().wait_stream(st)
+            okh = torch.empty((B,), dtype=torch.bool, pin_memory=True)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 outs = self._gpu(qs, K, z, nprobe, k)
-            self.graphs[key] = (g, qs, outs)
-        g, qs, (ok, I, nr, ids, sc, blas) = self.graphs[key]
+                okh.copy_(outs[0], non_blocking=True)  # the flags reach the host inside the graph
+            self.graphs[key] = (g, qs, outs, okh.numpy(), torch.cuda.Event())
+        g, qs, (ok, I, nr, ids, sc, blas), okh, done = self.graphs[key]
         qs.copy_(Qb)
         g.replay()
-        I, nr, ids, sc = _fresh(I, nr, ids, sc)
-        okh = ok.cpu()
-        if not bool(okh.all()):
-            bad = torch.nonzero(~okh).flatten().to(Qb.device)
+        done.record()
+        I, nr, ids, sc = _fresh(I, nr, ids, sc)  # runs while the host reads the flags
+        done.synchronize()
+        if not okh.all():
+            bad = torch.from_numpy(np.nonzero(~okh)[0]).to(Qb.device)
             self.nbad += len(bad)
             a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, *[t[bad].contiguous() for t in blas])
             I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
