@@ -55,6 +55,8 @@ def parse():
                          "(configs[4]); largek: k=100 with the z sweep (configs[3]); tier: the default engine with "
                          "its fp16 rows in a file on the local drive (the reference's NVMe tier)")
     ap.add_argument("--tier-dir", default=None, help="directory of the tier file (default: $TMPDIR or /tmp)")
+    ap.add_argument("--largek-points", default="768:1000,1536:1500",
+                    help="n_p:K points of the largek mode (from the reference's k=100 grid, src/v19_final.py:64)")
     ap.add_argument("--lat-points", default="256:200,384:400", help="n_p:K points of the latency mode")
     ap.add_argument("--lat-batches", default="1,16,64")
     ap.add_argument("--lat-z", default="1.5,2,3")
@@ -529,7 +531,7 @@ def largek_mode(args):
     torch.cuda.synchronize()
     log(f"2.25M index built in {time.time() - t:.1f}s")
     rows = []
-    for p in args.points.split(","):
+    for p in args.largek_points.split(","):
         nprobe, K = (int(v) for v in p.split(":")[:2])
         for z in (1.0, 2.0, 3.0, 4.0):
             E.nbad = 0
