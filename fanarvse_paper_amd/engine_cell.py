@@ -7,7 +7,7 @@ stage 3, src/engine3.py:135-175):
     I, reads, cand_ids = E.search(Qb, K, z, nprobe, k)
 A batch is one hipGraph replay per (B, K, z, nprobe, k) and one host synchronisation on the exactness
 flags; flagged queries are redone with rho = 1, beta = 1.5 and a 65,536-entry buffer, by a captured
-graph too (flagged rows padded to a power of two). search_host is the lean latency path
+graph too (flagged rows padded to a power of two, or a multiple of 64 beyond 64). search_host is the lean latency path
 (src/engine_cell.py:130-165, EngineT.search_host): the graph itself copies the flags and the top-k ids
 into pinned host memory, so a search is one replay and one stream synchronisation.
 
@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _lib, index, s2lut
-from .enginei8 import _fresh
+from .enginei8 import _fresh, capture, padded_rows
 
 
 class EngineS:
@@ -101,20 +101,7 @@ class EngineS:
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq, probe)
 
-    @staticmethod
-    def _capture(fn):
-        """Run fn three times on a side stream (allocations and lazy set-up happen there), then capture
-        one more run into a hipGraph. Returns (graph, fn's outputs)."""
-        st = torch.cuda.Stream()
-        st.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(st):
-            for _ in range(3):
-                fn()
-        torch.cuda.current_stream().wait_stream(st)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            outs = fn()
-        return g, outs
+    _capture = staticmethod(capture)
 
     def _main(self, Qb, K, z, nprobe, k, host=False):
         """The captured search of a (B, K, z, nprobe, k) batch. host: the graph also copies
@@ -161,10 +148,10 @@ class EngineS:
 
     def _fallback_rows(self, entry, bad):
         """Flagged rows `bad` (host int64) of the batch last replayed in `entry`, recomputed by a captured
-        fallback graph over a power-of-two padding of the rows (the last row repeated). Returns the
+        fallback graph over a padding of the rows (enginei8.padded_rows; the last row repeated). Returns the
         device tensors (I, reads, ids, scores) of the len(bad) rows."""
         nb = len(bad)
-        nbp = 1 << (nb - 1).bit_length()
+        nbp = padded_rows(nb)
         g, sel, outs = self._fallback_graph(entry, nbp)
         pad = np.concatenate([bad, np.full(nbp - nb, bad[-1], np.int64)])
         sel.copy_(torch.from_numpy(pad), non_blocking=False)

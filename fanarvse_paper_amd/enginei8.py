@@ -28,6 +28,27 @@ def pairs_fast(probe, NC, QM, scale=None):
     return qid, coff, ccnt, qcp, qrank
 
 
+def capture(fn):
+    """Run fn three times on a side stream (allocations and lazy set-up happen there), then capture one
+    more run into a hipGraph. Returns (graph, fn's outputs)."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(st)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = fn()
+    return g, outs
+
+
+def padded_rows(nb):
+    """Rows of a captured fallback graph for nb flagged queries: a power of two up to 64, then a
+    multiple of 64 (so a handful of graphs serves every count)."""
+    return 1 << (nb - 1).bit_length() if nb <= 64 else -(-nb // 64) * 64
+
+
 def _fresh(*ts):
     """Copies of the graph's output tensors (int32 / float32) for the caller, made by one gather kernel into
     one new buffer instead of one copy per tensor."""
@@ -178,17 +199,14 @@ class EngineI8:
         key = (B, K, float(z), nprobe, k)
         if key not in self.graphs:
             qs = Qb.clone()
-            st = torch.cuda.Stream()
-            st.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(st):
-                for _ in range(3):
-                    self._gpu(qs, K, z, nprobe, k)
-            torch.cuda.current_stream().wait_stream(st)
             okh = torch.empty((B,), dtype=torch.bool, pin_memory=True)
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+
+            def run():
                 outs = self._gpu(qs, K, z, nprobe, k)
                 okh.copy_(outs[0], non_blocking=True)  # the flags reach the host inside the graph
+                return outs
+
+            g, outs = capture(run)
             self.graphs[key] = (g, qs, outs, okh.numpy(), torch.cuda.Event())
         g, qs, (ok, I, nr, ids, sc, blas), okh, done = self.graphs[key]
         qs.copy_(Qb)
@@ -197,16 +215,43 @@ class EngineI8:
         I, nr, ids, sc = _fresh(I, nr, ids, sc)  # runs while the host reads the flags
         done.synchronize()
         if not okh.all():
-            bad = torch.from_numpy(np.nonzero(~okh)[0]).to(Qb.device)
-            self.nbad += len(bad)
-            a, b, c, s = self._fallback(Qb[bad], K, z, nprobe, k, *[t[bad].contiguous() for t in blas])
-            I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
+            bad = np.nonzero(~okh)[0].astype(np.int64)
+            nb = len(bad)
+            self.nbad += nb
+            fg, sel, (a, b, c, s, ok2) = self._fallback_graph(key, qs, blas, padded_rows(nb))
+            sel.copy_(torch.from_numpy(np.concatenate([bad, np.full(padded_rows(nb) - nb, bad[-1], np.int64)])))
+            fg.replay()
+            bd = torch.from_numpy(bad).to(Qb.device)
+            I[bd], nr[bd], ids[bd], sc[bd] = a[:nb], b[:nb], c[:nb], s[:nb]
+            self.nbad2 += int((~ok2[:nb]).sum())
         return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
+
+    def _fallback_graph(self, key, qs, blas, nbp):
+        """The captured fallback of nbp rows gathered (by `sel`) from the main graph's query and BLAS
+        buffers; it is replayed right after the main graph, so those hold the batch's values."""
+        fkey = ("fb", key, nbp)
+        if fkey not in self.graphs:
+            sel = torch.zeros(nbp, dtype=torch.int64, device=qs.device)
+            _, K, z, nprobe, k = key
+
+            def run():
+                a = [t.index_select(0, sel) for t in (qs,) + tuple(blas)]
+                return self._fallback_core(a[0], K, z, nprobe, k, *a[1:])
+
+            g, outs = capture(run)
+            self.graphs[fkey] = (g, sel, outs)
+        return self.graphs[fkey]
 
     def _fallback(self, Qb, K, z, nprobe, k, zq=None, QM=None, Zq=None):
         """Flagged queries again with r = K, n1 over 1.5K blocks, M = 65,536, an fp32 LUT and every
         candidate scored (throughput/enginei8.py:112-120). zq / QM / Zq: the rows of the main pass's BLAS
         products for these queries (recomputed when not given)."""
+        I, reads, ids, scores, ok = self._fallback_core(Qb, K, z, nprobe, k, zq, QM, Zq)
+        self.nbad2 += int((~ok).sum())
+        return I, reads, ids, scores
+
+    def _fallback_core(self, Qb, K, z, nprobe, k, zq=None, QM=None, Zq=None):
+        """The fallback without host synchronisation (capturable); also returns its own exactness flags."""
         qp = _lib.query_prep(Qb, self.Vr, self.s1["c"], zq)
         q8, qs, QC, Qh, _ = qp
         if QM is None:
@@ -216,8 +261,7 @@ class EngineI8:
             Zq = s2lut.rotate(self.code, Qh)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, rho_override=1.0, M_override=65536, qp=qp, delta=None)
         ok2, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=False, ncnt=None)
-        self.nbad2 += int((~ok).sum())
-        return I, reads, ids, scores
+        return I, reads, ids, scores, ok
 
     def trace(self, Qb, K, z, nprobe, k):
         """Eager run of one batch that returns every intermediate (for parity tests and profiling)."""
