@@ -191,8 +191,8 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
 
 // Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
 // Requires kk <= n. The kk keys above the radix bound are gathered, then each is stored at its rank
-// among them: a count of the larger keys when kk <= 128 (256 threads) or kk <= NT (larger blocks), a
-// bitonic sort above, which measures faster there. Block of NT threads; cnt: 1 int of LDS.
+// among them: a count of the larger keys (two keys per thread) when kk <= 2 NT, a bitonic sort above.
+// Block of NT threads; cnt: 1 int of LDS.
 template <int NT = 256, typename F>
 __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
   const int P = fvs_pow2_ceil(kk);
@@ -208,13 +208,20 @@ __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist,
     }
   }
   __syncthreads();
-  if (kk <= (NT > 256 ? NT : 128)) {
-    const uint64_t mine = threadIdx.x < kk ? s[threadIdx.x] : 0ull;
-    int rank = 0;
-    if (threadIdx.x < kk)
-      for (int t = 0; t < kk; t++) rank += s[t] > mine ? 1 : 0;  // one address for every lane: a broadcast read
+  if (kk <= 2 * NT) {
+    // each thread places keys t and t + NT at their ranks (a count of the larger keys; every lane reads
+    // the same address per step: a broadcast)
+    const uint64_t m0 = threadIdx.x < kk ? s[threadIdx.x] : 0ull;
+    const uint64_t m1 = threadIdx.x + NT < kk ? s[threadIdx.x + NT] : 0ull;
+    int r0 = 0, r1 = 0;
+    for (int t = 0; t < kk; t++) {
+      const uint64_t x = s[t];
+      r0 += x > m0 ? 1 : 0;
+      r1 += x > m1 ? 1 : 0;
+    }
     __syncthreads();
-    if (threadIdx.x < kk) s[rank] = mine;
+    if (threadIdx.x < kk) s[r0] = m0;
+    if (threadIdx.x + NT < kk) s[r1] = m1;
     __syncthreads();
   } else {
     fvs_block_bitonic<uint64_t, true>(s, P);
