@@ -64,7 +64,7 @@ struct EmitLds {
 };
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void k_i8_scan(
+__global__ __launch_bounds__(256, MODE == 0 ? 3 : 2) void k_i8_scan(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
     const int32_t *__restrict__ pcell, const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
@@ -264,14 +264,24 @@ __global__ __launch_bounds__(256, 2) void k_i8_scan(
             }
             if (MODE == 1 && !direct && valid) E->cnt8[c0 + jl][2 * w + h] = (uint8_t)nmine;
           };
-          v4i b0[8], b1[8];
-          load(b0, 0);
-          for (int t = 0; t < ntiles; t += 2) {
-            load(b1, min(t + 1, ntiles - 1));
-            compute(b0, t);
-            if (t + 1 >= ntiles) break;
-            load(b0, min(t + 2, ntiles - 1));
-            compute(b1, t + 1);
+          if constexpr (MODE == 0) {
+            // the first pass sees about one tile per item: one fragment set, fewer registers, three
+            // resident workgroups per CU instead of two
+            for (int t = 0; t < ntiles; t++) {
+              v4i b[8];
+              load(b, t);
+              compute(b, t);
+            }
+          } else {
+            v4i b0[8], b1[8];
+            load(b0, 0);
+            for (int t = 0; t < ntiles; t += 2) {
+              load(b1, min(t + 1, ntiles - 1));
+              compute(b0, t);
+              if (t + 1 >= ntiles) break;
+              load(b0, min(t + 2, ntiles - 1));
+              compute(b1, t + 1);
+            }
           }
         }
         __syncthreads();
@@ -350,7 +360,7 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   hipStream_t st = (hipStream_t)stream;
   // first pass: two resident workgroups per CU, each looping over items with the next item's loads in
   // flight during the current one; emit: one workgroup per item (its flush leaves no room to hide them)
-  const unsigned grid = mode == 0 ? (unsigned)min(P, 2 * fvs_cu_count()) : (unsigned)P;
+  const unsigned grid = mode == 0 ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, pblk, ps,
