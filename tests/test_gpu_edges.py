@@ -1,0 +1,107 @@
+"""Edge cases of both engines against the CPU oracle, bit for bit: the throughput engine at batch sizes
+that leave partial 32-query tiles or a single query (1, 3, 33, 257); an index with many empty and tiny
+cells (3,000 vectors over 512 cells, so most probed cells hold a few rows or none); and a dimension
+(d = 384) other than the configurations'. The three dense products come from the GPU's BLAS and are
+shared inputs of the oracle, as in the other parity tests."""
+import numpy as np
+import pytest
+import torch
+
+from fanarvse_paper_amd import datagen, index, trellis
+from fanarvse_paper_amd.engine_cell import EngineS
+from fanarvse_paper_amd.enginei8 import EngineI8
+
+pytestmark = pytest.mark.gpu
+
+
+def npy(t):
+    return t.detach().cpu().numpy()
+
+
+def u16(t):
+    return npy(t).view(np.uint16)
+
+
+def check_i8(E, idx, Q, K, z, nprobe, k, oracle_mod):
+    I, reads, ids = E.search(Q, K, z, nprobe, k)
+    tr = E.trace(Q, K, z, nprobe, k)
+    torch.cuda.synchronize()
+    out = oracle_mod.pipeline(idx, npy(Q), K, z, nprobe, k, QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]), zq=npy(tr["z"]))
+    assert np.array_equal(npy(I), out["I"])
+    assert np.array_equal(npy(reads), out["reads"])
+    assert np.array_equal(npy(ids), out["cand"])
+    return out
+
+
+def check_trellis(E, idx, Q, K, z, nprobe, k, oracle_mod):
+    I, reads, ids = E.search(Q, K, z, nprobe, k)
+    torch.cuda.synchronize()
+    Qr, QC, QM, Zq = E._dense(Q)
+    out = oracle_mod.tr_pipeline(idx, npy(Q), K, z, nprobe, k, Qr=npy(Qr), QM16=u16(QM), Zq=npy(Zq),
+                                 M=E._params(K, nprobe, B=len(Q))[0])
+    assert np.array_equal(npy(I), out["I"])
+    assert np.array_equal(npy(reads), out["reads"])
+    assert np.array_equal(npy(ids), out["cand"])
+    return out
+
+
+@pytest.fixture(scope="module")
+def i8env(oracle_mod):
+    print("\n[gpu edges] int8 index N=20000 d=768 NC=128", flush=True)
+    X = datagen.gen(20000, 768, 64, 0.7, seed=3, device="cuda")
+    Q = datagen.gen(257, 768, 64, 0.7, seed=4, device="cuda", dtype=torch.float32)
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=128)
+    return dict(E=EngineI8(s1, code, Z, zs, Vr, H=X), idx=oracle_mod.index_from_tables(s1, code, Z, zs, Vr, X), Q=Q)
+
+
+@pytest.mark.parametrize("B", [1, 3, 33, 257])
+def test_throughput_engine_odd_batches(i8env, oracle_mod, B):
+    print(f"\n[gpu edges] EngineI8 B={B}", flush=True)
+    check_i8(i8env["E"], i8env["idx"], i8env["Q"][:B].contiguous(), 120, 1.25, 16, 10, oracle_mod)
+
+
+def both_engines(X, Q, nlist, K, nprobe, oracle_mod, batches):
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=nlist)
+    counts = np.diff(s1["off"])
+    E = EngineI8(s1, code, Z, zs, Vr, H=X)
+    idx = oracle_mod.index_from_tables(s1, code, Z, zs, Vr, X)
+    ts1, tcode = trellis.build_index(X, nlist=nlist)
+    Et = EngineS(ts1, tcode, H=X)
+    tidx = oracle_mod.trellis_index_from_tables(ts1, tcode, X)
+    for B in batches:
+        check_i8(E, idx, Q[:B].contiguous(), K, 1.25, nprobe, 10, oracle_mod)
+        check_trellis(Et, tidx, Q[:B].contiguous(), K, 2.0, nprobe, 10, oracle_mod)
+    return counts, np.diff(ts1["off"])
+
+
+def test_tiny_cells(oracle_mod):
+    """3,000 vectors over 512 cells: most probed cells hold a handful of rows."""
+    print("\n[gpu edges] N=3000 over 512 cells, both engines", flush=True)
+    X = datagen.gen(3000, 768, 16, 0.7, seed=5, device="cuda")
+    Q = datagen.gen(40, 768, 16, 0.7, seed=6, device="cuda", dtype=torch.float32)
+    counts, _ = both_engines(X, Q, 512, 60, 48, oracle_mod, (1, 40))
+    assert np.median(counts) < 8
+
+
+def test_duplicate_rows_and_empty_cells(oracle_mod):
+    """4,000 rows drawn from 300 distinct vectors: k-means starts from repeated centroids, so many cells
+    stay empty, and every score has exact ties that the (score, id) order must break alike."""
+    print("\n[gpu edges] duplicated rows, empty cells, both engines", flush=True)
+    base = datagen.gen(300, 768, 12, 0.7, seed=9, device="cuda")
+    pick = torch.from_numpy(np.random.default_rng(10).integers(0, 300, 4000)).to(base.device)
+    X = base[pick].contiguous()
+    Q = datagen.gen(33, 768, 12, 0.7, seed=11, device="cuda", dtype=torch.float32)
+    counts, tcounts = both_engines(X, Q, 256, 80, 64, oracle_mod, (1, 33))
+    assert (counts == 0).sum() > 0 and (tcounts == 0).sum() > 0
+
+
+def test_dimension_384(oracle_mod):
+    print("\n[gpu edges] d=384, both engines", flush=True)
+    X = datagen.gen(12000, 384, 32, 0.7, seed=7, device="cuda")
+    Q = datagen.gen(50, 384, 32, 0.7, seed=8, device="cuda", dtype=torch.float32)
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=64)
+    E = EngineI8(s1, code, Z, zs, Vr, H=X)
+    check_i8(E, oracle_mod.index_from_tables(s1, code, Z, zs, Vr, X), Q, 100, 1.25, 12, 10, oracle_mod)
+    ts1, tcode = trellis.build_index(X, nlist=64)
+    Et = EngineS(ts1, tcode, H=X)
+    check_trellis(Et, oracle_mod.trellis_index_from_tables(ts1, tcode, X), Q, 100, 2.0, 12, 10, oracle_mod)
