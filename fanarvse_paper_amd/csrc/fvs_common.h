@@ -59,6 +59,10 @@ __device__ __forceinline__ void fvs_lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Index of the calling wave in its workgroup, as a value the compiler knows to be wave-uniform: branches
+// and loops that depend on it compile to scalar code, and values carried through them stay in SGPRs.
+__device__ __forceinline__ int fvs_wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
+
 // Number of set bits of a wave mask below this lane.
 __device__ __forceinline__ int fvs_lane_prefix(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
@@ -77,7 +81,7 @@ __host__ __device__ constexpr int fvs_sh_ints(int NT) { return NT / 64 + 4; }
 // Inclusive prefix sum over threadIdx.x for a block of NT threads (a multiple of 64). tmp: NT/64 ints.
 template <int NT = 256>
 __device__ __forceinline__ int fvs_block_scan(int v, int *tmp) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = fvs_wave_id();
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     int t = __shfl_up(v, o, FVS_WAVE);

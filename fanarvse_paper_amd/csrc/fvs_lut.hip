@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void k_lut_build(const uint16_t *__restrict__ 
   }
   // per-tier sums, one wave per tier: lane l sums coordinates start+l, start+l+64, ... in double,
   // then a fixed xor butterfly (the unrolled tier loop keeps the argument-struct index uniform)
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = fvs_wave_id();
 #pragma unroll
   for (int t = 0; t < FVS_MAX_TIERS; t++) {
     if (t < ta.T && (t & 3) == wv) {

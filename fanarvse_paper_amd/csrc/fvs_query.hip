@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, co
   }
 
   // per-row max |z| over the 256 coordinates
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = fvs_wave_id();
 #pragma unroll
   for (int rr = 0; rr < QB; rr++) {
     const float m = fvs_wave_max(fabsf(acc[rr]));
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void k_query_code(const float *__restrict__ z,
                                                     int d, const float *__restrict__ c, int8_t *__restrict__ q8,
                                                     float *__restrict__ qs, float *__restrict__ qc,
                                                     uint16_t *__restrict__ qh) {
-  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t q = (int64_t)blockIdx.x * 4 + fvs_wave_id();
   if (q >= B) return;
   const int lane = threadIdx.x & 63;
   const float4 zz = reinterpret_cast<const float4 *>(z + q * kR)[lane];

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(NT) void k_refine(const float *__restrict__ est, co
   __syncthreads();
 
   // exact scores of the ambiguous candidates
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = fvs_wave_id();
   const int na = L.namb;
   if (na > 0) {
     float qv[NG][8];
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void k_refine_rows(const float *__restrict__ e
   int32_t *aid = reinterpret_cast<int32_t *>(score + K);   // [K] row of the j-th ambiguous slot in `rows`
   int16_t *amb = reinterpret_cast<int16_t *>(aid + K);     // [K]
   const int64_t q = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   const float *e = est + q * (int64_t)K;
   const uint8_t *fl = flag + q * (int64_t)K;
   const int na = namb[q];

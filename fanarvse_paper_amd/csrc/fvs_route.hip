@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave(const uin
                                                                       int np, int64_t B,
                                                                       int32_t *__restrict__ probe) {
   __shared__ uint32_t sbuf[kRouteWaves][FVS_WAVE * R];
-  const int lane = threadIdx.x & (FVS_WAVE - 1), wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (FVS_WAVE - 1), wv = fvs_wave_id();
   const int64_t q = (int64_t)blockIdx.x * kRouteWaves + wv;
   if (q >= B) return;  // wave-uniform, and no block barrier follows
   uint32_t *s = sbuf[wv];
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave_f32(const
                                                                           int np, int64_t B,
                                                                           int32_t *__restrict__ probe) {
   __shared__ uint64_t sbuf[kRouteWaves][FVS_WAVE * R];
-  const int lane = threadIdx.x & (FVS_WAVE - 1), wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (FVS_WAVE - 1), wv = fvs_wave_id();
   const int64_t q = (int64_t)blockIdx.x * kRouteWaves + wv;
   if (q >= B) return;  // wave-uniform, and no block barrier follows
   uint64_t *s = sbuf[wv];
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kRouteBlk) void k_route_blk_f32(const uint16_t *__r
   __shared__ uint64_t s[1024];
   __shared__ int wsum[NW];
   __shared__ int sh[4];
-  const int tid = threadIdx.x, lane = tid & (FVS_WAVE - 1), wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (FVS_WAVE - 1), wv = fvs_wave_id();
   const int64_t q = blockIdx.x;
   const int c0 = tid * KPT;
   const float add = ADD ? qadd[q] : 0.f;
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__
   __shared__ int sh[16];
   __shared__ int cnt;
   const int64_t q = blockIdx.x;
-  const int tid = threadIdx.x, w = tid >> 6;
+  const int tid = threadIdx.x, w = fvs_wave_id();
   const uint16_t *row = QM + q * NC;
   for (int i = tid; i < NC; i += 256) v[i] = (uint16_t)fvs_ord16(row[i]);
   int want = np;
@@ -593,7 +593,7 @@ __global__ __launch_bounds__(512) void k_rank_build(const int32_t *__restrict__ 
   // ranks: one wave per query (8 at a time), its probe row read 64 entries per load with up to 16 loads in
   // flight; entries that fall in [c0, c0 + kTileC) are scattered into the tile
   constexpr int kPU = 16;
-  const int lane = tid & (FVS_WAVE - 1), wv = tid >> 6;
+  const int lane = tid & (FVS_WAVE - 1), wv = fvs_wave_id();
   for (int qq = wv; qq < kTileQ; qq += 512 / FVS_WAVE) {
     if (q0 + qq >= B) break;
     const int32_t *pr = probe + (q0 + qq) * npr;
@@ -642,7 +642,7 @@ __global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_count(const uint
                                                                       int32_t *__restrict__ ccnt_a,
                                                                       int32_t *__restrict__ ccnt_b) {
   const int lane = threadIdx.x & (FVS_WAVE - 1);
-  const int c = blockIdx.x * kCellWaves + (threadIdx.x >> 6);
+  const int c = blockIdx.x * kCellWaves + fvs_wave_id();
   if (c >= NC) return;
   const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
   int ma = 0, mb = 0;
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(1024) void k_cell_scan(const int32_t *__restrict__ 
   __shared__ int wsum[1024 / FVS_WAVE];
   const int32_t *ccnt = blockIdx.x ? ccnt_b : ccnt_a;
   int32_t *coff = blockIdx.x ? coff_b : coff_a;
-  const int t = threadIdx.x, lane = t & (FVS_WAVE - 1), w = t >> 6;
+  const int t = threadIdx.x, lane = t & (FVS_WAVE - 1), w = fvs_wave_id();
   const int per = (NC + 1023) / 1024;
   const int c0 = t * per, c1 = min(c0 + per, NC);
   int run = 0;
@@ -701,7 +701,7 @@ __global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_emit(
     const uint16_t *__restrict__ rank, const uint16_t *__restrict__ score, int64_t Bp, const float *__restrict__ mnorm,
     const float *__restrict__ qadd, int NC, PairList la, PairList lb) {
   const int lane = threadIdx.x & (FVS_WAVE - 1);
-  const int c = blockIdx.x * kCellWaves + (threadIdx.x >> 6);
+  const int c = blockIdx.x * kCellWaves + fvs_wave_id();
   if (c >= NC) return;
   const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
   const uint4 *ss = reinterpret_cast<const uint4 *>(score + (int64_t)c * Bp);

@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256, MODE == 0 ? 3 : 2) void k_i8_scan(
     E = &Es;
   }
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = fvs_wave_id();
   const int h = lane >> 5, li = lane & 31;
 
   // Items p = blockIdx.x, blockIdx.x + gridDim.x, ...: right after an item's tile loop the next item's

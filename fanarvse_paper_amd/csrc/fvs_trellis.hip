@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void k_trellis_encode(const float *__restrict_
   __shared__ int path[kTrR];
   __shared__ unsigned long long best;
   const int64_t v = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   for (int i = tid; i < S; i += 256) vals[i] = tab[i];
   x[tid] = Zs[v * kTrR + tid];
   if (tid == 0) best = ~0ull;
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
                                                  int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
   __shared__ float stab[1 << kMaxL];
   __shared__ float4 qbuf[4][kTrR / 4];  // per wave: the query vector of the current step
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   const int S = 1 << L;
   for (int i = tid; i < S; i += 256) stab[i] = tab[i];
   __syncthreads();
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict_
   __shared__ float qn2[kMaxT];
   const int64_t q = blockIdx.x / nchunk;
   const int m0 = (int)(blockIdx.x % nchunk) * 4 * cpw, m1 = min(K, m0 + 4 * cpw);
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   for (int i = tid; i < D; i += 256) zq[i] = Zq[q * D + i];
   for (int i = tid; i < 256 * tiers.T; i += 256) cbs[i] = cb[i];
   __syncthreads();
