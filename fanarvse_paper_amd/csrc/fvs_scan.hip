@@ -7,12 +7,13 @@
 //   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the
 //     row scales of its 256 rows are staged in LDS up front (kMeta pairs at a time), so no global
 //     load in the tile loop depends on another;
-//   * every wave loads the B fragments of its next tile straight into registers (16-byte lane
-//     loads of the query codes, served by L1/L2: the four waves of an item read the same 8 KB) while
-//     it multiplies the current one. The waves of an item never wait for each other inside the tile
-//     loop; they synchronise only when the pair list is staged and when candidates are flushed.
-// Two blocks per wave halve the B-fragment gathers per MFMA (they are the latency the tile loop
-// waits on) at the cost of occupancy 2.
+//   * every wave loads the B fragments of a tile straight into registers (16-byte lane loads of
+//     the query codes, served by L1/L2: the four waves of an item read the same 8 KB). The waves of
+//     an item never wait for each other inside the tile loop; they synchronise only when the pair
+//     list is staged and when candidates are flushed.
+// Two blocks per wave halve the B-fragment gathers per MFMA. One fragment set per tile (no load of
+// the next tile ahead) and emit regions sized for it keep the kernel at 168 VGPRs and 50 KB of LDS:
+// three resident workgroups per CU, whose waves hide each other's load latency.
 //
 // Operand layout: lane l holds row/column (l & 31) and, for MFMA step s (k-block of 32 bytes), the
 // 16 bytes at 32*s + 16*(l >> 5); A and B use the same assignment, so the contraction is exact for
@@ -41,9 +42,9 @@ constexpr int kR = 256;
 constexpr int kNB = 2;       // 32-row blocks per wave
 constexpr int kCB = 4 * kNB; // 32-row blocks per work item
 constexpr int kMeta = 512;   // pairs staged in LDS at a time
-constexpr int kEW = 1024;    // LDS slots per wave: kEW - 64 for candidates, 64 dummy slots
+constexpr int kEW = 768;     // LDS slots per wave: kEW - 64 for candidates, 64 dummy slots
 constexpr int kCap = kEW - 64;
-constexpr int kMaxQ = 2048;  // queries per cell handled by the staged emit
+constexpr int kMaxQ = 1024;  // queries per cell handled by the staged emit
 
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
@@ -64,7 +65,7 @@ struct EmitLds {
 };
 
 template <int MODE>
-__global__ __launch_bounds__(256, MODE == 0 ? 3 : 2) void k_i8_scan(
+__global__ __launch_bounds__(256, 3) void k_i8_scan(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
     const int32_t *__restrict__ pcell, const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
@@ -265,24 +266,12 @@ __global__ __launch_bounds__(256, MODE == 0 ? 3 : 2) void k_i8_scan(
             }
             if (MODE == 1 && !direct && valid) E->cnt8[c0 + jl][2 * w + h] = (uint8_t)nmine;
           };
-          if constexpr (MODE == 0) {
-            // the first pass sees about one tile per item: one fragment set, fewer registers, three
-            // resident workgroups per CU instead of two
-            for (int t = 0; t < ntiles; t++) {
-              v4i b[8];
-              load(b, t);
-              compute(b, t);
-            }
-          } else {
-            v4i b0[8], b1[8];
-            load(b0, 0);
-            for (int t = 0; t < ntiles; t += 2) {
-              load(b1, min(t + 1, ntiles - 1));
-              compute(b0, t);
-              if (t + 1 >= ntiles) break;
-              load(b0, min(t + 2, ntiles - 1));
-              compute(b1, t + 1);
-            }
+          // one fragment set: loading the next tile ahead would hold 32 more VGPRs and cost the third
+          // resident workgroup, which hides more latency than the prefetch did
+          for (int t = 0; t < ntiles; t++) {
+            v4i b[8];
+            load(b, t);
+            compute(b, t);
           }
         }
         __syncthreads();
@@ -359,8 +348,9 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // first pass: two resident workgroups per CU, each looping over items with the next item's loads in
-  // flight during the current one; emit: one workgroup per item (its flush leaves no room to hide them)
+  // first pass: three resident workgroups per CU, each looping over items with the next item's loads in
+  // flight during the current one; emit: one workgroup per item (a persistent emit with the next item's
+  // loads in flight during the flush measured no faster)
   const unsigned grid = mode == 0 ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;

@@ -107,7 +107,7 @@ class EngineS:
         """The captured search of a (B, K, z, nprobe, k) batch. host: the graph also copies
         [ok | top-k ids] (int64) into pinned host memory."""
         B = len(Qb)
-        key = ("host" if host else "dev", B, K, float(z), nprobe, k)
+        key = ("host" if host else "dev", B, K, float(z), nprobe, k, self.M)  # a change of M captures anew
         if key not in self.graphs:
             qs = Qb.clone()
             # host: [ok | top-k ids] as int64; otherwise the flags alone (bool) reach the host in the graph

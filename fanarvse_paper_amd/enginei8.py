@@ -99,6 +99,10 @@ class EngineI8:
         self.nbad2 = 0
 
     # ------------------------------------------------------------------ stages
+    def _knobs(self):
+        """The knob values captured work depends on: a search after a change captures new graphs."""
+        return (self.MSZ, self.BETA, self.RHO, self.DELTA, self.LUTF, self.LUTH)
+
     def _check_knobs(self):
         if self.PROJ:
             raise NotImplementedError("PROJ routing is not implemented")
@@ -196,7 +200,7 @@ class EngineI8:
         the picks read in full precision, the stage-2 estimates of the surely-in ones."""
         Qb = Qb.float().contiguous()
         B = len(Qb)
-        key = (B, K, float(z), nprobe, k)
+        key = (B, K, float(z), nprobe, k, self._knobs())
         if key not in self.graphs:
             qs = Qb.clone()
             okh = torch.empty((B,), dtype=torch.bool, pin_memory=True)
@@ -232,7 +236,7 @@ class EngineI8:
         fkey = ("fb", key, nbp)
         if fkey not in self.graphs:
             sel = torch.zeros(nbp, dtype=torch.int64, device=qs.device)
-            _, K, z, nprobe, k = key
+            _, K, z, nprobe, k, _ = key
 
             def run():
                 a = [t.index_select(0, sel) for t in (qs,) + tuple(blas)]

@@ -22,11 +22,24 @@ def u16(t):
     return npy(t).view(np.uint16)
 
 
-def check_i8(E, idx, Q, K, z, nprobe, k, oracle_mod):
+def check_i8(E, idx, Q, K, z, nprobe, k, oracle_mod, knobs=None):
     I, reads, ids = E.search(Q, K, z, nprobe, k)
     tr = E.trace(Q, K, z, nprobe, k)
     torch.cuda.synchronize()
-    out = oracle_mod.pipeline(idx, npy(Q), K, z, nprobe, k, QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]), zq=npy(tr["z"]))
+    out = oracle_mod.pipeline(idx, npy(Q), K, z, nprobe, k, knobs=knobs, QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]),
+                              zq=npy(tr["z"]))
+    cnt = npy(tr["cnt"])
+    assert np.array_equal(cnt, out["cnt"])
+    assert tr["M"] == out["M"]
+    bval, bpos = npy(tr["bval"]), npy(tr["bpos"])
+    # emitted sets (order-free) of a sample of queries whose candidates all fit the buffer (beyond it, which
+    # ones were kept depends on the emission order; such queries take the fallback)
+    for q in range(0, len(cnt), max(1, len(cnt) // 16)):
+        n = int(cnt[q])
+        if n > tr["M"]:
+            continue
+        assert sorted(zip(bval[q, :n].tolist(), bpos[q, :n].tolist())) == \
+            sorted(zip(out["bval"][q, :n].tolist(), out["bpos"][q, :n].tolist())), f"query {q}"
     assert np.array_equal(npy(I), out["I"])
     assert np.array_equal(npy(reads), out["reads"])
     assert np.array_equal(npy(ids), out["cand"])
@@ -105,3 +118,46 @@ def test_dimension_384(oracle_mod):
     ts1, tcode = trellis.build_index(X, nlist=64)
     Et = EngineS(ts1, tcode, H=X)
     check_trellis(Et, oracle_mod.trellis_index_from_tables(ts1, tcode, X), Q, 100, 2.0, 12, 10, oracle_mod)
+
+
+@pytest.fixture(scope="module")
+def coarse(oracle_mod):
+    """20,000 rows over 32 cells (about 625 rows, three scan items per cell)."""
+    print("\n[gpu edges] coarse index N=20000 d=768 NC=32", flush=True)
+    X = datagen.gen(20000, 768, 8, 0.7, seed=12, device="cuda")
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=32)
+    return dict(X=X, E=EngineI8(s1, code, Z, zs, Vr, H=X), idx=oracle_mod.index_from_tables(s1, code, Z, zs, Vr, X))
+
+
+def test_cells_beyond_staged_query_limit(coarse, oracle_mod):
+    """1,500 queries probing 16 of 32 cells: the hottest cells are probed by more than the 1,024 queries
+    the staged emit holds, so they take the direct path (one global atomic per candidate)."""
+    print("\n[gpu edges] hot cells: B=1500 nprobe=16", flush=True)
+    Q = datagen.gen(1500, 768, 8, 0.7, seed=13, device="cuda", dtype=torch.float32)
+    E = coarse["E"]
+    tr = E.trace(Q, 300, 1.25, 16, 10)
+    per_cell = np.bincount(npy(tr["probe"]).reshape(-1), minlength=32)
+    assert per_cell.max() > 1024
+    check_i8(E, coarse["idx"], Q, 300, 1.25, 16, 10, oracle_mod)
+
+
+def test_emit_region_overflow(coarse, oracle_mod):
+    """K = 4,000 of the 10,000 probed rows: t0 is low, each wave emits thousands of candidates per item,
+    far beyond its LDS region, and every item is redone on the direct path. A 65,536-entry candidate
+    buffer on both sides holds every candidate, so the emitted sets are compared whole."""
+    print("\n[gpu edges] emit region overflow: B=600 K=4000", flush=True)
+    Q = datagen.gen(600, 768, 8, 0.7, seed=14, device="cuda", dtype=torch.float32)
+    E = coarse["E"]
+    nb = E.nbad
+    E.search(Q, 4000, 1.25, 16, 10)  # the reference's 3,072-entry buffer: every query overflows
+    assert E.nbad - nb == len(Q)
+    msz = E.MSZ
+    E.MSZ = 65536  # a knob change captures a new graph for the same call
+    try:
+        nb = E.nbad
+        out = check_i8(E, coarse["idx"], Q, 4000, 1.25, 16, 10, oracle_mod, knobs=dict(MSZ=65536))
+        # flagged now only where the oracle flags too (too few candidates or the delta rule), not for overflow
+        assert E.nbad - nb == len(out["bad"]) < len(Q) // 10
+    finally:
+        E.MSZ = msz
+    assert np.mean(out["cnt"]) > 4000 and out["cnt"].max() <= 65536
