@@ -171,14 +171,17 @@ def main():
 
 def _time_launch(fn, reps, torch, setup=None):
     """Average device time of one fn() launch: reps launches back to back between two HIP events on the
-    current stream (the stream the libfvs wrappers launch on). When every launch needs a setup kernel
-    (a counter reset), the same number of setup launches is timed alone and subtracted."""
+    current stream (the stream the libfvs wrappers launch on), after one untimed round of the same
+    launches (the clocks settle under load; the first round after an idle host sync runs slower). When
+    every launch needs a setup kernel (a counter reset), the same number of setup launches is timed
+    alone and subtracted."""
     st = torch.cuda.current_stream()
 
     def run(body):
+        for _ in range(reps):
+            body()
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         a.record(st)
         for _ in range(reps):
             body()

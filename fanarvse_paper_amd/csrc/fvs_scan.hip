@@ -252,13 +252,17 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
                   }
                 }
               } else {  // direct path
+                // the lane's first row of the block; the empty asm keeps the compiler from hoisting the 16
+                // per-element row ids out of the tile loop, where they would hold (and spill) 32 VGPRs
+                int rb = bk[u] * 32 + 4 * h;
+                asm volatile("" : "+v"(rb));
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                   if (ev[v] >= th) {
                     const int idx = atomicAdd(&cnt[m.qid], 1);
                     if (idx < CAP) {
                       bval[(int64_t)m.qid * CAP + idx] = ev[v];
-                      bpos[(int64_t)m.qid * CAP + idx] = bk[u] * 32 + acc_row(v, h);
+                      bpos[(int64_t)m.qid * CAP + idx] = rb + 8 * (v >> 2) + (v & 3);
                     }
                   }
                 }
