@@ -214,7 +214,7 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     reps = args.kernel_reps
     t_first = _time_launch(lambda: _lib.i8_scan(0, E.blocks, q8, qs, pr1, E.Z, E.zs, bm=bm, MB=E.MB, n1=n1), reps,
                            torch)
-    t_emit = _time_launch(lambda: _lib.i8_scan(1, E.blocks, q8, qs, prn, E.Z, E.zs, t0=t0, cnt=cnt, bval=bval,
+    t_emit = _time_launch(lambda: _lib.i8_scan(1, E.rchunks, q8, qs, prn, E.Z, E.zs, t0=t0, cnt=cnt, bval=bval,
                                                bpos=bpos, CAP=M), reps, torch, setup=lambda: _lib.fill_u32(cnt, 0))
     pre = (tr["L"], tr["qsum"], tr["qn2"])
     ncnt = tr["ncnt"] if E.DELTA is not None else None

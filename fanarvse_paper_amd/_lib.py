@@ -207,11 +207,12 @@ def pairs2(probe, n1, NC, QM, mnorm, scratch=None, qadd=None):
 
 
 def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1, MB=1, n1=1):
-    """First pass (mode 0) or emit (mode 1) over the static (cell, block) items (throughput/civf8.py:89-91).
+    """First pass (mode 0) or emit (mode 1) over the stage-1 work items (throughput/civf8.py:89-91).
 
-    `blocks` must come from index.static_blocks over the same index as Z (its rows lie inside Z);
-    no host synchronisation happens here, so the call can be captured in a graph."""
-    pcell, pblk, ps, pe = blocks
+    `blocks` = (cell, first row, cell start, cell end): index.static_chunks for mode 0 (items on global
+    32-row blocks), index.row_chunks or static_chunks for mode 1, over the same index as Z (its rows lie
+    inside Z); no host synchronisation happens here, so the call can be captured in a graph."""
+    pcell, prow, ps, pe = blocks
     qid, qrank, coff, ccnt, qcp = pr
     P_ = pcell.shape[0]
     N, R = Z.shape
@@ -225,7 +226,7 @@ def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=
     f32, i32 = torch.float32, torch.int32
     _check(lib().fvs_i8_scan(mode, P_, _dev(q8, torch.int8, "q8"), _dev(qs, f32, "qs", (B,)), _dev(qid, i32, "qid"),
                              _dev(qrank, i32, "qrank"), _dev(coff, i32, "coff"), _dev(ccnt, i32, "ccnt"),
-                             _dev(pcell, i32, "pcell"), _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"),
+                             _dev(pcell, i32, "pcell"), _dev(prow, i32, "prow"), _dev(ps, i32, "ps"),
                              _dev(pe, i32, "pe"), _dev(Z, torch.int8, "Z"), _dev(zs, f32, "zs", (N,)), N, R,
                              _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"),
                              _opt(bval, f32, "bval"), _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1,

@@ -1,9 +1,13 @@
 // int8 stage-1 scan on gfx950 MFMA (v_mfma_i32_32x32x32_i8).
 //
-// Work item = (cell, chunk of up to 8 consecutive global 32-row blocks of the cell), one 4-wave
-// workgroup per item. Wave w keeps blocks 2w and 2w+1 of the chunk (64 code rows) as MFMA A operands
-// in registers for the whole item, so each code byte is read from HBM once per pass. The cell's
-// queries stream through as B operands in tiles of 32:
+// Work item = (cell, up to 256 consecutive rows of it from a first row r0), one 4-wave workgroup per
+// item; its 32-row blocks start at r0, r0 + 32, ... The first pass needs the reference's global 32-row
+// blocks (its block maxima are per global block), so its items start on a multiple of 32; the emit
+// pass, whose output does not depend on the grouping, takes items that start at the cell's first row
+// (a cell of up to 256 rows is one item, with no block straddling the cell start). Wave w keeps blocks
+// 2w and 2w+1 of the item (64 code rows) as MFMA A operands in registers for the whole item, so each
+// code byte is read from HBM once per pass. The cell's queries stream through as B operands in tiles
+// of 32:
 //   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the
 //     row scales of its 256 rows are staged in LDS up front (kMeta pairs at a time), so no global
 //     load in the tile loop depends on another;
@@ -68,7 +72,7 @@ template <int MODE>
 __global__ __launch_bounds__(256, 3) void k_i8_scan(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
-    const int32_t *__restrict__ pcell, const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps,
+    const int32_t *__restrict__ pcell, const int32_t *__restrict__ prow, const int32_t *__restrict__ ps,
     const int32_t *__restrict__ pe, int P, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
     const float *__restrict__ qcp, const float *__restrict__ t0, int32_t *__restrict__ cnt,
     float *__restrict__ bval, int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
@@ -87,13 +91,13 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
   // Items p = blockIdx.x, blockIdx.x + gridDim.x, ...: right after an item's tile loop the next item's
   // pair ids, row scales and code blocks are requested, so their latency runs under the flush.
   struct Item {
-    int p, c, qn, qoff, blk0, cs, ce;
+    int p, c, qn, qoff, r0, cs, ce;  // r0: first row of the item
   };
   auto item_at = [&](int p) {
     Item it{p, 0, 0, 0, 0, 0, 0};
     if (p < P) {
       it.c = pcell[p];
-      it.blk0 = pblk[p];
+      it.r0 = prow[p];
       it.cs = ps[p];
       it.ce = pe[p];
       it.qn = ccnt[it.c];
@@ -112,15 +116,14 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
       pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
     }
     if (tid < 32 * kCB) {
-      const int r = it.blk0 * 32 + tid;
+      const int r = it.r0 + tid;
       zr = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
     }
-    const int lastblk = (it.ce - 1) / 32;
 #pragma unroll
     for (int u = 0; u < kNB; u++) {
-      const int bk = it.blk0 + kNB * w + u;
-      int64_t zr_ = (int64_t)bk * 32 + li;
-      if (bk > lastblk || zr_ > N - 1) zr_ = N - 1;
+      const int b0 = it.r0 + 32 * (kNB * w + u);  // first row of the block
+      int64_t zr_ = (int64_t)b0 + li;
+      if (b0 >= it.ce || zr_ > N - 1) zr_ = N - 1;  // rows past the cell carry a NaN scale
       const v4i *zp = reinterpret_cast<const v4i *>(Z + zr_ * kR + h * 16);
 #pragma unroll
       for (int s = 0; s < 8; s++) a[u][s] = zp[2 * s];
@@ -144,18 +147,13 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
       p += stride;
       continue;
     }
-    const int qn = cur.qn, qoff = cur.qoff, blk0 = cur.blk0, cs = cur.cs;
+    const int qn = cur.qn, qoff = cur.qoff, cs = cur.cs;
     const bool staged = MODE == 1 && qn <= kMaxQ;
-    const int row0 = blk0 * 32;  // first row of the item
-    const int lastblk = (cur.ce - 1) / 32;
+    const int row0 = cur.r0;  // first row of the item
     if (tid < 32 * kCB) zsl[tid] = zr;
-    int bk[kNB];
     bool act[kNB];
 #pragma unroll
-    for (int u = 0; u < kNB; u++) {
-      bk[u] = blk0 + kNB * w + u;
-      act[u] = bk[u] <= lastblk;
-    }
+    for (int u = 0; u < kNB; u++) act[u] = row0 + 32 * (kNB * w + u) < cur.ce;
     const bool any = act[0];
     int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
     if constexpr (MODE == 1) {
@@ -235,7 +233,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
                 for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
                 mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
                 if (h == 0 && valid)
-                  bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + (bk[u] - cs / 32)] = mx;
+                  bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + kNB * w + u - (cs >> 5))] = mx;
               } else if (!direct) {
                 float *est = E->est[w];
                 uint32_t *tag = E->tag[w];
@@ -254,7 +252,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
               } else {  // direct path
                 // the lane's first row of the block; the empty asm keeps the compiler from hoisting the 16
                 // per-element row ids out of the tile loop, where they would hold (and spill) 32 VGPRs
-                int rb = bk[u] * 32 + 4 * h;
+                int rb = row0 + 32 * (kNB * w + u) + 4 * h;
                 asm volatile("" : "+v"(rb));
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
@@ -342,7 +340,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
 
 extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
                            const int32_t *qrank, const int32_t *coff, const int32_t *ccnt, const int32_t *pcell,
-                           const int32_t *pblk, const int32_t *ps, const int32_t *pe, const int8_t *Z,
+                           const int32_t *prow, const int32_t *ps, const int32_t *pe, const int8_t *Z,
                            const float *zs, int64_t N, int32_t R, const float *qcp, const float *t0, int32_t *cnt,
                            float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1,
                            void *stream) {
@@ -350,7 +348,7 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (mode != 0 && mode != 1) return FVS_E_ARG;
   if (P < 0 || N <= 0) return FVS_E_ARG;
   if (P == 0) return FVS_OK;
-  if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
+  if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
   // first pass: three resident workgroups per CU, each looping over items with the next item's loads in
   // flight during the current one; emit: one workgroup per item (a persistent emit with the next item's
@@ -358,11 +356,11 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   const unsigned grid = mode == 0 ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, pblk, ps,
+    hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, prow, ps,
                        pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<1>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, pblk, ps,
+    hipLaunchKernelGGL(k_i8_scan<1>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, prow, ps,
                        pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   }
   return fvs_launch_status();

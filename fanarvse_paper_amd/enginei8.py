@@ -87,7 +87,8 @@ class EngineI8:
         self.H = H
         s2lut.prepare_u(code)
         _, self.MB = index.static_blocks(s1["off_t"], self.BN)
-        self.blocks = index.static_chunks(s1["off_t"], self.BN, self.CB)
+        self.blocks = index.static_chunks(s1["off_t"], self.BN, self.CB)  # first pass: global 32-row blocks
+        self.rchunks = index.row_chunks(s1["off_t"], self.BN * self.CB)   # emit: chunks from each cell's start
         N = Z.shape[0]
         if int(s1["off_t"][-1]) != N or int(self.blocks[3].max()) > N:
             raise ValueError("EngineI8: cell offsets do not match the code rows")
@@ -143,7 +144,7 @@ class EngineI8:
         bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
         bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
         pr = prn
-        _lib.i8_scan(1, self.blocks, q8, qs, pr, self.Z, self.zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
+        _lib.i8_scan(1, self.rchunks, q8, qs, pr, self.Z, self.zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
         pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, min(kd, K - 1), delta)
         self._est1, self._ncnt, self._t0, self._cnt = est1, ncnt, t0, cnt
         self._bm, self._bval, self._bpos, self._n1, self._M = bm, bval, bpos, n1, M

@@ -102,9 +102,9 @@ def static_blocks(off_t, BN=32):
 
 
 def static_chunks(off_t, BN=32, CB=8):
-    """Work items of the stage-1 kernels: every cell's static blocks (static_blocks) grouped into chunks of
-    up to CB consecutive blocks. Returns (cell, first global block, cell start, cell end) int32 tensors;
-    each item covers blocks [blk0, min(blk0 + CB, last block of the cell + 1))."""
+    """Work items of the first pass: every cell's static blocks (static_blocks) grouped into chunks of up
+    to CB consecutive global blocks. Returns (cell, first row = BN * first global block, cell start, cell
+    end) int32 tensors; each item covers blocks [blk0, min(blk0 + CB, last block of the cell + 1))."""
     off = off_t.long()
     s, e = off[:-1], off[1:]
     nb = torch.where(e > s, (e - 1) // BN - s // BN + 1, torch.zeros_like(s))
@@ -113,7 +113,22 @@ def static_chunks(off_t, BN=32, CB=8):
     first = torch.cumsum(nch, 0) - nch
     blk0 = s[cell] // BN + CB * (torch.arange(len(cell), device=off.device) - first[cell])
     i32 = lambda x: x.to(torch.int32).contiguous()
-    return i32(cell), i32(blk0), i32(s[cell]), i32(e[cell])
+    return i32(cell), i32(blk0 * BN), i32(s[cell]), i32(e[cell])
+
+
+def row_chunks(off_t, rows=256):
+    """Work items of the emit pass: every non-empty cell's rows in chunks of `rows` from its first row.
+    Returns (cell, first row, cell start, cell end) int32 tensors. The emitted set is per row, so any
+    grouping gives the same candidates; starting at the cell's first row leaves no 32-row block that
+    straddles the cell start, and a cell of up to `rows` rows is a single item."""
+    off = off_t.long()
+    s, e = off[:-1], off[1:]
+    nch = (e - s + rows - 1) // rows
+    cell = torch.repeat_interleave(torch.arange(len(s), device=off.device), nch)
+    first = torch.cumsum(nch, 0) - nch
+    r0 = s[cell] + rows * (torch.arange(len(cell), device=off.device) - first[cell])
+    i32 = lambda x: x.to(torch.int32).contiguous()
+    return i32(cell), i32(r0), i32(s[cell]), i32(e[cell])
 
 
 def build_index(X16, nlist=4096, R=256, bits_per_dim=2.5, seed=0, with_codes=True):

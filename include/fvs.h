@@ -114,10 +114,13 @@ int fvs_pairs2(const int32_t *probe, int64_t B, int32_t npr, int32_t n1, int32_t
  * bpos, bmc, CAP, MB) (throughput/civf8.py:89-91), which the Triton pair _first8c/_emit8c
  * (throughput/ivf8c_kern.py:2-36) also implements; plus qrank/n1 so that the first pass writes each
  * query's block maxima straight into its own row.
- *   One workgroup per item p < P: a cell and up to 8 consecutive global 32-row blocks of it (pcell, pblk,
- *   ps, pe: the cell, the first global block index, and the cell's first and end row; the item covers
- *   blocks pblk .. min(pblk + 7, (pe - 1) / 32)). The items must cover each static (cell, block) of the
- *   reference's work list (src/s1cell.py:161-168) exactly once. For every query q of the cell's pair list:
+ *   One workgroup per item p < P: a cell and up to 256 consecutive rows of it (pcell, prow, ps, pe: the
+ *   cell, the item's first row, and the cell's first and end row; the item covers rows
+ *   [max(prow, ps), min(prow + 256, pe)) as eight 32-row blocks starting at prow). Mode 0: prow is a
+ *   multiple of 32 and the items cover each static (cell, global 32-row block) of the reference's work
+ *   list (src/s1cell.py:161-168) exactly once. Mode 1: the items cover each row of each cell exactly
+ *   once (any grouping; prow = ps + 256 j is the one that wastes least). For every query q of the cell's
+ *   pair list:
  *     acc = sum_j q8[q][j] * Z[n][j] (int32, exact), est = fmaf((float)acc * qs[q], zs[n], qcp[pair]).
  *   mode 0 (first pass): bm[(q*n1 + qrank[pair])*MB + blk - cs/32] = max over the block's rows in the
  *     cell; entries of blocks a cell does not have are left untouched.
@@ -127,7 +130,7 @@ int fvs_pairs2(const int32_t *probe, int64_t B, int32_t npr, int32_t n1, int32_t
  */
 int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
                 const int32_t *qrank, const int32_t *coff, const int32_t *ccnt, const int32_t *pcell,
-                const int32_t *pblk, const int32_t *ps, const int32_t *pe, const int8_t *Z, const float *zs,
+                const int32_t *prow, const int32_t *ps, const int32_t *pe, const int8_t *Z, const float *zs,
                 int64_t N, int32_t R, const float *qcp, const float *t0, int32_t *cnt, float *bval,
                 int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
 

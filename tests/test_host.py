@@ -19,15 +19,35 @@ def test_static_chunks_cover_every_static_block_once(oracle_mod):
     off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
     cell, blk, ps, pe, MB = oracle_mod.static_blocks(off)
     want = sorted(zip(cell.tolist(), blk.tolist()))
-    c, b0, s, e = (t.numpy() for t in index.static_chunks(torch.from_numpy(off), 32, 8))
+    c, r0, s, e = (t.numpy() for t in index.static_chunks(torch.from_numpy(off), 32, 8))
+    assert (r0 % 32 == 0).all()
     got = []
     for i in range(len(c)):
         last = (e[i] - 1) // 32
         assert s[i] == off[c[i]] and e[i] == off[c[i] + 1]
-        got += [(int(c[i]), int(bb)) for bb in range(b0[i], min(b0[i] + 8, last + 1))]
+        got += [(int(c[i]), int(bb)) for bb in range(r0[i] // 32, min(r0[i] // 32 + 8, last + 1))]
     assert sorted(got) == want and len(got) == len(set(got))
     _, MBt = index.static_blocks(torch.from_numpy(off), 32)
     assert MBt == MB
+
+
+def test_row_chunks_cover_every_row_once():
+    """Emit items: each row of each cell in exactly one item of at most 256 rows, the first item of a
+    cell at its first row, and a cell of up to 256 rows in one item."""
+    rng = np.random.default_rng(3)
+    sizes = rng.integers(0, 700, 60)
+    sizes[[2, 9]] = 0
+    sizes[[4, 5, 6]] = [256, 257, 512]
+    off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    c, r0, s, e = (t.numpy() for t in index.row_chunks(torch.from_numpy(off), 256))
+    seen = np.zeros(off[-1], np.int32)
+    for i in range(len(c)):
+        assert s[i] == off[c[i]] and e[i] == off[c[i] + 1] and s[i] <= r0[i] < e[i]
+        seen[r0[i]:min(r0[i] + 256, e[i])] += 1
+    assert (seen == 1).all()
+    items = np.bincount(c, minlength=len(sizes))
+    assert (items == (sizes + 255) // 256).all()
+    assert items[4] == 1 and items[5] == 2 and items[6] == 2
 
 
 def test_unimplemented_knobs_raise():
