@@ -24,6 +24,7 @@ SIGNATURES = {
     "fvs_abi_version": [],
     "fvs_error_string": [ctypes.c_int],
     "fvs_fill_u32": [P, I64, U32, P],
+    "fvs_pack_ids": [P, P, I64, I32, P, P],
     "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
@@ -104,6 +105,14 @@ def fill_u32(t, value):
     if t.element_size() != 4:
         raise TypeError("fill_u32: 32-bit tensor expected")
     _check(lib().fvs_fill_u32(_dev(t, t.dtype, "dst"), t.numel(), U32(value), _stream()), "fvs_fill_u32")
+
+
+def pack_ids(ok, I, out):
+    """out int64 [B, k+1] = [ok | I] in one launch; out may be a pinned host tensor, written directly."""
+    B, k = I.shape
+    _check(lib().fvs_pack_ids(_dev(ok.view(torch.uint8), torch.uint8, "ok", (B,)), _dev(I, torch.int32, "I"), B, k,
+                              _dev(out, torch.int64, "out", (B, k + 1), host_ok=True), _stream()), "fvs_pack_ids")
+    return out
 
 
 def query_prep(Q, Vr, c, z=None):

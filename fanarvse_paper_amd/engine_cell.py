@@ -116,8 +116,7 @@ class EngineS:
             def run():
                 outs = self._gpu(qs, K, z, nprobe, k)
                 if host:
-                    hb.copy_(torch.cat([outs[0].to(torch.int64)[:, None], outs[1].to(torch.int64)], 1),
-                             non_blocking=True)
+                    _lib.pack_ids(outs[0], outs[1], hb)  # one launch writes the pinned buffer directly
                 else:
                     hb.copy_(outs[0], non_blocking=True)
                 return outs

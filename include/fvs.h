@@ -47,6 +47,15 @@ const char *fvs_error_string(int code);
 int fvs_fill_u32(void *dst, int64_t n, uint32_t value, void *stream);
 
 /*
+ * The latency path's host result in one launch: out i64 [B, k+1] = [ok[q] | I[q][0..k)] (ok u8 [B],
+ * I i32 [B, k]). out may be pinned host memory: the launch writes it directly, and the values are
+ * visible to the host once the stream has been synchronised. Replaces the int64 casts, the
+ * concatenation and the device-to-host copy of the flags and ids that src/engine_cell.py:152-165
+ * performs after its graph (ok.cpu(), I.cpu()).
+ */
+int fvs_pack_ids(const uint8_t *ok, const int32_t *I, int64_t B, int32_t k, int64_t *out, void *stream);
+
+/*
  * Query code (a6) plus the global-centre term and the fp16 copy of the queries.
  * Replaces throughput/enginei8.py:38 (qs = max|z|/127; q8 = round(z/qs), with z = Qb @ Vr computed by
  * the caller's fp32 BLAS as in the reference), throughput/enginei8.py:62 (QC = Qb @ c) and the

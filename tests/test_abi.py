@@ -48,6 +48,8 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_select(n, n, n, 4, 16, 5000, 0, 0.0, n, n, n, n, n) == E_CAP          # K > 4096
     assert L.fvs_select(n, n, n, 4, 16, 8, 8, 0.0, n, n, n, n, n) == E_ARG             # kd >= K
     assert L.fvs_route_topk(n, 4, 100, 0, n, n) == E_ARG
+    assert L.fvs_pack_ids(n, n, 4, 0, n, n) == E_ARG                                  # k = 0
+    assert L.fvs_pack_ids(n, n, 0, 10, n, n) == 0                                     # empty batch
     assert L.fvs_route_topk(n, 4, 100, 101, n, n) == E_ARG                             # nprobe > NC
     assert L.fvs_i8_scan(0, 10, *[n] * 12, 100, 128, *[n] * 6, 1, 1, 1, n) == E_SHAPE  # R != 256
     assert L.fvs_i8_scan(2, 10, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == E_ARG    # bad mode

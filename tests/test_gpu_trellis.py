@@ -152,11 +152,31 @@ def test_lean_path_matches_search(env, B):
     returns search's top-k ids."""
     E = env["E"]
     Q = env["Q"][:B].contiguous()
+    Q2 = env["Q"].flip(0)[:B].contiguous()  # another batch: a stale host buffer would show the other's ids
     I = npy(E.search(Q, K, Z_, NPROBE, KK)[0])
+    I2 = npy(E.search(Q2, K, Z_, NPROBE, KK)[0])
     for _ in range(2):
-        h = E.search_host(Q, K, Z_, NPROBE, KK)
-        assert h.dtype == np.int64 and h.shape == (B, KK)
-        assert np.array_equal(h, I)
+        for q, want in ((Q, I), (Q2, I2)):
+            h = E.search_host(q, K, Z_, NPROBE, KK)
+            assert h.dtype == np.int64 and h.shape == (B, KK)
+            assert np.array_equal(h, want)
+
+
+def test_pack_ids_to_pinned_and_device():
+    """fvs_pack_ids writes [ok | ids] as int64 straight into pinned host memory (and device memory)."""
+    from fanarvse_paper_amd import _lib
+
+    g = torch.Generator(device="cpu").manual_seed(5)
+    for B, k in ((1, 10), (37, 10), (300, 100)):
+        ok = (torch.rand(B, generator=g) > 0.3).to(torch.uint8).cuda()
+        I = torch.randint(-1, 1 << 30, (B, k), generator=g, dtype=torch.int32).cuda()
+        want = torch.cat([ok.long()[:, None], I.long()], 1).cpu().numpy()
+        host = torch.full((B, k + 1), -7, dtype=torch.int64, pin_memory=True)
+        dev = torch.full((B, k + 1), -7, dtype=torch.int64, device="cuda")
+        _lib.pack_ids(ok.view(torch.bool), I, host)
+        _lib.pack_ids(ok.view(torch.bool), I, dev)
+        torch.cuda.current_stream().synchronize()
+        assert np.array_equal(host.numpy(), want) and np.array_equal(dev.cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("B", [1, 5, 64])
