@@ -96,36 +96,62 @@ __device__ __forceinline__ int fvs_block_scan(int v, int *tmp) {
 }
 __device__ __forceinline__ int fvs_block_scan256(int v, int *tmp) { return fvs_block_scan<256>(v, tmp); }
 
+// One radix pass's bucket choice, made by wave 0 alone: the 256 bins in descending order, four per lane,
+// one wave prefix sum; the lane whose range holds the k-th key writes (bucket, k - keys above it, bucket
+// size) to sh[R], sh[R + 1], sh[R + 2]. Every bin is zeroed as it is read, ready for the next pass.
+template <int R>
+__device__ __forceinline__ void fvs_pick_bucket(int *hist, int *sh, int k) {
+  const int lane = threadIdx.x & 63;
+  int h[4], s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int b = 255 - 4 * lane - j;
+    h[j] = hist[b];
+    hist[b] = 0;
+    s += h[j];
+  }
+  int inc = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, FVS_WAVE);
+    if (lane >= o) inc += t;
+  }
+  int e = inc - s;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    if (e < k && k <= e + h[j]) {
+      sh[R] = 255 - 4 * lane - j;
+      sh[R + 1] = k - e;
+      sh[R + 2] = h[j];
+    }
+    e += h[j];
+  }
+}
+
 // k-th largest (1-based, counted with multiplicity) of n keys key(i), 1 <= k <= n, by an MSD radix
-// select of 8 bits per pass. Block of NT >= 256 threads; hist: 256 ints of LDS, sh: fvs_sh_ints(NT)
-// ints of LDS. Every thread returns the same key.
+// select of 8 bits per pass: per pass a histogram of the keys that match the prefix so far, one
+// barrier, the bucket choice by wave 0, one barrier. Block of NT >= 256 threads; hist: 256 ints of LDS,
+// sh: fvs_sh_ints(NT) ints of LDS. Every thread returns the same key.
 template <typename KT, int NT = 256, typename F>
 __device__ KT fvs_block_kth(F key, int n, int k, int *hist, int *sh) {
   static_assert(NT >= 256 && NT % 64 == 0, "block of at least 256 threads");
   constexpr int R = NT / 64;
   KT prefix = 0, pmask = 0;
+  if (threadIdx.x < 256) hist[threadIdx.x] = 0;
+  __syncthreads();
   for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
-    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
-    __syncthreads();
     for (int i = threadIdx.x; i < n; i += NT) {
       KT x = key(i);
       if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
     }
     __syncthreads();
-    const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
-    const int h = threadIdx.x < 256 ? hist[b] : 0;
-    const int inc = fvs_block_scan<NT>(h, sh);
-    const int exc = inc - h;
-    if (threadIdx.x < 256 && exc < k && k <= inc) {
-      sh[R] = b;
-      sh[R + 1] = k - exc;
-    }
+    if (fvs_wave_id() == 0) fvs_pick_bucket<R>(hist, sh, k);
     __syncthreads();
     prefix |= (KT)sh[R] << shift;
     pmask |= (KT)0xff << shift;
     k = sh[R + 1];
-    __syncthreads();
   }
+  __syncthreads();  // every thread has read sh before the caller reuses it
   return prefix;
 }
 
@@ -165,31 +191,22 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
   static_assert(NT >= 256 && NT % 64 == 0, "block of at least 256 threads");
   constexpr int R = NT / 64;
   KT prefix = 0, pmask = 0;
+  if (threadIdx.x < 256) hist[threadIdx.x] = 0;
+  __syncthreads();
   for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
-    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
-    __syncthreads();
     for (int i = threadIdx.x; i < n; i += NT) {
       KT x = key(i);
       if ((x & pmask) == prefix) atomicAdd(&hist[(int)((x >> shift) & 0xff)], 1);
     }
     __syncthreads();
-    const int b = 255 - (int)threadIdx.x;  // thread order = descending bucket
-    const int h = threadIdx.x < 256 ? hist[b] : 0;
-    const int inc = fvs_block_scan<NT>(h, sh);
-    const int exc = inc - h;
-    if (threadIdx.x < 256 && exc < k && k <= inc) {
-      sh[R] = b;
-      sh[R + 1] = k - exc;
-      sh[R + 2] = h;
-    }
+    if (fvs_wave_id() == 0) fvs_pick_bucket<R>(hist, sh, k);
     __syncthreads();
     prefix |= (KT)sh[R] << shift;
     pmask |= (KT)0xff << shift;
     k = sh[R + 1];
-    const bool whole = sh[R + 2] == k;
-    __syncthreads();
-    if (whole) break;
+    if (sh[R + 2] == k) break;  // the whole bucket is in (the same decision in every thread)
   }
+  __syncthreads();  // every thread has read sh (and hist is zero) before the caller reuses them
   return prefix;
 }
 
