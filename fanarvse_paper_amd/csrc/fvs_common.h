@@ -75,8 +75,8 @@ __device__ __forceinline__ float fvs_wave_max(float v) {
 }
 
 // Ints of LDS the block helpers below need for their `sh` argument with NT threads: NT / 64 for the scan,
-// then three results.
-__host__ __device__ constexpr int fvs_sh_ints(int NT) { return NT / 64 + 4; }
+// then up to six results.
+__host__ __device__ constexpr int fvs_sh_ints(int NT) { return NT / 64 + 8; }
 
 // Inclusive prefix sum over threadIdx.x for a block of NT threads (a multiple of 64). tmp: NT/64 ints.
 template <int NT = 256>
@@ -181,6 +181,38 @@ __host__ __device__ __forceinline__ int fvs_pow2_ceil(int n) {
   int p = 1;
   while (p < n) p <<= 1;
   return p;
+}
+
+// Two k-th largest selections in the same passes: (the kA-th largest of keyA, the kB-th largest of keyB)
+// over i < n, 1 <= kA, kB <= n. Waves 0 and 1 pick the two buckets of a pass concurrently, so both
+// cost the barriers of one. hist: 512 ints of LDS. Block of NT >= 256 threads.
+template <typename KT, int NT = 256, typename FA, typename FB>
+__device__ void fvs_block_kth2(FA keyA, FB keyB, int n, int kA, int kB, int *hist, int *sh, KT &outA, KT &outB) {
+  static_assert(NT >= 256 && NT % 64 == 0, "block of at least 256 threads");
+  constexpr int R = NT / 64;
+  KT pa = 0, pb = 0, pmask = 0;
+  for (int i = threadIdx.x; i < 512; i += NT) hist[i] = 0;
+  __syncthreads();
+  for (int shift = (int)sizeof(KT) * 8 - 8; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < n; i += NT) {
+      const KT a = keyA(i), b = keyB(i);
+      if ((a & pmask) == pa) atomicAdd(&hist[(int)((a >> shift) & 0xff)], 1);
+      if ((b & pmask) == pb) atomicAdd(&hist[256 + (int)((b >> shift) & 0xff)], 1);
+    }
+    __syncthreads();
+    const int w = fvs_wave_id();
+    if (w == 0) fvs_pick_bucket<R>(hist, sh, kA);
+    if (w == 1) fvs_pick_bucket<R + 3>(hist + 256, sh, kB);
+    __syncthreads();
+    pa |= (KT)sh[R] << shift;
+    pb |= (KT)sh[R + 3] << shift;
+    pmask |= (KT)0xff << shift;
+    kA = sh[R + 1];
+    kB = sh[R + 4];
+  }
+  __syncthreads();
+  outA = pa;
+  outB = pb;
 }
 
 // A bound T with #{i : key(i) >= T} == kk for n UNIQUE keys, 1 <= kk <= n: the MSD radix select of

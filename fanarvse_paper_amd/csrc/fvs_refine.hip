@@ -18,7 +18,7 @@ constexpr int kSmallB = 64;    // batches up to this size use 1024-thread blocks
 
 struct RefineLds {  // fixed part; the per-slot arrays follow in dynamic LDS
   uint64_t s[kMaxk];
-  int hist[256];
+  int hist[512];
   int sh[fvs_sh_ints(1024)];
   int namb, gcnt;
 };
@@ -91,8 +91,10 @@ __global__ __launch_bounds__(NT) void k_refine(const float *__restrict__ est, co
   }
   if (tid == 0) L.namb = 0;
   __syncthreads();
-  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t, NT>([&](int i) { return fvs_ord32(hi[i]); }, K, k + 1, L.hist, L.sh));
-  const float lk = fvs_unord32(fvs_block_kth<uint32_t, NT>([&](int i) { return fvs_ord32(lo[i]); }, K, k, L.hist, L.sh));
+  uint32_t hk1u, lku;  // the (k+1)-th largest upper bound and the k-th largest lower bound, in one set of passes
+  fvs_block_kth2<uint32_t, NT>([&](int i) { return fvs_ord32(hi[i]); }, [&](int i) { return fvs_ord32(lo[i]); }, K,
+                               k + 1, k, L.hist, L.sh, hk1u, lku);
+  const float hk1 = fvs_unord32(hk1u), lk = fvs_unord32(lku);
   for (int i = tid; i < K; i += NT) {
     const bool sure = lo[i] > hk1;
     const bool am = (hi[i] >= lk) && !sure;
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(256) void k_classify(const float *__restrict__ est,
                                                   int K, float z, int k, int32_t *__restrict__ ids,
                                                   uint8_t *__restrict__ flag, int32_t *__restrict__ namb,
                                                   int32_t *__restrict__ aslot) {
-  __shared__ int hist[256];
+  __shared__ int hist[512];
   __shared__ int sh[fvs_sh_ints(256)];
   extern __shared__ uint8_t dyn[];
   float *lo = reinterpret_cast<float *>(dyn);  // [K]
@@ -165,8 +167,10 @@ __global__ __launch_bounds__(256) void k_classify(const float *__restrict__ est,
     ids[q * (int64_t)K + i] = order ? order[pq[i]] : pq[i];
   }
   __syncthreads();
-  const float hk1 = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(hi[i]); }, K, k + 1, hist, sh));
-  const float lk = fvs_unord32(fvs_block_kth<uint32_t>([&](int i) { return fvs_ord32(lo[i]); }, K, k, hist, sh));
+  uint32_t hk1u, lku;
+  fvs_block_kth2<uint32_t>([&](int i) { return fvs_ord32(hi[i]); }, [&](int i) { return fvs_ord32(lo[i]); }, K, k + 1,
+                           k, hist, sh, hk1u, lku);
+  const float hk1 = fvs_unord32(hk1u), lk = fvs_unord32(lku);
   int base = 0;
   for (int i0 = 0; i0 < K; i0 += 256) {
     const int i = i0 + tid;
