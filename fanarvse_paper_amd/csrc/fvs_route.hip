@@ -766,41 +766,42 @@ int64_t pairs_pitch(int64_t B) { return (B + kTileQ - 1) / kTileQ * kTileQ; }
 int64_t matrix_bytes(int64_t B, int NC) { return ((int64_t)NC * pairs_pitch(B) * 2 + 255) / 256 * 256; }
 
 // One or two pair lists (first na columns, and first nb columns when lb is given) from one rank matrix.
-// Small batches (B <= kPairsSmallB, NC <= kPairsSmallNC): the whole builder in one workgroup. The per-cell
-// counts of both lists sit in LDS (atomics over the probe rows), one block scan turns them into offsets,
-// and the queries are then emitted one at a time in ascending order: a query's probed cells are distinct,
-// so its pairs take consecutive per-cell cursors without atomics, and each cell's pairs come out in
-// ascending query order, as the matrix builder writes them. Same outputs, bit for bit, in one launch
-// instead of four.
-constexpr int kPairsSmallB = 64;
-constexpr int kPairsSmallNC = 8192;
+// Small batches (B <= kPairsSmallB, NC <= kPairsSmallNC): the whole builder in one workgroup. Each cell's queries
+// are a 64-bit mask in LDS, one per list (atomic ORs over the probe rows); a block scan of their
+// popcounts gives the offsets, and every pair then finds its slot at once: the cell's offset plus the
+// number of lower queries in the cell's mask. That is the ascending query order of the matrix builder,
+// bit for bit, in one launch instead of four. One workgroup runs out of memory parallelism as the batch
+// grows: at 64 queries the four-launch builder is faster again, so batches above 16 use it.
+constexpr int kPairsSmallB = 16;  // <= 64 (one mask bit per query)
+constexpr int kPairsSmallNC = 4096;
 
 __global__ __launch_bounds__(1024) void k_pairs_small(const int32_t *__restrict__ probe, int B, int npr, int NC,
                                                       const uint16_t *__restrict__ QM, const float *__restrict__ mnorm,
                                                       const float *__restrict__ qadd, int32_t *__restrict__ ccnt_a,
                                                       PairList la, int32_t *__restrict__ ccnt_b, PairList lb, int two) {
-  __shared__ int cur[2][kPairsSmallNC];
+  __shared__ uint64_t qm[2][kPairsSmallNC];  // queries of each cell, per list
+  __shared__ int off[2][kPairsSmallNC];      // each cell's first slot, per list
   __shared__ int wsum[2][1024 / FVS_WAVE];
   const int t = threadIdx.x, lane = t & (FVS_WAVE - 1), w = fvs_wave_id();
   for (int c = t; c < NC; c += 1024) {
-    cur[0][c] = 0;
-    cur[1][c] = 0;
+    qm[0][c] = 0ull;
+    qm[1][c] = 0ull;
   }
   __syncthreads();
   const int n = two ? (int)max(la.n, lb.n) : (int)la.n;
   for (int i = t; i < B * n; i += 1024) {
     const int q = i / n, r = i - q * n;
     const int c = probe[(int64_t)q * npr + r];
-    if (r < (int)la.n) atomicAdd(&cur[0][c], 1);
-    if (two && r < (int)lb.n) atomicAdd(&cur[1][c], 1);
+    if (r < (int)la.n) atomicOr(&qm[0][c], 1ull << q);
+    if (two && r < (int)lb.n) atomicOr(&qm[1][c], 1ull << q);
   }
   __syncthreads();
-  // exclusive scans: thread t owns the run of cells [t * per, t * per + per)
+  // exclusive scans of the counts: thread t owns the run of cells [t * per, t * per + per)
   const int per = (NC + 1023) / 1024;
   const int c0 = t * per, c1 = min(c0 + per, NC);
   for (int l = 0; l < 1 + two; l++) {
     int run = 0;
-    for (int c = c0; c < c1; c++) run += cur[l][c];
+    for (int c = c0; c < c1; c++) run += __popcll(qm[l][c]);
     const int inc = wave_incl_scan_i32(run, lane);
     if (lane == FVS_WAVE - 1) wsum[l][w] = inc;
     __syncthreads();
@@ -809,34 +810,32 @@ __global__ __launch_bounds__(1024) void k_pairs_small(const int32_t *__restrict_
     int32_t *ccnt = l ? ccnt_b : ccnt_a;
     int32_t *coff = const_cast<int32_t *>(l ? lb.coff : la.coff);
     for (int c = c0; c < c1; c++) {
-      const int k = cur[l][c];
+      const int k = __popcll(qm[l][c]);
       ccnt[c] = k;
       coff[c] = base;
-      cur[l][c] = base;  // becomes the cell's write cursor
+      off[l][c] = base;
       base += k;
     }
   }
   __syncthreads();
-  for (int q = 0; q < B; q++) {
-    const float add = qadd ? qadd[q] : 0.f;
-    for (int r = t; r < n; r += 1024) {
-      const int c = probe[(int64_t)q * npr + r];
-      float x = fvs_h2f(QM[(int64_t)q * NC + c]) * (mnorm ? mnorm[c] : 1.0f);
-      if (qadd) x = x + add;
-      if (r < (int)la.n) {
-        const int o = cur[0][c]++;
-        la.qid[o] = q;
-        la.qrank[o] = r;
-        la.qcp[o] = x;
-      }
-      if (two && r < (int)lb.n) {
-        const int o = cur[1][c]++;
-        lb.qid[o] = q;
-        lb.qrank[o] = r;
-        lb.qcp[o] = x;
-      }
+  for (int i = t; i < B * n; i += 1024) {
+    const int q = i / n, r = i - q * n;
+    const int c = probe[(int64_t)q * npr + r];
+    const uint64_t below = (1ull << q) - 1ull;  // q < 64
+    float x = fvs_h2f(QM[(int64_t)q * NC + c]) * (mnorm ? mnorm[c] : 1.0f);
+    if (qadd) x = x + qadd[q];
+    if (r < (int)la.n) {
+      const int o = off[0][c] + __popcll(qm[0][c] & below);
+      la.qid[o] = q;
+      la.qrank[o] = r;
+      la.qcp[o] = x;
     }
-    __syncthreads();  // the next query may probe the same cells
+    if (two && r < (int)lb.n) {
+      const int o = off[1][c] + __popcll(qm[1][c] & below);
+      lb.qid[o] = q;
+      lb.qrank[o] = r;
+      lb.qcp[o] = x;
+    }
   }
 }
 

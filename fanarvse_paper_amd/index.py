@@ -18,6 +18,17 @@ import torch
 from . import _lib, s2lut
 
 
+def segment_sum(x, seg, n):
+    """Row sums of x per segment id (seg sorted ascending, ids < n) as an [n, cols] tensor. Each segment is
+    reduced on its own and written to its own row, so the result is the same on every run (a float
+    index_add_ on the GPU adds with atomics, in an order that changes from run to run)."""
+    out = torch.zeros((n, x.shape[1]), dtype=x.dtype, device=x.device)
+    if len(seg):
+        ids, counts = torch.unique_consecutive(seg, return_counts=True)
+        out[ids] = torch.segment_reduce(x, "sum", lengths=counts, axis=0)
+    return out
+
+
 def spherical_kmeans(X16, nlist, seed=0, iters=15, sample=200000, chunk=50000):
     """Spherical k-means centroids (unit rows) fitted on a random sample (src/ideas_engine2.py:27-33)."""
     g = np.random.default_rng(seed)
@@ -27,7 +38,8 @@ def spherical_kmeans(X16, nlist, seed=0, iters=15, sample=200000, chunk=50000):
     cen = samp[torch.from_numpy(g.permutation(len(samp))[:nlist]).to(X16.device)].clone()
     for _ in range(iters):
         a = torch.cat([(samp[j:j + chunk] @ cen.T).argmax(1) for j in range(0, len(samp), chunk)])
-        cen = torch.nn.functional.normalize(torch.zeros_like(cen).index_add_(0, a, samp) + 1e-9, dim=1)
+        o = torch.argsort(a, stable=True)
+        cen = torch.nn.functional.normalize(segment_sum(samp[o], a[o], nlist) + 1e-9, dim=1)
     return cen
 
 
@@ -47,8 +59,8 @@ def build_stage1_cells(X16, nlist=4096, seed=0):
     off = torch.searchsorted(A[order].contiguous(), torch.arange(nlist + 1, device=dev))
     cell = A[order]
     means = torch.zeros(nlist, X16.shape[1], device=dev)
-    for j in range(0, N, 65536):
-        means.index_add_(0, cell[j:j + 65536], X16[order[j:j + 65536]].float())
+    for j in range(0, N, 65536):  # rows are in cell order: per chunk, segment sums added in chunk order
+        means += segment_sum(X16[order[j:j + 65536]].float(), cell[j:j + 65536], nlist)
     cnt = (off[1:] - off[:-1]).clamp(min=1).float()
     means /= cnt[:, None]
     means16 = means.half().contiguous()

@@ -161,3 +161,17 @@ def test_emit_region_overflow(coarse, oracle_mod):
     finally:
         E.MSZ = msz
     assert np.mean(out["cnt"]) > 4000 and out["cnt"].max() <= 65536
+
+
+def test_index_build_is_deterministic():
+    """Two builds of the same rows give identical tables (cell sums are segment reductions, not float
+    atomics), so bench runs and saved indexes are reproducible."""
+    print("\n[gpu edges] index build twice", flush=True)
+    X = datagen.gen(40000, 768, 32, 0.7, seed=15, device="cuda")
+    a = index.build_index(X, nlist=128)
+    b = index.build_index(X, nlist=128)
+    for k in ("order", "off_t", "means16", "inv_mnorm"):
+        assert torch.equal(a[0][k], b[0][k]), k
+    assert torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])  # int8 codes and scales
+    ta, tb = trellis.build_index(X, nlist=128), trellis.build_index(X, nlist=128)
+    assert torch.equal(ta[0]["words"], tb[0]["words"]) and torch.equal(ta[0]["scale1"], tb[0]["scale1"])
