@@ -140,7 +140,88 @@ __global__ __launch_bounds__(256) void k_query_code(const float *__restrict__ z,
   if (lane == 0) qc[q] = (float)s;
 }
 
+// The three dense products of a small batch in one launch, one wave per output row:
+//   rows [0, R):          Qr[b][j] = <Q[b], W1T[j]>            (f32)
+//   rows [R, R + NC):     QM[b][c] = fp16(<fp16(Q[b]), M16[c]>) (fp16 inputs, f32 sum, one rounding)
+//   rows [R + NC, +D):    Zq[b][t] = <Q[b], VPT[t]>            (f32)
+// Each lane sums its 4-element slices of the row in k order for every query of the batch, then a fixed
+// xor butterfly reduces the lanes. The products are the BLAS ones of a large batch, computed where
+// three library launches would each cost more than the 24 MB they read.
+constexpr int kDenseMaxB = 8;
+
+__global__ __launch_bounds__(256) void k_dense_small(const float *__restrict__ Q, int B, int d,
+                                                     const float *__restrict__ W1T, int R, float *__restrict__ Qr,
+                                                     const uint16_t *__restrict__ M16, int NC,
+                                                     uint16_t *__restrict__ QM, const float *__restrict__ VPT, int D,
+                                                     float *__restrict__ Zq) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + fvs_wave_id();
+  if (row >= R + NC + D) return;  // wave-uniform; no barrier below
+  const int kind = row < R ? 0 : (row < R + NC ? 1 : 2);
+  float acc[kDenseMaxB];
+#pragma unroll
+  for (int b = 0; b < kDenseMaxB; b++) acc[b] = 0.f;
+  for (int i0 = 4 * lane; i0 < d; i0 += 256) {
+    float x[4];
+    if (kind == 1) {
+      const uint2 h = *reinterpret_cast<const uint2 *>(M16 + (int64_t)(row - R) * d + i0);
+      x[0] = fvs_h2f((uint16_t)(h.x & 0xffffu));
+      x[1] = fvs_h2f((uint16_t)(h.x >> 16));
+      x[2] = fvs_h2f((uint16_t)(h.y & 0xffffu));
+      x[3] = fvs_h2f((uint16_t)(h.y >> 16));
+    } else {
+      const float *src = kind == 0 ? W1T + (int64_t)row * d : VPT + (int64_t)(row - R - NC) * d;
+      const float4 v = *reinterpret_cast<const float4 *>(src + i0);
+      x[0] = v.x;
+      x[1] = v.y;
+      x[2] = v.z;
+      x[3] = v.w;
+    }
+#pragma unroll
+    for (int b = 0; b < kDenseMaxB; b++) {
+      if (b < B) {
+        const float4 qv = *reinterpret_cast<const float4 *>(Q + (int64_t)b * d + i0);
+        float q[4] = {qv.x, qv.y, qv.z, qv.w};
+        if (kind == 1) {
+#pragma unroll
+          for (int u = 0; u < 4; u++) q[u] = fvs_h2f(fvs_f2h(q[u]));  // the fp16 copy of the query
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[b] = __builtin_fmaf(q[u], x[u], acc[b]);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kDenseMaxB; b++) {
+    if (b < B) {
+      float v = acc[b];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, FVS_WAVE);
+      if (lane == 0) {
+        if (kind == 0)
+          Qr[(int64_t)b * R + row] = v;
+        else if (kind == 1)
+          QM[(int64_t)b * NC + row - R] = fvs_f2h(v);
+        else
+          Zq[(int64_t)b * D + row - R - NC] = v;
+      }
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int fvs_dense_small(const float *Q, int64_t B, int32_t d, const float *W1T, int32_t R, float *Qr,
+                               const uint16_t *M16, int32_t NC, uint16_t *QM, const float *VPT, int32_t D, float *Zq,
+                               void *stream) {
+  if (B < 0 || B > kDenseMaxB || d <= 0 || d % 4 != 0 || R < 0 || NC < 0 || D < 0) return FVS_E_ARG;
+  if (B == 0 || R + NC + D == 0) return FVS_OK;
+  if (!Q || (R && (!W1T || !Qr)) || (NC && (!M16 || !QM)) || (D && (!VPT || !Zq))) return FVS_E_ARG;
+  const int64_t rows = (int64_t)R + NC + D;
+  hipLaunchKernelGGL(k_dense_small, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, Q, (int)B, d,
+                     W1T, R, Qr, M16, NC, QM, VPT, D, Zq);
+  return fvs_launch_status();
+}
 
 extern "C" int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *z, int32_t R, const float *c,
                               int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream) {

@@ -39,6 +39,9 @@ class EngineS:
         self.W1 = s1["W1"].contiguous()
         self.inv_mnorm = s1["inv_mnorm"].float().contiguous()
         self.means16 = s1["means16"].contiguous()
+        # row-major transposes for the one-launch dense products of small batches (_lib.dense_small)
+        self.W1T = self.W1.T.contiguous()
+        self.VPT = code["VP"].float().T.contiguous()
         self.graphs = {}
         self.nbad = 0
         self._done = torch.cuda.Event() if torch.cuda.is_available() else None
@@ -81,6 +84,10 @@ class EngineS:
     def _dense(self, Qb):
         """The dense products: Qr = Qb @ W1 (f32), QM = fp16(Qb) @ means16.T (fp16), Zq = Qb @ VP (f32);
         and qc = <Qb, c> (canonical double sum)."""
+        if len(Qb) <= _lib.DENSE_MAX_B:  # one launch instead of three library products
+            Qr, QM, Zq = _lib.dense_small(Qb, self.W1T, self.means16, self.VPT)
+            _, _, QC, _, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
+            return Qr, QC, QM, Zq
         Qr = (Qb @ self.W1).contiguous()
         _, _, QC, Qh, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
         QM = (Qh @ self.means16.T).contiguous()

@@ -230,3 +230,26 @@ def test_small_batch_buffer_equals_overflow_fallback(env, oracle_mod, B):
     assert np.array_equal(npy(reads), out["reads"])
     assert np.array_equal(npy(ids), out["cand"])
     assert np.array_equal(npy(sc).view(np.uint32), out["scores"].view(np.uint32))
+
+
+@pytest.mark.parametrize("B", [1, 5, 8])
+def test_dense_small_products_accuracy(env, B):
+    """The one-launch dense products of small batches against float64: Qr and Zq within the fp32
+    accumulation bound (d * 2^-24 * sum |terms|, generous by 4x), QM within that bound plus half an fp16
+    ulp of the value (one rounding of the output); the fp16 query copy is rounded as the kernel does."""
+    E = env["E"]
+    Q = env["Q"][:B].contiguous()
+    Qr, QM, Zq = _lib.dense_small(Q, E.W1T, E.means16, E.VPT)
+    torch.cuda.synchronize()
+    q = Q.double().cpu()
+    d = q.shape[1]
+    bound = lambda a, x: 4 * d * 2.0 ** -24 * (a.abs() @ x.abs())
+    for got, mat, qq in ((Qr, E.W1, q), (Zq, E.code["VP"].float(), q)):
+        m = mat.double().cpu()
+        ref = qq @ m
+        assert ((got.double().cpu() - ref).abs() <= bound(qq, m) + 1e-30).all()
+    qh = Q.half().double().cpu()
+    m = E.means16.double().cpu().T
+    ref = qh @ m
+    tol = bound(qh, m) + ref.abs() * 2.0 ** -11
+    assert ((QM.double().cpu() - ref).abs() <= tol + 1e-7).all()
