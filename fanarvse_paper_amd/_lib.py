@@ -25,7 +25,7 @@ SIGNATURES = {
     "fvs_error_string": [ctypes.c_int],
     "fvs_fill_u32": [P, I64, U32, P],
     "fvs_pack_ids": [P, P, I64, I32, P, P],
-    "fvs_dense_small": [P, I64, I32, P, I32, P, P, I32, P, P, I32, P, P],
+    "fvs_dense_small": [P, I64, I32, P, I32, P, P, I32, P, P, I32, P, P, P, P],
     "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
@@ -119,9 +119,9 @@ def pack_ids(ok, I, out):
 DENSE_MAX_B = 8
 
 
-def dense_small(Q, W1T, M16, VPT):
-    """(Qr f32 [B, R], QM fp16 [B, NC], Zq f32 [B, D]) = (Q @ W1T.T, fp16(fp16(Q) @ M16.T), Q @ VPT.T) in one
-    launch, for B <= DENSE_MAX_B (the default engine's small-batch dense products)."""
+def dense_small(Q, W1T, M16, VPT, c):
+    """(Qr f32 [B, R], QM fp16 [B, NC], Zq f32 [B, D], qc f32 [B]) = (Q @ W1T.T, fp16(fp16(Q) @ M16.T), Q @ VPT.T,
+    query_prep's <Q, c>) in one launch, for B <= DENSE_MAX_B (the default engine's small-batch products)."""
     B, d = Q.shape
     R, NC, D = W1T.shape[0], M16.shape[0], VPT.shape[0]
     if B > DENSE_MAX_B or W1T.shape[1] != d or M16.shape[1] != d or VPT.shape[1] != d:
@@ -129,11 +129,13 @@ def dense_small(Q, W1T, M16, VPT):
     Qr = _empty((B, R), torch.float32, Q.device)
     QM = _empty((B, NC), torch.float16, Q.device)
     Zq = _empty((B, D), torch.float32, Q.device)
+    qc = _empty((B,), torch.float32, Q.device)
     _check(lib().fvs_dense_small(_dev(Q, torch.float32, "Q"), B, d, _dev(W1T, torch.float32, "W1T"), R,
                                  _dev(Qr, torch.float32, "Qr"), _dev(M16, torch.float16, "M16"), NC,
                                  _dev(QM, torch.float16, "QM"), _dev(VPT, torch.float32, "VPT"), D,
-                                 _dev(Zq, torch.float32, "Zq"), _stream()), "fvs_dense_small")
-    return Qr, QM, Zq
+                                 _dev(Zq, torch.float32, "Zq"), _dev(c, torch.float32, "c", (d,)),
+                                 _dev(qc, torch.float32, "qc"), _stream()), "fvs_dense_small")
+    return Qr, QM, Zq, qc
 
 
 def query_prep(Q, Vr, c, z=None):

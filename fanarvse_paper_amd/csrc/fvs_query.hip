@@ -144,6 +144,8 @@ __global__ __launch_bounds__(256) void k_query_code(const float *__restrict__ z,
 //   rows [0, R):          Qr[b][j] = <Q[b], W1T[j]>            (f32)
 //   rows [R, R + NC):     QM[b][c] = fp16(<fp16(Q[b]), M16[c]>) (fp16 inputs, f32 sum, one rounding)
 //   rows [R + NC, +D):    Zq[b][t] = <Q[b], VPT[t]>            (f32)
+//   row R + NC + D:       qc[b] = <Q[b], c>, the canonical double sum of k_query_code (lane l takes
+//                         k = l, l + 64, ..., then the same xor butterfly), so it is the same value
 // Each lane sums its 4-element slices of the row in k order for every query of the batch, then a fixed
 // xor butterfly reduces the lanes. The products are the BLAS ones of a large batch, computed where
 // three library launches would each cost more than the 24 MB they read.
@@ -153,10 +155,21 @@ __global__ __launch_bounds__(256) void k_dense_small(const float *__restrict__ Q
                                                      const float *__restrict__ W1T, int R, float *__restrict__ Qr,
                                                      const uint16_t *__restrict__ M16, int NC,
                                                      uint16_t *__restrict__ QM, const float *__restrict__ VPT, int D,
-                                                     float *__restrict__ Zq) {
+                                                     float *__restrict__ Zq, const float *__restrict__ c,
+                                                     float *__restrict__ qc) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + fvs_wave_id();
-  if (row >= R + NC + D) return;  // wave-uniform; no barrier below
+  if (row > R + NC + D) return;  // wave-uniform; no barrier below
+  if (row == R + NC + D) {
+    for (int b = 0; b < B; b++) {
+      double sd = 0.0;
+      for (int k = lane; k < d; k += 64) sd += (double)Q[(int64_t)b * d + k] * (double)c[k];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) sd += __shfl_xor(sd, o, FVS_WAVE);
+      if (lane == 0) qc[b] = (float)sd;
+    }
+    return;
+  }
   const int kind = row < R ? 0 : (row < R + NC ? 1 : 2);
   float acc[kDenseMaxB];
 #pragma unroll
@@ -213,13 +226,13 @@ __global__ __launch_bounds__(256) void k_dense_small(const float *__restrict__ Q
 
 extern "C" int fvs_dense_small(const float *Q, int64_t B, int32_t d, const float *W1T, int32_t R, float *Qr,
                                const uint16_t *M16, int32_t NC, uint16_t *QM, const float *VPT, int32_t D, float *Zq,
-                               void *stream) {
+                               const float *c, float *qc, void *stream) {
   if (B < 0 || B > kDenseMaxB || d <= 0 || d % 4 != 0 || R < 0 || NC < 0 || D < 0) return FVS_E_ARG;
-  if (B == 0 || R + NC + D == 0) return FVS_OK;
-  if (!Q || (R && (!W1T || !Qr)) || (NC && (!M16 || !QM)) || (D && (!VPT || !Zq))) return FVS_E_ARG;
-  const int64_t rows = (int64_t)R + NC + D;
+  if (B == 0) return FVS_OK;
+  if (!Q || !c || !qc || (R && (!W1T || !Qr)) || (NC && (!M16 || !QM)) || (D && (!VPT || !Zq))) return FVS_E_ARG;
+  const int64_t rows = (int64_t)R + NC + D + 1;
   hipLaunchKernelGGL(k_dense_small, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, Q, (int)B, d,
-                     W1T, R, Qr, M16, NC, QM, VPT, D, Zq);
+                     W1T, R, Qr, M16, NC, QM, VPT, D, Zq, c, qc);
   return fvs_launch_status();
 }
 

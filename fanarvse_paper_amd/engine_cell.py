@@ -85,8 +85,7 @@ class EngineS:
         """The dense products: Qr = Qb @ W1 (f32), QM = fp16(Qb) @ means16.T (fp16), Zq = Qb @ VP (f32);
         and qc = <Qb, c> (canonical double sum)."""
         if len(Qb) <= _lib.DENSE_MAX_B:  # one launch instead of three library products
-            Qr, QM, Zq = _lib.dense_small(Qb, self.W1T, self.means16, self.VPT)
-            _, _, QC, _, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)
+            Qr, QM, Zq, QC = _lib.dense_small(Qb, self.W1T, self.means16, self.VPT, self.s1["c"])
             return Qr, QC, QM, Zq
         Qr = (Qb @ self.W1).contiguous()
         _, _, QC, Qh, _ = _lib.query_prep(Qb, self.W1, self.s1["c"], Qr)

@@ -59,12 +59,14 @@ int fvs_pack_ids(const uint8_t *ok, const int32_t *I, int64_t B, int32_t k, int6
  * The default engine's three dense products for a batch of at most 8 queries, in one launch. Replaces the
  * library products Qb @ s1["W1"] and Qb.half() @ s1["means16"].T of src/engine_cell.py:76,79 and the
  * stage-2 query rotation Qb @ VP of src/tiered_fused.py:57 at small batch: Qr f32 [B, R] = Q @ W1T^T, QM fp16 [B, NC] = fp16(fp16(Q) @ M16^T) (f32
- * sums), Zq f32 [B, D] = Q @ VPT^T. W1T f32 [R, d], M16 fp16 [NC, d] and VPT f32 [D, d] are row-major (the
- * transposes of W1 and VP, made once). Each output is one wave's dot: per lane, 4-element slices in k
- * order, then the xor butterfly 32..1. d must be a multiple of 4.
+ * sums), Zq f32 [B, D] = Q @ VPT^T, and qc f32 [B] = <Q, c> exactly as fvs_query_prep computes it (the
+ * reference's QC = Qb @ s1["c"], src/engine_cell.py:76). W1T f32 [R, d], M16 fp16 [NC, d] and VPT f32 [D, d]
+ * are row-major (the transposes of W1 and VP, made once). Each product output is one wave's dot: per
+ * lane, 4-element slices in k order, then the xor butterfly 32..1. d must be a multiple of 4.
  */
 int fvs_dense_small(const float *Q, int64_t B, int32_t d, const float *W1T, int32_t R, float *Qr, const uint16_t *M16,
-                    int32_t NC, uint16_t *QM, const float *VPT, int32_t D, float *Zq, void *stream);
+                    int32_t NC, uint16_t *QM, const float *VPT, int32_t D, float *Zq, const float *c, float *qc,
+                    void *stream);
 
 /*
  * Query code (a6) plus the global-centre term and the fp16 copy of the queries.

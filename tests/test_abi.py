@@ -50,8 +50,8 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_route_topk(n, 4, 100, 0, n, n) == E_ARG
     assert L.fvs_pack_ids(n, n, 4, 0, n, n) == E_ARG                                  # k = 0
     assert L.fvs_pack_ids(n, n, 0, 10, n, n) == 0                                     # empty batch
-    assert L.fvs_dense_small(n, 9, 1536, n, 256, n, n, 4096, n, n, 1536, n, n) == E_ARG  # B > 8
-    assert L.fvs_dense_small(n, 1, 1538, n, 256, n, n, 4096, n, n, 1536, n, n) == E_ARG  # d % 4
+    assert L.fvs_dense_small(n, 9, 1536, n, 256, n, n, 4096, n, n, 1536, n, n, n, n) == E_ARG  # B > 8
+    assert L.fvs_dense_small(n, 1, 1538, n, 256, n, n, 4096, n, n, 1536, n, n, n, n) == E_ARG  # d % 4
     assert L.fvs_route_topk(n, 4, 100, 101, n, n) == E_ARG                             # nprobe > NC
     assert L.fvs_i8_scan(0, 10, *[n] * 12, 100, 128, *[n] * 6, 1, 1, 1, n) == E_SHAPE  # R != 256
     assert L.fvs_i8_scan(2, 10, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == E_ARG    # bad mode

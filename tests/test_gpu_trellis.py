@@ -239,8 +239,10 @@ def test_dense_small_products_accuracy(env, B):
     ulp of the value (one rounding of the output); the fp16 query copy is rounded as the kernel does."""
     E = env["E"]
     Q = env["Q"][:B].contiguous()
-    Qr, QM, Zq = _lib.dense_small(Q, E.W1T, E.means16, E.VPT)
+    Qr, QM, Zq, qc = _lib.dense_small(Q, E.W1T, E.means16, E.VPT, E.s1["c"])
+    qc_ref = _lib.query_prep(Q, E.W1, E.s1["c"], Qr)[2]
     torch.cuda.synchronize()
+    assert torch.equal(qc.view(torch.int32), qc_ref.view(torch.int32))  # the same canonical double sum
     q = Q.double().cpu()
     d = q.shape[1]
     bound = lambda a, x: 4 * d * 2.0 ** -24 * (a.abs() @ x.abs())
