@@ -164,8 +164,8 @@ def test_emit_region_overflow(coarse, oracle_mod):
 
 
 def test_index_build_is_deterministic():
-    """Two builds of the same rows give identical tables (cell sums are segment reductions, not float
-    atomics), so bench runs and saved indexes are reproducible."""
+    """Two builds of the same rows in one process give identical tables: the cell sums are segment
+    reductions, not float atomics that add in a different order on each call."""
     print("\n[gpu edges] index build twice", flush=True)
     X = datagen.gen(40000, 768, 32, 0.7, seed=15, device="cuda")
     a = index.build_index(X, nlist=128)
