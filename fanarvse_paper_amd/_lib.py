@@ -33,7 +33,7 @@ SIGNATURES = {
     "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
-    "fvs_threshold": [P, P, I32, P, I64, I32, I32, I32, P, P, P],
+    "fvs_threshold": [P, P, I32, P, I32, I64, I32, I32, I32, P, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
@@ -41,7 +41,8 @@ SIGNATURES = {
     "fvs_classify": [P, P, P, P, I64, I32, F32, I32, P, P, P, P, P],
     "fvs_refine_rows": [P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "fvs_trellis_encode": [P, P, I64, I32, P, I32, P, I32, P, P, P],
-    "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, I32, I32, P, P, P, P, P, P, I32, I32, I32, P],
+    "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, I32, I32, I32, P, P, P, P, P, P, I32, I32, I32,
+                    P],
     "fvs_route_topk_scaled": [P, P, P, I64, I32, I32, P, P],
     "fvs_tiered_score": [P, P, P, I32, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
 }
@@ -62,7 +63,7 @@ def lib():
             fn.argtypes = args
             fn.restype = {"fvs_error_string": ctypes.c_char_p, "fvs_pairs_scratch_bytes": ctypes.c_int64}.get(
                 name, ctypes.c_int)
-        if L.fvs_abi_version() != 1:
+        if L.fvs_abi_version() != 2:
             raise RuntimeError("libfvs.so ABI version mismatch")
         _lib = L
     return _lib
@@ -269,8 +270,10 @@ def threshold(bm, probe, off, n1, MB, r, cnt=None):
     """t0 [B] from the first-pass block maxima; with cnt, also zeroes the emit pass's counters."""
     B, npr = probe.shape
     t0 = _empty((B,), torch.float32, probe.device)
+    if off.dim() != 1 or off.numel() < 2:
+        raise ValueError("threshold: off must hold NC + 1 cell offsets")
     _check(lib().fvs_threshold(_dev(bm, torch.float32, "bm"), _dev(probe, torch.int32, "probe"), npr,
-                               _dev(off, torch.int32, "off"), B, n1, MB, r, _dev(t0, torch.float32, "t0"),
+                               _dev(off, torch.int32, "off"), off.numel() - 1, B, n1, MB, r, _dev(t0, torch.float32, "t0"),
                                _opt(cnt, torch.int32, "cnt", (B,)), _stream()), "fvs_threshold")
     return t0
 
@@ -402,10 +405,11 @@ def trellis_encode(Zs, nz, tab, L, words, scale1, paths=None):
 
 
 def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1,
-            MB=1, n1=1, row0=0):
+            MB=1, n1=1, row0=0, half=False):
     """Trellis stage-1 first pass (mode 0) or emit (mode 1) over the static (cell, block) items
     (src/s1cell.py:121-154 semantics with the canonical fp32 dot of include/fvs.h). words/scale1 hold index
-    rows row0 .. (device or pinned host memory)."""
+    rows row0 .. (device or pinned host memory). half: both dot operands rounded to fp16 first (the
+    reference's tensor-core operands for batches above 8 queries)."""
     pcell, pblk, ps, pe = blocks
     qid, qrank, coff, ccnt, qcp = pr
     P_ = pcell.shape[0]
@@ -421,7 +425,7 @@ def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval
                              _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"), _dev(pe, i32, "pe"),
                              _dev(words, i32, "words", host_ok=True), row0, W,
                              _dev(scale1, torch.float16, "scale1", (N,), host_ok=True), _dev(tab, f32, "tab", (2 ** L,)), L, R,
-                             _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"),
+                             int(bool(half)), _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"),
                              _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1, _stream()), "fvs_tr_scan")
 
 

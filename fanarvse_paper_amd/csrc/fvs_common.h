@@ -22,6 +22,9 @@ __device__ __forceinline__ float fvs_h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t fvs_f2h(float f) {  // round to nearest even
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+__device__ __forceinline__ float fvs_round_h(float f) {  // f rounded to the nearest fp16 value (ties to even)
+  return (float)(_Float16)f;
+}
 
 // Order-preserving maps to unsigned keys (larger float -> larger key); -0 is mapped like +0.
 __device__ __forceinline__ uint32_t fvs_ord32(float x) {

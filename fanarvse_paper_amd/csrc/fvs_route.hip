@@ -792,6 +792,7 @@ __global__ __launch_bounds__(1024) void k_pairs_small(const int32_t *__restrict_
   for (int i = t; i < B * n; i += 1024) {
     const int q = i / n, r = i - q * n;
     const int c = probe[(int64_t)q * npr + r];
+    if ((unsigned)c >= (unsigned)NC) continue;  // a probe id outside [0, NC) names no cell: no pair
     if (r < (int)la.n) atomicOr(&qm[0][c], 1ull << q);
     if (two && r < (int)lb.n) atomicOr(&qm[1][c], 1ull << q);
   }
@@ -821,6 +822,7 @@ __global__ __launch_bounds__(1024) void k_pairs_small(const int32_t *__restrict_
   for (int i = t; i < B * n; i += 1024) {
     const int q = i / n, r = i - q * n;
     const int c = probe[(int64_t)q * npr + r];
+    if ((unsigned)c >= (unsigned)NC) continue;
     const uint64_t below = (1ull << q) - 1ull;  // q < 64
     float x = fvs_h2f(QM[(int64_t)q * NC + c]) * (mnorm ? mnorm[c] : 1.0f);
     if (qadd) x = x + qadd[q];

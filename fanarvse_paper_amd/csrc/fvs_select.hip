@@ -16,19 +16,25 @@ __device__ __forceinline__ int cell_blocks(const int32_t *off, int c) {
 constexpr int kSmallB = 64;
 
 // One block of NT threads per query. Valid values: bm[q][j][b], j < n1, b < blocks(probe[q][j]).
+// A probe id outside [0, NC) reads no offsets: its cell counts as empty, and the query's t0 becomes 1e30,
+// so its emit pass keeps nothing and its exactness flag (K <= cnt) is cleared.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
-                                                  int npr, const int32_t *__restrict__ off, int n1, int MB, int r,
-                                                  float *__restrict__ t0, int32_t *__restrict__ cnt) {
+                                                  int npr, const int32_t *__restrict__ off, int NC, int n1, int MB,
+                                                  int r, float *__restrict__ t0, int32_t *__restrict__ cnt) {
   __shared__ int nb[kMaxN1];
   __shared__ int hist[256];
   __shared__ int sh[fvs_sh_ints(NT)];
   const int64_t q = blockIdx.x;
-  int mine = 0;
+  int mine = 0, bad = 0;
   for (int j = threadIdx.x; j < n1; j += NT) {
-    nb[j] = cell_blocks(off, probe[q * npr + j]);
+    const int c = probe[q * npr + j];
+    const bool in = (unsigned)c < (unsigned)NC;
+    nb[j] = in ? cell_blocks(off, c) : 0;
+    bad |= in ? 0 : 1;
     mine += nb[j];
   }
+  const bool any_bad = __syncthreads_or(bad);
   // block sum of the valid counts
   const int tot = fvs_block_scan<NT>(mine, sh);
   if (threadIdx.x == NT - 1) sh[NT / 64 + 2] = tot;
@@ -41,7 +47,7 @@ __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, 
     const int j = i / MB, b = i - j * MB;
     return b < nb[j] ? fvs_ord32(row[i]) : 0u;
   };
-  const int kk = min(min(r, n), nv);
+  const int kk = any_bad ? 0 : min(min(r, n), nv);
   float out = 1e30f;
   if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t, NT>(key, n, kk, hist, sh));
   if (threadIdx.x == 0) {
@@ -137,19 +143,19 @@ __global__ __launch_bounds__(NT) void k_select(const float *__restrict__ bval, c
 
 }  // namespace
 
-extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
-                             int32_t n1, int32_t MB, int32_t r, float *t0, int32_t *cnt, void *stream) {
-  if (B < 0 || n1 <= 0 || n1 > npr || MB <= 0 || r <= 0) return FVS_E_ARG;
+extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int32_t NC,
+                             int64_t B, int32_t n1, int32_t MB, int32_t r, float *t0, int32_t *cnt, void *stream) {
+  if (B < 0 || NC <= 0 || n1 <= 0 || n1 > npr || MB <= 0 || r <= 0) return FVS_E_ARG;
   if (n1 > kMaxN1) return FVS_E_CAPACITY;
   if ((int64_t)n1 * MB > (int64_t)1 << 30) return FVS_E_ARG;
   if (B == 0) return FVS_OK;
   if (!bm || !probe || !off || !t0) return FVS_E_ARG;
   if (B <= kSmallB)
-    hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
-                       MB, r, t0, cnt);
+    hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, bm, probe, npr, off, NC,
+                       n1, MB, r, t0, cnt);
   else
-    hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, n1,
-                       MB, r, t0, cnt);
+    hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, NC,
+                       n1, MB, r, t0, cnt);
   return fvs_launch_status();
 }
 

@@ -133,6 +133,8 @@ __global__ __launch_bounds__(256) void k_trellis_encode(const float *__restrict_
 // coordinates [128 h, 128 h + 128) with h = l / 32, into registers; for each query of the cell it
 // forms the half dot product as a sequential fmaf chain and adds the two halves:
 //   est = fmaf(scale1, lo + hi, qcp),  lo / hi = sum over j < 128 / j >= 128 of tab[state_j] * Qr[j].
+// half != 0: both operands are first rounded to fp16 (the table once, each query element as it is staged),
+// as the reference's tensor-core dot takes them; their products are exact in fp32.
 // mode 0: bm[(q*n1 + qrank)*MB + blk - cs/32] = max over the block's rows in the cell.
 // mode 1: every (q, row) with est >= t0[q] is appended to the query's buffer (one atomic each).
 // words and scale1 hold rows row0 .. of the index (a staged chunk, or the whole index with row0 = 0).
@@ -144,14 +146,15 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
                                                  const int32_t *__restrict__ pe, int P, const uint32_t *__restrict__ words,
                                                  int64_t row0, int W, const uint16_t *__restrict__ scale1,
                                                  const float *__restrict__ tab,
-                                                 int L, const float *__restrict__ qcp, const float *__restrict__ t0,
+                                                 int L, int half, const float *__restrict__ qcp,
+                                                 const float *__restrict__ t0,
                                                  int32_t *__restrict__ cnt, float *__restrict__ bval,
                                                  int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
   __shared__ float stab[1 << kMaxL];
   __shared__ float4 qbuf[4][kTrR / 4];  // per wave: the query vector of the current step
   const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   const int S = 1 << L;
-  for (int i = tid; i < S; i += 256) stab[i] = tab[i];
+  for (int i = tid; i < S; i += 256) stab[i] = half ? fvs_round_h(tab[i]) : tab[i];
   __syncthreads();
   const int p = blockIdx.x * 4 + w;
   if (p >= P) return;
@@ -188,7 +191,8 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
     const int q = __builtin_amdgcn_readfirstlane(qid[pidx]);  // one query per wave and step
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the previous step's reads of qbuf are issued
     __builtin_amdgcn_wave_barrier();
-    qbuf[w][lane] = nxt;
+    qbuf[w][lane] = half ? make_float4(fvs_round_h(nxt.x), fvs_round_h(nxt.y), fvs_round_h(nxt.z), fvs_round_h(nxt.w))
+                         : nxt;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -343,10 +347,12 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
                            const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk,
                            const int32_t *ps, const int32_t *pe, const uint32_t *words, int64_t row0, int32_t W,
                            const uint16_t *scale1,
-                           const float *tab, int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt,
-                           float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream) {
+                           const float *tab, int32_t L, int32_t R, int32_t half, const float *qcp, const float *t0,
+                           int32_t *cnt, float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1,
+                           void *stream) {
   if (R != kTrR) return FVS_E_SHAPE;
   if (mode != 0 && mode != 1) return FVS_E_ARG;
+  if (half != 0 && half != 1) return FVS_E_ARG;
   if (L < 2 || L > kMaxL || W != (R + L - 1 + 31) / 32 || W > 10 || P < 0 || row0 < 0) return FVS_E_ARG;
   if (P == 0) return FVS_OK;
   if (!Qr || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !words || !scale1 || !tab || !qcp)
@@ -356,11 +362,11 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<0>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       row0, W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<1>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       row0, W, scale1, tab, L, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
   }
   return fvs_launch_status();
 }

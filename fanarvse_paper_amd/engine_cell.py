@@ -13,11 +13,16 @@ into pinned host memory, so a search is one replay and one stream synchronisatio
 
 Stage 1 is the static work-list scan (src/s1cell.py:176-195) for every batch size. The reference
 switches to per-(query, cell) programs for B <= 8 and to a dense probe mask for B <= 32
-(src/s1small_cell.py:29-88); those kernels select by the same threshold-and-emit rule but estimate
-with different dot-product arithmetic (fp32 sums vs fp16 tensor-core dots). Here a single kernel with
-one canonical fp32 dot order serves all batch sizes, so a query's results do not depend on the
-batch it arrives in. For ok queries, Lemma 2 (paper/main.tex:206-213) makes the candidate set
-independent of the threshold heuristic anyway.
+(src/s1small_cell.py:29-88); those kernels select by the same threshold-and-emit rule. Their operand
+precision is kept: above TINY = 8 queries the reference's tensor-core dots take fp16 operands
+(Qr.half() and the decoded table values .to(tl.float16), src/s1cell.py:127,131-132,
+src/s1small_cell.py:57-59), at most 8 queries keep fp32 operands (src/s1small_cell.py:17-20). One work-list
+kernel serves every size with one fp32 accumulation order; `half` selects the operand rounding. The
+fallback of `search` rounds to fp16 too (the reference redoes flagged queries with search_guess, whose
+queries are Qr.half(), src/engine3.py:45-48 via src/engine_cell.py:60-64); the lean path's fallback for a
+lone query keeps fp32 (src/engine_cell.py:165 runs search_small again). The dense products differ by
+batch size as well (fvs_dense_small up to 8 queries, library products above), so a query's estimates
+can change between a batch of 8 and a batch of 9.
 """
 import numpy as np
 import torch
@@ -29,6 +34,7 @@ from .enginei8 import _fresh, capture, padded_rows
 class EngineS:
     BN = 32
     M = None          # emit buffer size; None = index.emit_buffer(B, K)
+    TINY = 8          # batches up to TINY keep fp32 stage-1 operands (src/engine_cell.py:48)
 
     def __init__(self, s1, code, H=None):
         self.s1, self.code, self.H = s1, code, H
@@ -58,8 +64,9 @@ class EngineS:
         n1 = min(max(int(np.ceil(beta * K / (N / NC / self.BN + 1))), 1), nprobe)
         return M, n1, int(np.ceil(rho * K))
 
-    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None):
-        """Threshold-and-emit over the trellis codes (src/s1cell.py:176-195). Returns (pos, ok)."""
+    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None, half=True):
+        """Threshold-and-emit over the trellis codes (src/s1cell.py:176-195). Returns (pos, ok). half: fp16
+        dot operands (src/s1cell.py:127,131-132)."""
         s1 = self.s1
         NC = len(s1["off"]) - 1
         B = Qr.shape[0]
@@ -69,14 +76,15 @@ class EngineS:
         scratch = _lib.pairs_scratch(B, NC, dev)
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
-        _lib.tr_scan(0, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=self.MB, n1=n1)
+        _lib.tr_scan(0, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=self.MB, n1=n1,
+                     half=half)
         cnt = torch.empty((B,), dtype=torch.int32, device=dev)  # zeroed by the threshold kernel
         t0 = _lib.threshold(bm, probe, s1["off_t"], n1, self.MB, r, cnt)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
         pr = prn
         _lib.tr_scan(1, self.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, t0=t0, cnt=cnt, bval=bval,
-                     bpos=bpos, CAP=M)
+                     bpos=bpos, CAP=M, half=half)
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
         self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
         return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
@@ -103,7 +111,7 @@ class EngineS:
             raise RuntimeError("EngineS.H (fp16 vectors in id order) must be set before searching")
         Qr, QC, QM, Zq = self._dense(Qb)
         probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
-        pos, ok = self.stage1(Qr, QM, probe, K)
+        pos, ok = self.stage1(Qr, QM, probe, K, half=len(Qb) > self.TINY)
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq, probe)
 
@@ -142,10 +150,11 @@ class EngineS:
         if fkey not in self.graphs:
             sel = torch.zeros(nbp, dtype=torch.int64, device=qs.device)
             K, z, k = key[2], key[3], key[5]
+            half = not (key[0] == "host" and key[1] == 1)  # a lone lean-path query keeps fp32 operands
 
             def run():
                 a = [t.index_select(0, sel) for t in (qs,) + tuple(dense)]
-                return self._fallback(a[0], K, z, k, *a[1:])
+                return self._fallback(a[0], K, z, k, *a[1:], half=half)
 
             g, outs = self._capture(run)
             self.graphs[fkey] = (g, sel, outs)
@@ -200,10 +209,10 @@ class EngineS:
             out[bad] = self._fallback_rows(entry, bad)[0].cpu().numpy()
         return out
 
-    def _fallback(self, Qb, K, z, k, Qr, QC, QM, Zq, probe):
+    def _fallback(self, Qb, K, z, k, Qr, QC, QM, Zq, probe, half=True):
         """Flagged queries again with rho = 1, beta = 1.5 and M = 65,536 (the reference recomputes them with
         the work-list path and a larger buffer, src/engine_cell.py:98-101)."""
-        pos, _ = self.stage1(Qr, QM, probe, K, rho_override=1.0, M_override=65536)
+        pos, _ = self.stage1(Qr, QM, probe, K, rho_override=1.0, M_override=65536, half=half)
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return I, reads, ids, scores
 
@@ -212,7 +221,7 @@ class EngineS:
         Qb = Qb.float().contiguous()
         Qr, QC, QM, Zq = self._dense(Qb)
         probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
-        pos, ok = self.stage1(Qr, QM, probe, K)
+        pos, ok = self.stage1(Qr, QM, probe, K, half=len(Qb) > self.TINY)
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return dict(Qr=Qr, QC=QC, QM=QM, Zq=Zq, probe=probe, bm=self._bm, n1=self._n1, M=self._M, t0=self._t0,
                     cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, ok=ok, est=self._est, sd=self._sd,

@@ -120,7 +120,9 @@ class SpaceX(EngineS):
             self.copied_bytes += (r1 - r0) * (4 * self.Wd + 2)
             main.wait_event(ready)
             blocks = tuple(b[i0:i1] for b in self.blocks)
-            _lib.tr_scan(mode, blocks, Qr, pr, w, s, self.s1["tab"], self.s1["L"], row0=r0, **kw)
+            # fp16 operands at every batch size: the reference's host-resident engine always runs
+            # search_static (host_resident/space_x.py:15,42)
+            _lib.tr_scan(mode, blocks, Qr, pr, w, s, self.s1["tab"], self.s1["L"], row0=r0, half=True, **kw)
             ev = torch.cuda.Event()
             ev.record(main)
             done[slot] = ev

@@ -33,13 +33,13 @@ class EngineSTier(EngineS):
         Qb = Qb.float().contiguous()
         Qr, QC, QM, Zq = self._dense(Qb)
         probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
-        pos, ok = self.stage1(Qr, QM, probe, K)
+        pos, ok = self.stage1(Qr, QM, probe, K, half=len(Qb) > self.TINY)
         okh = ok.cpu().numpy()
         if not okh.all():  # flagged queries: stage 1 again with the fallback's settings (src/engine_cell.py:98-101)
             bad = torch.from_numpy(np.nonzero(~okh)[0]).to(Qb.device)
             self.nbad += len(bad)
             pos[bad], _ = self.stage1(Qr[bad].contiguous(), QM[bad].contiguous(), probe[bad].contiguous(), K,
-                                      rho_override=1.0, M_override=65536)
+                                      rho_override=1.0, M_override=65536, half=True)
         est, sd = _lib.tiered_score(pos, QC, Zq, self.code)
         ids, flag, namb, aslot = _lib.classify(est, sd, pos, self.s1["order"], z, k)
         aid = ids.gather(1, aslot.long())

@@ -44,23 +44,35 @@ class IndexFormatError(ValueError):
     """The file is not an index file of a version this build reads, or it is damaged."""
 
 
+def _put(arrays, path, a):
+    """Register an array under its path; two objects flattened to one path would overwrite each other."""
+    if path in arrays:
+        raise ValueError(f"{path}: two arrays map to the same key")
+    arrays[path] = a
+
+
 def _flatten(obj, arrays, path):
     if isinstance(obj, torch.Tensor):
         if obj.dtype not in _TORCH_TO_NP:
             raise TypeError(f"{path}: unsupported tensor dtype {obj.dtype}")
-        arrays[path] = obj.detach().to("cpu").contiguous().numpy()
+        _put(arrays, path, obj.detach().to("cpu").contiguous().numpy())
         return {"__array__": path, "torch": True, "gpu": obj.device.type == "cuda",
                 "pinned": obj.device.type == "cpu" and obj.is_pinned()}
     if isinstance(obj, np.ndarray):
         if obj.dtype.name not in _NP_NAMES:
             raise TypeError(f"{path}: unsupported array dtype {obj.dtype}")
-        arrays[path] = np.ascontiguousarray(obj)
+        _put(arrays, path, np.ascontiguousarray(obj))
         return {"__array__": path, "torch": False}
     if isinstance(obj, dict):
+        for k in obj:
+            if not (k is None or isinstance(k, (bool, int, float, str, np.integer, np.floating, np.bool_))):
+                raise TypeError(f"{path}: dict keys must be scalars, not {type(k).__name__}")
+            if isinstance(k, str) and "." in k:
+                raise ValueError(f"{path}: dict key {k!r} contains '.', the path separator")
         if all(isinstance(k, str) and not k.startswith("__") for k in obj):
             return {k: _flatten(v, arrays, f"{path}.{k}") for k, v in obj.items()}
         # other keys (the per-bit-width tables use int keys) as a list of [key, value] pairs
-        return {"__dict__": [[_flatten(k, {}, path), _flatten(v, arrays, f"{path}.{i}")]
+        return {"__dict__": [[_flatten(k, arrays, path), _flatten(v, arrays, f"{path}.{i}")]
                              for i, (k, v) in enumerate(obj.items())]}
     if isinstance(obj, (list, tuple)):
         items = [_flatten(v, arrays, f"{path}.{i}") for i, v in enumerate(obj)]

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FVS_ABI_VERSION 1
+#define FVS_ABI_VERSION 2
 
 #define FVS_OK 0
 #define FVS_E_ARG (-1)      /* an argument is out of its documented range            */
@@ -162,9 +162,11 @@ int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, cons
  *   bm f32 [B, n1, MB] written by fvs_i8_scan mode 0; probe i32 [B, npr]; off i32 [NC+1] cell offsets.
  *   Valid values of query q: bm[q][j][b] for j < n1 and b < blocks(cell probe[q][j]).
  *   t0[q] = the min(r, n1*MB, #valid)-th largest valid value, or 1e30 if none is valid.
+ *   A probe id outside [0, NC) among the first n1 reads no offsets and sets t0[q] = 1e30: the query then
+ *   emits nothing, and its exactness flag (K <= cnt) is cleared.
  *   cnt i32 [B] (may be NULL): set to 0, the emit pass's candidate counters (saves a fill launch).
  */
-int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int64_t B,
+int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr, const int32_t *off, int32_t NC, int64_t B,
                   int32_t n1, int32_t MB, int32_t r, float *t0, int32_t *cnt, void *stream);
 
 /*
@@ -274,13 +276,18 @@ int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, c
  *   state_j = bits j .. j+L-1 of the row's stream (MSB first), v_j = tab[state_j];
  *   est = fmaf((float)scale1, lo + hi, qcp), lo = sequential fmaf over j < R/2 of v_j * Qr[j] from +0,
  *   hi likewise over j >= R/2.
+ *   half = 1: v_j and Qr[j] are each rounded to fp16 (nearest, ties to even) before the products, the operand
+ *   precision of the reference's tensor-core dot in search_static / search_mask (src/s1cell.py:127,131-132,
+ *   147,151-152; src/s1small_cell.py:57-59); half = 0 keeps fp32 operands, as its small-batch kernels do
+ *   (src/s1small_cell.py:17-21,101). The products of fp16 operands are exact in fp32, so the accumulation
+ *   order above is the only rounding left.
  * R must be 256; 2 <= L <= 12.
  */
 int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
                 const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk, const int32_t *ps,
                 const int32_t *pe, const uint32_t *words, int64_t row0, int32_t W, const uint16_t *scale1, const float *tab,
-                int32_t L, int32_t R, const float *qcp, const float *t0, int32_t *cnt, float *bval, int32_t *bpos,
-                float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
+                int32_t L, int32_t R, int32_t half, const float *qcp, const float *t0, int32_t *cnt, float *bval,
+                int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
 
 /*
  * Routing on fp32 keys (a7 for the default engine). Replaces route() (src/engine_cell.py:40-42):

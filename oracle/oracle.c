@@ -270,18 +270,26 @@ void or_first_pass(const int8_t *q8, const float *qs, const int32_t *probe, int 
   first_pass_gen(est_i8_cb, &ctx, probe, npr, n1, off, QM, NC, mnorm, B, MB, bm);
 }
 
-void or_threshold(const float *bm, const int32_t *probe, int npr, const int32_t *off, int64_t B, int n1, int MB, int r,
-                  float *t0) {
+/* A probe id outside [0, NC) is no cell (this build's guard, not a reference rule): it reads no offsets and
+ * the query's t0 becomes 1e30, so its emit keeps nothing and its exactness flag is cleared. */
+void or_threshold(const float *bm, const int32_t *probe, int npr, const int32_t *off, int NC, int64_t B, int n1,
+                  int MB, int r, float *t0) {
 #pragma omp parallel for schedule(static)
   for (int64_t q = 0; q < B; q++) {
     uint32_t *v = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)n1 * MB);
-    int nv = 0;
+    int nv = 0, bad = 0;
     for (int j = 0; j < n1; j++) {
-      const int nb = cell_blocks(off, probe[q * npr + j]);
+      const int c = probe[q * npr + j];
+      if (c < 0 || c >= NC) {
+        bad = 1;
+        continue;
+      }
+      const int nb = cell_blocks(off, c);
       for (int b = 0; b < nb; b++) v[nv++] = ord32(bm[((int64_t)q * n1 + j) * MB + b]);
     }
     int kk = r < n1 * MB ? r : n1 * MB;
     if (kk > nv) kk = nv;
+    if (bad) kk = 0;
     if (kk == 0) {
       t0[q] = 1e30f;
     } else {
@@ -607,34 +615,41 @@ typedef struct {
   int W;
   const uint16_t *scale1;
   const float *tab;
-  int L, R;
+  int L, R, half;
 } tr_ctx;
 
-/* est = fmaf(scale1, lo + hi, qcp); lo and hi are sequential fmaf chains over the two halves. */
+/* est = fmaf(scale1, lo + hi, qcp); lo and hi are sequential fmaf chains over the two halves of
+ * tab[state_j] * Qr[j] (src/s1cell.py:147-152 with a fixed summation order). half: both operands are first
+ * rounded to fp16, as the reference's `.to(tl.float16)` before tl.dot does (src/s1cell.py:127,131-132);
+ * half = 0 keeps the fp32 operands of its small-batch kernels (src/s1small_cell.py:17-20). */
+static inline float tr_op(float x, int half) { return half ? h2f(f2h(x)) : x; }
+
 static float est_tr_cb(const void *ctx, int64_t q, int64_t r, float qcp) {
   const tr_ctx *c = (const tr_ctx *)ctx;
   const float *qv = c->Qr + q * c->R;
   const uint32_t *w = c->words + r * c->W;
   float lo = 0.f, hi = 0.f;
   const int H = c->R / 2;
-  for (int j = 0; j < H; j++) lo = fmaf(c->tab[tr_window(w, c->W, j, c->L)], qv[j], lo);
-  for (int j = H; j < c->R; j++) hi = fmaf(c->tab[tr_window(w, c->W, j, c->L)], qv[j], hi);
+  for (int j = 0; j < H; j++)
+    lo = fmaf(tr_op(c->tab[tr_window(w, c->W, j, c->L)], c->half), tr_op(qv[j], c->half), lo);
+  for (int j = H; j < c->R; j++)
+    hi = fmaf(tr_op(c->tab[tr_window(w, c->W, j, c->L)], c->half), tr_op(qv[j], c->half), hi);
   return fmaf(h2f(c->scale1[r]), lo + hi, qcp);
 }
 
 void or_tr_first_pass(const float *Qr, const int32_t *probe, int npr, int n1, const int32_t *off,
-                      const uint32_t *words, int W, const uint16_t *scale1, const float *tab, int L, int R,
+                      const uint32_t *words, int W, const uint16_t *scale1, const float *tab, int L, int R, int half,
                       const uint16_t *QM, int NC, const float *qadd, int64_t B, int MB, float *bm) {
-  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R, half};
   g_qadd = qadd;
   first_pass_gen(est_tr_cb, &ctx, probe, npr, n1, off, QM, NC, NULL, B, MB, bm);
   g_qadd = NULL;
 }
 
 void or_tr_emit(const float *Qr, const int32_t *probe, int npr, int np, const int32_t *off, const uint32_t *words,
-                int W, const uint16_t *scale1, const float *tab, int L, int R, const uint16_t *QM, int NC,
+                int W, const uint16_t *scale1, const float *tab, int L, int R, int half, const uint16_t *QM, int NC,
                 const float *qadd, const float *t0, int64_t B, int M, int32_t *cnt, float *bval, int32_t *bpos) {
-  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R};
+  const tr_ctx ctx = {Qr, words, W, scale1, tab, L, R, half};
   g_qadd = qadd;
   emit_gen(est_tr_cb, &ctx, probe, npr, np, off, QM, NC, NULL, t0, B, M, cnt, bval, bpos);
   g_qadd = NULL;

@@ -194,7 +194,8 @@ def threshold(bm, probe, off, n1, MB, r):
     off = _c(off, np.int32)
     B, npr = probe.shape
     t0 = np.empty(B, np.float32)
-    lib().or_threshold(_p(bm), _p(probe), I32(npr), _p(off), I64(B), I32(n1), I32(MB), I32(r), _p(t0))
+    lib().or_threshold(_p(bm), _p(probe), I32(npr), _p(off), I32(len(off) - 1), I64(B), I32(n1), I32(MB), I32(r),
+                       _p(t0))
     return t0
 
 
@@ -389,7 +390,7 @@ def route_topk_scaled(QM16, scale, nprobe, qadd=None):
     return probe
 
 
-def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB, qadd=None):
+def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB, qadd=None, half=False):
     Qr = _c(Qr, np.float32)
     probe = _c(probe, np.int32)
     off = _c(off, np.int32)
@@ -401,12 +402,12 @@ def tr_first_pass(Qr, probe, n1, off, words, scale1, tab, L, QM16, MB, qadd=None
     bm = np.full((B, n1, MB), -1e30, np.float32)
     qa = None if qadd is None else _c(qadd, np.float32)
     lib().or_tr_first_pass(_p(Qr), _p(probe), I32(npr), I32(n1), _p(off), _p(words), I32(words.shape[1]), _p(scale1),
-                           _p(tab), I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]),
+                           _p(tab), I32(L), I32(Qr.shape[1]), I32(int(bool(half))), _p(QM16), I32(QM16.shape[1]),
                            _p(qa) if qa is not None else None, I64(B), I32(MB), _p(bm))
     return bm
 
 
-def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M, qadd=None):
+def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M, qadd=None, half=False):
     Qr = _c(Qr, np.float32)
     probe = _c(probe, np.int32)
     off = _c(off, np.int32)
@@ -421,7 +422,8 @@ def tr_emit(Qr, probe, off, words, scale1, tab, L, QM16, t0, M, qadd=None):
     bpos = np.empty((B, M), np.int32)
     qa = None if qadd is None else _c(qadd, np.float32)
     lib().or_tr_emit(_p(Qr), _p(probe), I32(npr), I32(npr), _p(off), _p(words), I32(words.shape[1]), _p(scale1), _p(tab),
-                     I32(L), I32(Qr.shape[1]), _p(QM16), I32(QM16.shape[1]), _p(qa) if qa is not None else None, _p(t0),
+                     I32(L), I32(Qr.shape[1]), I32(int(bool(half))), _p(QM16), I32(QM16.shape[1]),
+                     _p(qa) if qa is not None else None, _p(t0),
                      I64(B), I32(M), _p(cnt), _p(bval), _p(bpos))
     return cnt, bval, bpos
 
@@ -467,29 +469,34 @@ def tr_params(K, nprobe, N, NC, M=None, rho_override=None, M_override=None, BN=3
     return M, n1, int(np.ceil(rho * K))
 
 
-def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=None, qadd=None):
+def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=None, qadd=None, half=False):
     N = idx["words"].shape[0]
     NC = len(idx["off"]) - 1
     M, n1, r = tr_params(K, probe.shape[1], N, NC, M, rho_override, M_override)
     MB = static_blocks(idx["off"])[4]
     bm = tr_first_pass(Qr, probe[:, :n1], n1, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, MB,
-                       qadd)
+                       qadd, half)
     t0 = threshold(bm, probe, idx["off"], n1, MB, r)
     cnt, bval, bpos = tr_emit(Qr, probe, idx["off"], idx["words"], idx["scale1"], idx["tab"], idx["L"], QM16, t0, M,
-                              qadd)
+                              qadd, half)
     pos, est1, ok, ncnt = select(bval, bpos, cnt, K, 0, None)
     return dict(n1=n1, r=r, M=M, MB=MB, bm=bm, t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos, est1=est1, ok=ok)
 
 
-def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, proj=False, order=True):
+def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, proj=False, order=True, half=None,
+                fb_half=True):
     """The default engine's batch (EngineS._gpu + the fallback): Qr = Q @ W1 (f32), QM16 = fp16(Q) @ means16.T
     (fp16), Zq = Q @ VP (f32) are the shared dense products. proj: QM16 = fp16(Qr) @ meansR.T and the pair term
-    and routing key add <q, c> (host_resident/space_x.py:33-39). order=False: ids are sorted positions."""
+    and routing key add <q, c> (host_resident/space_x.py:33-39). order=False: ids are sorted positions.
+    half: fp16 stage-1 operands (None: the reference's choice by batch size, fp16 above 8 queries,
+    src/engine_cell.py:48-53,82-83); fb_half: the same for the fallback pass."""
     Q = _c(Q, np.float32)
     _, _, qc, _ = query_prep(Q, None, idx["c"], Qr)
     qadd = qc if proj else None
     probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe, qadd)
-    s1 = tr_stage1(idx, Qr, QM16, probe, K, M, qadd=qadd)
+    if half is None:
+        half = len(Q) > 8
+    s1 = tr_stage1(idx, Qr, QM16, probe, K, M, qadd=qadd, half=half)
     est, sd = tiered_score(s1["pos"], qc, Zq, idx["rec"], idx["soff"], idx["TS"], idx["toff"], idx["cb"])
     ordr = idx["order"] if order else np.arange(len(idx["order"]), dtype=np.int32)
     H = idx["H"] if order else idx["Hs"]
@@ -500,7 +507,7 @@ def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, pr
     out["bad"] = bad
     if fallback and len(bad):
         f1 = tr_stage1(idx, np.asarray(Qr)[bad], np.asarray(QM16)[bad], probe[bad], K, M, rho_override=1.0,
-                       M_override=65536, qadd=None if qadd is None else qadd[bad])
+                       M_override=65536, qadd=None if qadd is None else qadd[bad], half=fb_half)
         estf, sdf = tiered_score(f1["pos"], qc[bad], np.asarray(Zq)[bad], idx["rec"], idx["soff"], idx["TS"],
                                  idx["toff"], idx["cb"])
         idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], ordr, H, Q[bad], z, k)

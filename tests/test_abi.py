@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(L):
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.fvs_abi_version() == 1
+    assert L.fvs_abi_version() == 2
     assert L.fvs_error_string(-1) and L.fvs_error_string(-3) and L.fvs_error_string(0)
 
 
@@ -57,7 +57,8 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_i8_scan(2, 10, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == E_ARG    # bad mode
     assert L.fvs_refine(*[n] * 6, 4, 10, 64, 1.0, 10, *[n] * 5) == E_ARG               # K <= k
     assert L.fvs_refine(*[n] * 6, 4, 20, 60, 1.0, 10, *[n] * 5) == E_ARG               # d % 8
-    assert L.fvs_threshold(n, n, 4, n, 4, 5, 2, 3, n, n, n) == E_ARG                   # n1 > npr
+    assert L.fvs_threshold(n, n, 4, n, 16, 4, 5, 2, 3, n, n, n) == E_ARG               # n1 > npr
+    assert L.fvs_threshold(n, n, 4, n, 0, 4, 2, 2, 3, n, n, n) == E_ARG                # NC = 0
     assert L.fvs_pairs_scratch_bytes(10, 7) > 0
     # zero-sized batches are valid no-ops
     assert L.fvs_select(n, n, n, 0, 16, 8, 0, 0.0, n, n, n, n, n) == 0

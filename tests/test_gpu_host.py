@@ -39,7 +39,7 @@ def test_streamed_engine_matches_oracle(env, oracle_mod, variant):
     torch.cuda.synchronize()
     Qr, QC, QM, Zq = E._dense(Q)
     out = oracle_mod.tr_pipeline(env["idx"], npy(Q), K, z, nprobe, k, Qr=npy(Qr), QM16=npy(QM).view(np.uint16),
-                                 Zq=npy(Zq), proj=E.proj, order=False)
+                                 Zq=npy(Zq), proj=E.proj, order=False, half=True)  # search_static: fp16 operands
     assert np.array_equal(npy(I), out["I"])
     assert np.array_equal(npy(reads), out["reads"])
     assert np.array_equal(npy(ids), out["cand"])

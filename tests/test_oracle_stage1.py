@@ -121,6 +121,26 @@ def test_threshold_rule_cases(oracle_mod):
     assert t0[1] != wrong
 
 
+def test_threshold_out_of_range_probe_ids(oracle_mod):
+    """A probe id outside [0, NC) (a stale or foreign list) reads no cell offsets: the query gets t0 = 1e30,
+    so it emits nothing and is flagged; the other queries keep their thresholds."""
+    off = np.array([0, 70, 70, 100], np.int32)
+    MB = 4
+    bm = np.full((4, 2, MB), -1e30, np.float32)
+    bm[:, 0, :3] = [0.5, 0.9, 0.1]
+    bm[:, 1, :2] = [0.7, 0.3]
+    good = np.array([[0, 2, 1]] * 4, np.int32)
+    t_good = oracle_mod.threshold(bm, good, off, 2, MB, 3)
+    bad = good.copy()
+    bad[1, 1] = 3          # == NC
+    bad[2, 0] = -1
+    bad[3, 2] = 1 << 20    # past n1: not read by the threshold
+    t_bad = oracle_mod.threshold(bm, bad, off, 2, MB, 3)
+    assert t_bad[0] == t_good[0] == np.float32(0.5)
+    assert t_bad[1] == t_bad[2] == np.float32(1e30)
+    assert t_bad[3] == t_good[3]
+
+
 def test_emit_is_threshold_set_and_lemma2(tiny, s1run):
     """cnt = #{probed rows: est >= t0}; for ok queries the top K of the buffer equals the brute-force top K
     of all probed rows (Lemma 2)."""

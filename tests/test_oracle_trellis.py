@@ -151,6 +151,42 @@ def test_trellis_estimate_matches_float64(oracle_mod):
     assert cnt[0] >= 1 and np.all(bval[0, :cnt[0]] >= t0[0])
 
 
+def test_trellis_fp16_operands(oracle_mod):
+    """half=True rounds both operands of every product to fp16 (the reference's `.to(tl.float16)` before
+    tl.dot, src/s1cell.py:127,131-132): the estimates then match the float64 dot of the rounded operands to
+    fp32 accumulation error, and differ from the fp32-operand estimate by far more. Rounding only one of
+    the two operands (a planted mistake) fails the first check."""
+    rng = np.random.default_rng(19)
+    L, R = 10, 256
+    tab = (0.95 * trellis.make_table(L)).astype(np.float32)
+    N = 96
+    bits = rng.integers(0, 2, (N, R + L - 1))
+    words = trellis.paths_to_words(_stream_paths(bits, L), L)
+    scale1 = fp16_bits(rng.uniform(0.05, 0.2, N).astype(np.float32))
+    off = np.array([0, N], np.int32)
+    Qr = rng.standard_normal((2, R)).astype(np.float32)
+    QM = fp16_bits(np.zeros((2, 1), np.float32))
+    probe = np.zeros((2, 1), np.int32)
+    t0 = np.full(2, -1e30, np.float32)
+    v = tab[trellis.decode_states(words, R, L)]
+    s = scale1.view(np.float16).astype(np.float64)
+    r16 = lambda x: x.astype(np.float16).astype(np.float64)
+    want16 = (r16(v) @ r16(Qr).T).T * s[None]
+    want32 = (v.astype(np.float64) @ Qr.astype(np.float64).T).T * s[None]
+    one_side = (r16(v) @ Qr.astype(np.float64).T).T * s[None]
+    for half, want in ((True, want16), (False, want32)):
+        cnt, bval, bpos = oracle_mod.tr_emit(Qr, probe, off, words, scale1, tab, L, QM, t0, N, half=half)
+        assert np.all(cnt == N)
+        got = np.empty((2, N))
+        for q in range(2):
+            got[q, bpos[q]] = bval[q]
+        err = np.abs(got - want) / (1 + np.abs(want))
+        assert err.max() < 2e-6
+        if half:
+            assert (np.abs(want16 - want32) / (1 + np.abs(want32))).mean() > 20 * err.max()
+            assert (np.abs(got - one_side) / (1 + np.abs(one_side))).max() > 10 * err.max()
+
+
 def test_route_scaled_orders_by_fp32_key(oracle_mod):
     rng = np.random.default_rng(2)
     QM = fp16_bits(rng.standard_normal((4, 50)).astype(np.float32))

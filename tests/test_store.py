@@ -140,3 +140,22 @@ def test_unstorable_objects_are_rejected(tmp_path):
     tricky = {"__array__": 1, "__tuple__": [2]}      # keys that look like markers are stored as pairs
     store.save(p, x=tricky)
     same(tricky, store.load(p)["x"])
+
+
+def test_colliding_keys_are_rejected(tmp_path):
+    """Array keys are '.'-joined paths: a key containing '.', two objects on one path, or an array used as a
+    dict key (which would be dropped) are refused instead of silently overwriting or losing an array."""
+    p = str(tmp_path / "k.fvs")
+    t = torch.arange(4, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        store.save(p, x={"a.b": t})
+    with pytest.raises(ValueError):
+        store.save(p, **{"x.0": t, "x": [t]})
+    with pytest.raises(TypeError):
+        store.save(p, x={1: t, torch.tensor(3): t})
+    with pytest.raises(TypeError):
+        store.save(p, x={np.int64(1): t, (1, 2): t})
+    assert not os.path.exists(p)
+    ok = {1: t, "1": t + 1}                            # an int and a str key stay distinct (stored as pairs)
+    store.save(p, x=ok)
+    same(ok, store.load(p)["x"])
