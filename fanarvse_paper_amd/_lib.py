@@ -32,6 +32,7 @@ SIGNATURES = {
     "fvs_pairs_scratch_bytes": [I64, I32],
     "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
+    "fvs_i8_scan_civf8": [I32, I32] + [P] * 17 + [I32, I32, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_threshold": [P, P, I32, P, I32, I64, I32, I32, I32, P, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],

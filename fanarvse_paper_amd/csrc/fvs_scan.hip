@@ -336,7 +336,111 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
   }
 }
 
+// ------------------------------------------------------------------ the reference's one-block work items
+// civf8.launch semantics (throughput/civf8.py:89-91): one work item per (cell, global 32-row block) of
+// src/s1cell.py:161-168, block maxima indexed by pair. One wave per item, four items per workgroup; the
+// wave keeps the block's 32 code rows as the MFMA A operand (rows outside the cell clamped into it, their
+// row scale NaN) and streams the cell's queries through as B in tiles of 32 (lane: query column l % 32,
+// 16 rows of the block). No LDS and no barrier: the waves of a workgroup are independent.
+//   mode 0: bmc[pair * MB + blk - cs / 32] = max over the block's rows in the cell (fmaxf from -1e30).
+//   mode 1: a lane counts its query's passing rows, takes one atomic range of cnt[q] for them and writes
+//           them in row order; the buffer's order is as unspecified as the reference's.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_i8_civf8(
+    const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
+    const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
+    const int32_t *__restrict__ pblk, const int32_t *__restrict__ ps, const int32_t *__restrict__ pe, int P,
+    const int8_t *__restrict__ Z, const float *__restrict__ zs, const float *__restrict__ qcp,
+    const float *__restrict__ t0, int32_t *__restrict__ cnt, float *__restrict__ bval, int32_t *__restrict__ bpos,
+    float *__restrict__ bmc, int CAP, int MB) {
+  const int lane = threadIdx.x & 63, w = fvs_wave_id();
+  const int h = lane >> 5, li = lane & 31;
+  const int p = blockIdx.x * 4 + w;
+  if (p >= P) return;
+  const int c = pcell[p];
+  const int qn = ccnt[c];
+  if (qn == 0) return;
+  const int qoff = coff[c], blk = pblk[p], cs = ps[p], ce = pe[p];
+  const int r0 = blk * 32;
+  const int rr = min(max(r0 + li, cs), ce - 1);  // a row of the cell for every lane
+  v4i a[8];
+  const v4i *zp = reinterpret_cast<const v4i *>(Z + (int64_t)rr * kR + h * 16);
+#pragma unroll
+  for (int s = 0; s < 8; s++) a[s] = zp[2 * s];
+  float zr[16];  // the scales of this lane's 16 rows: NaN outside the cell (never passes, ignored by fmaxf)
+#pragma unroll
+  for (int v = 0; v < 16; v++) {
+    const int r = r0 + acc_row(v, h);
+    zr[v] = (r >= cs && r < ce) ? zs[r] : __builtin_nanf("");
+  }
+  for (int j0 = 0; j0 < qn; j0 += 32) {
+    const int j = j0 + li;
+    const bool jv = j < qn;
+    const int pidx = qoff + (jv ? j : qn - 1);
+    const int q = qid[pidx];
+    const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)q * kR + h * 16);
+    v4i b[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) b[s] = src[2 * s];
+    v16i acc = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], b[s], acc, 0, 0, 0);
+    const float qsv = qs[q], qc = qcp[pidx];
+    float ev[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) ev[v] = __builtin_fmaf((float)acc[v] * qsv, zr[v], qc);
+    if constexpr (MODE == 0) {
+      float mx = -1e30f;
+#pragma unroll
+      for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
+      if (h == 0 && jv) bmc[(int64_t)(qoff + j) * MB + (blk - cs / 32)] = mx;
+    } else {
+      const float th = jv ? t0[q] : __builtin_inff();
+      uint32_t bits = 0;
+#pragma unroll
+      for (int v = 0; v < 16; v++) bits |= (ev[v] >= th ? 1u : 0u) << v;
+      if (bits) {
+        int idx = atomicAdd(&cnt[q], __builtin_popcount(bits));
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          if ((bits >> v) & 1u) {
+            if (idx < CAP) {
+              bval[(int64_t)q * CAP + idx] = ev[v];
+              bpos[(int64_t)q * CAP + idx] = r0 + acc_row(v, h);
+            }
+            idx++;
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int fvs_i8_scan_civf8(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
+                                 const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk,
+                                 const int32_t *ps, const int32_t *pe, const int8_t *Z, const float *zs,
+                                 const float *qcp, const float *t0, int32_t *cnt, float *bval, int32_t *bpos,
+                                 float *bmc, int32_t CAP, int32_t MB, void *stream) {
+  if (mode != 0 && mode != 1) return FVS_E_ARG;
+  if (P < 0) return FVS_E_ARG;
+  if (P == 0) return FVS_OK;
+  if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
+  const dim3 grid((unsigned)((P + 3) / 4));
+  hipStream_t st = (hipStream_t)stream;
+  if (mode == 0) {
+    if (!bmc || MB <= 0) return FVS_E_ARG;
+    hipLaunchKernelGGL(k_i8_civf8<0>, grid, dim3(256), 0, st, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, P, Z, zs,
+                       qcp, t0, cnt, bval, bpos, bmc, CAP, MB);
+  } else {
+    if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
+    hipLaunchKernelGGL(k_i8_civf8<1>, grid, dim3(256), 0, st, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, P, Z, zs,
+                       qcp, t0, cnt, bval, bpos, bmc, CAP, MB);
+  }
+  return fvs_launch_status();
+}
 
 extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
                            const int32_t *qrank, const int32_t *coff, const int32_t *ccnt, const int32_t *pcell,

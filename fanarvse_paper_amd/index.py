@@ -47,6 +47,20 @@ def assign(X16, cen, chunk=100000):
     return torch.cat([(X16[j:j + chunk].float() @ cen.T).argmax(1) for j in range(0, X16.shape[0], chunk)])
 
 
+def cell_means(X16, order, cell, off, nlist, chunk=65536):
+    """fp32 means of each cell's members (src/engine_cell.py:12-15): the rows X16[order] are in cell order,
+    so each chunk's segment sums are added in chunk order (reproducible). X16 on the GPU or the host (rows
+    gathered there and copied to cell's device); empty cells get the zero vector."""
+    dev = cell.device
+    means = torch.zeros(nlist, X16.shape[1], device=dev)
+    oc = order.long().to(X16.device)
+    N = order.shape[0]
+    for j in range(0, N, chunk):
+        means += segment_sum(X16[oc[j:j + chunk]].to(dev).float(), cell[j:j + chunk].long(), nlist)
+    cnt = (off[1:] - off[:-1]).clamp(min=1).float().to(dev)
+    return means / cnt[:, None]
+
+
 def build_stage1_cells(X16, nlist=4096, seed=0):
     """Stage-1 tables: c, order (sorted position -> id, int32), off (numpy int64 [NC+1]), off_t (int32
     tensor), cell (cell of each sorted position), means16 (fp16 cell means), inv_mnorm."""
@@ -58,11 +72,7 @@ def build_stage1_cells(X16, nlist=4096, seed=0):
     order = torch.argsort(A, stable=True)
     off = torch.searchsorted(A[order].contiguous(), torch.arange(nlist + 1, device=dev))
     cell = A[order]
-    means = torch.zeros(nlist, X16.shape[1], device=dev)
-    for j in range(0, N, 65536):  # rows are in cell order: per chunk, segment sums added in chunk order
-        means += segment_sum(X16[order[j:j + 65536]].float(), cell[j:j + 65536], nlist)
-    cnt = (off[1:] - off[:-1]).clamp(min=1).float()
-    means /= cnt[:, None]
+    means = cell_means(X16, order, cell, off, nlist)
     means16 = means.half().contiguous()
     inv_mnorm = (1.0 / means16.float().norm(dim=1).clamp(min=1e-12)).contiguous()
     return dict(c=c.contiguous(), order=order.to(torch.int32).contiguous(), off=off.cpu().numpy().astype(np.int64),
@@ -81,9 +91,41 @@ def pca_int8_basis(X16, R=256, nmean=200000, step=10):
     return torch.from_numpy(V).float().to(X16.device).contiguous()
 
 
-def build_codes(s1, X16, Vr):
-    """int8 codes of the cell residuals in sorted order and their scales (throughput/enginei8.py:19-27)."""
-    return _lib.build_codes(X16, s1["order"], s1["cell"], s1["means16"], Vr.contiguous())
+def sorted_cells(s1):
+    """Cell of each sorted position (int32 tensor): s1["cell"], or searchsorted over the offsets as the
+    reference derives it (throughput/enginei8.py:21)."""
+    if s1.get("cell") is not None:
+        return s1["cell"].to(torch.int32).contiguous()
+    off = torch.as_tensor(np.asarray(s1["off"]) if "off" in s1 else s1["off_t"].cpu(), dtype=torch.int64)
+    dev = s1["means16"].device
+    N = int(off[-1])
+    off = off.to(dev)
+    return (torch.searchsorted(off, torch.arange(N, device=dev), right=True) - 1).to(torch.int32).contiguous()
+
+
+def build_codes(s1, X16, V, R=256, chunk=65536):
+    """(Z, zs, Vr): int8 codes of the cell residuals in sorted order, their scales and Vr = V[:, :R]; the
+    reference's build_codes(s1, X16, V, R) (throughput/enginei8.py:19-27), on the GPU (fvs_build_codes).
+    X16 fp16 [n_ids, d] in id order, on the GPU or in host memory (then gathered and copied chunk by chunk,
+    as the reference does); s1 needs order, means16 and the cell offsets."""
+    dev = s1["means16"].device
+    Vr = V[:, :R].to(device=dev, dtype=torch.float32).contiguous()
+    order = s1["order"].to(device=dev, dtype=torch.int32).contiguous()
+    cell = sorted_cells(s1)
+    means16 = s1["means16"].contiguous()
+    if X16.is_cuda:
+        Z, zs = _lib.build_codes(X16, order, cell, means16, Vr)
+        return Z, zs, Vr
+    N = order.shape[0]
+    Z = torch.empty((N, R), dtype=torch.int8, device=dev)
+    zs = torch.empty((N,), dtype=torch.float32, device=dev)
+    oc = order.long().cpu()
+    for j in range(0, N, chunk):
+        xs = X16[oc[j:j + chunk]].to(dev).contiguous()
+        n = xs.shape[0]
+        ident = torch.arange(n, dtype=torch.int32, device=dev)
+        Z[j:j + n], zs[j:j + n] = _lib.build_codes(xs, ident, cell[j:j + n].contiguous(), means16, Vr)
+    return Z, zs, Vr
 
 
 def emit_buffer(B, K, budget=1 << 29):
@@ -148,10 +190,10 @@ def build_index(X16, nlist=4096, R=256, bits_per_dim=2.5, seed=0, with_codes=Tru
     s1 = build_stage1_cells(X16, nlist, seed)
     lam, V = s2lut.pca_basis(X16, s1["c"])
     TS = s2lut.allocate(lam, int(bits_per_dim * X16.shape[1]))
-    code = s2lut.encode_uniform(X16, s1["order"], s1["c"], V, TS, seed)
+    code = s2lut.encode_uniform_tiers(X16, s1["order"], s1["c"], V, TS, seed)
     s2lut.prepare_u(code)
     Vr = pca_int8_basis(X16, R)
     Z = zs = None
     if with_codes:
-        Z, zs = build_codes(s1, X16, Vr)
+        Z, zs, Vr = build_codes(s1, X16, Vr, R)
     return s1, code, Z, zs, Vr

@@ -159,7 +159,18 @@ def lloyd_cb(b):
     return y, (y[1:] + y[:-1]) / 2
 
 
-def encode_uniform(X16, order, c, V, TS, seed=0, chunk=16384):
+def encode_uniform(code, host16, order, c, seed=0):
+    """The reference's encode_uniform(code, host16, order, c, seed) (throughput/s2lut.py:18-29): the tiered
+    refinement of `code` (its tiers TS and PCA basis V) re-encoded with uniform codebooks. Returns a new
+    code dict: `code`'s entries plus the uniform tables (records, deltas, rotations)."""
+    out = dict(code)
+    out.pop("VP", None)
+    out.pop("VP16", None)
+    out.update(encode_uniform_tiers(host16, order, c, code["V"], code["TS"], seed))
+    return out
+
+
+def encode_uniform_tiers(X16, order, c, V, TS, seed=0, chunk=16384):
     """Uniform-codebook tiered code of x - c for the vectors in sorted order (throughput/s2lut.py:18-29
     with src/tiered.py:155-170), written straight into packed records.
     Returns the code dict: TS, V, rots, deltas, cb_uniform, rec [N, RB] uint8, RB, soff, toff, bytes."""
@@ -174,7 +185,9 @@ def encode_lloyd(X16, order, c, V, TS, seed=0, chunk=16384):
 
 
 def encode_tiered(X16, order, c, V, TS, seed=0, chunk=16384, kind="uniform"):
-    dev = X16.device
+    """Tier records of the vectors X16[order] (X16 on the GPU, or in host memory: rows are gathered on the
+    host and the encode runs on V's device)."""
+    dev = V.device
     N = len(order)
     rots = tier_rotations(TS, seed)
     deltas, cbs, levels = {}, {}, {}
@@ -189,10 +202,11 @@ def encode_tiered(X16, order, c, V, TS, seed=0, chunk=16384, kind="uniform"):
     toff, soff, RB = record_layout(TS)
     rec = torch.zeros((N, RB), dtype=torch.uint8, device=dev)
     ss = torch.empty((N, len(TS), 2), dtype=torch.float16, device=dev)
-    oc = order.long().to(dev)
+    oc = order.long().to(X16.device)
     Pt = [P.to(dev) for P in rots]
+    c = c.to(dev)
     for j in range(0, N, chunk):
-        Zc = (X16[oc[j:j + chunk]].float() - c) @ V
+        Zc = (X16[oc[j:j + chunk]].to(dev).float() - c) @ V
         n = len(Zc)
         for t, ((s, e, bb), P) in enumerate(zip(TS, Pt)):
             F = Zc[:, s:e] @ P

@@ -94,21 +94,59 @@ def rotation_basis(X16, c, R=R_DEFAULT, seed=0, n=50000):
     return torch.from_numpy((V @ q).astype(np.float32)).to(X16.device)
 
 
-def encode_cells(X16, s1, W1, tab, L=L_DEFAULT, chunk=16384):
-    """Trellis codes of the cell residuals x - means16[cell] in sorted order (src/engine_cell.py:8-24):
-    Z = (x - m) @ W1, nz = |Z|, Zs = Z / nz * sqrt(R), words and scale1 from the GPU encoder."""
-    order, cell = s1["order"].long(), s1["cell"].long()
-    means = s1["means16"].float()
+def encode_cells(X16, s1, W1, tab, L=L_DEFAULT, chunk=16384, means=None):
+    """Trellis codes of the cell residuals x - means[cell] in sorted order (src/engine_cell.py:8-24):
+    Z = (x - m) @ W1, nz = |Z|, Zs = Z / nz * sqrt(R), words and scale1 from the GPU encoder. means: the fp32
+    cell means (default: s1["means16"]); X16 on the GPU or the host (rows gathered there)."""
+    dev = W1.device
+    order = s1["order"].long().to(X16.device)
+    cell = index.sorted_cells(s1).long().to(dev)
+    means = s1["means16"].float() if means is None else means
     N = len(order)
     R = W1.shape[1]
-    words = torch.empty((N, n_words(R, L)), dtype=torch.int32, device=X16.device)
-    scale1 = torch.empty((N,), dtype=torch.float16, device=X16.device)
+    words = torch.empty((N, n_words(R, L)), dtype=torch.int32, device=dev)
+    scale1 = torch.empty((N,), dtype=torch.float16, device=dev)
     for j in range(0, N, chunk):
-        Z = (X16[order[j:j + chunk]].float() - means[cell[j:j + chunk]]) @ W1
+        Z = (X16[order[j:j + chunk]].to(dev).float() - means[cell[j:j + chunk]]) @ W1
         nz = Z.norm(dim=1).clamp(min=1e-6)
         Zs = (Z / nz[:, None] * R ** 0.5).contiguous()
         words[j:j + len(Z)], scale1[j:j + len(Z)] = encode(Zs, nz.contiguous(), tab, L)
     return words, scale1
+
+
+def cellify(s1, host16, L=L_DEFAULT):
+    """The reference's cellify(s1) (src/engine_cell.py:8-24): the stage-1 trellis codes of an index already
+    routed to its final cells, re-encoded against the cell means. s1 needs order, off, W1 and tab; the
+    reference reads the base vectors and L from its `rf` module, here they are arguments (host16 fp16
+    [N, d] in id order, on the GPU or the host). Returns dict(s1) with words and scale1 (codes of
+    x - mean(cell), fp32 means), means16 (the fp16 means) and cell."""
+    out = dict(s1)
+    W1, tab = s1["W1"], s1["tab"]
+    dev = W1.device
+    off = torch.as_tensor(np.asarray(s1["off"]), dtype=torch.int64, device=dev)
+    NC = len(off) - 1
+    N = int(off[-1])
+    cell = (torch.searchsorted(off, torch.arange(N, device=dev), right=True) - 1).to(torch.int32).contiguous()
+    means = index.cell_means(host16, s1["order"], cell, off, NC)
+    out["cell"] = cell
+    out["words"], out["scale1"] = encode_cells(host16, out, W1, tab, L, means=means)
+    out["means16"] = means.half().contiguous()
+    out["L"] = L
+    return out
+
+
+def compact(s1c):
+    """The reference's compact(s1c) (src/engine_cell.py:26-32): one fp16 table of cell means serves routing
+    (key q.mean / |mean|) and the stage-1 pair term; inv_mnorm = 1 / |means16| (>= 1e-12), int32 ids,
+    cen = inv_mnorm. Also the int32 offsets off_t the kernels read."""
+    out = dict(s1c)
+    nrm = out["means16"].float().norm(dim=1).clamp(min=1e-12)
+    out["inv_mnorm"] = (1.0 / nrm).contiguous()
+    out["order"] = out["order"].to(torch.int32).contiguous()
+    out["cen"] = out["inv_mnorm"]
+    out["off"] = np.asarray(out["off"]).astype(np.int64)
+    out["off_t"] = torch.as_tensor(out["off"], dtype=torch.int32, device=nrm.device).contiguous()
+    return out
 
 
 def build_index(X16, nlist=4096, R=R_DEFAULT, L=L_DEFAULT, bits_per_dim=2.5, seed=0):
@@ -123,9 +161,9 @@ def build_index(X16, nlist=4096, R=R_DEFAULT, L=L_DEFAULT, bits_per_dim=2.5, see
     T = make_table(L)
     alpha = choose_alpha(T, L, R, device=X16.device)
     tab = (alpha * torch.from_numpy(T)).to(X16.device).contiguous()
-    words, scale1 = encode_cells(X16, s1, W1, tab, L)
+    s1.update(W1=W1, tab=tab, alpha=alpha, L=L)
+    s1 = compact(cellify(s1, X16, L))
     lam, V = s2lut.pca_basis(X16, c)
     TS = s2lut.allocate(lam, int(bits_per_dim * X16.shape[1]))
     code = s2lut.encode_lloyd(X16, s1["order"], c, V, TS, seed=seed)
-    s1.update(W1=W1, tab=tab, alpha=alpha, L=L, words=words, scale1=scale1)
     return s1, code

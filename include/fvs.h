@@ -131,11 +131,34 @@ int fvs_pairs2(const int32_t *probe, int64_t B, int32_t npr, int32_t n1, int32_t
                int32_t *qid, int32_t *qrank, float *qcp, void *stream);
 
 /*
- * int8 stage-1 scan on MFMA (a9, a11). Same inputs and outputs as the reference's CUDA twin
- * civf8.launch(mode, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, t0, cnt, bval,
- * bpos, bmc, CAP, MB) (throughput/civf8.py:89-91), which the Triton pair _first8c/_emit8c
- * (throughput/ivf8c_kern.py:2-36) also implements; plus qrank/n1 so that the first pass writes each
- * query's block maxima straight into its own row.
+ * The reference's operator seam for the int8 stage-1 scan (a9, a11), argument for argument:
+ * civf8.launch(mode, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, t0, cnt, bval, bpos, bmc,
+ * CAP, MB) (throughput/civf8.py:89-91, called by EngineI8.stage1_i8 at throughput/enginei8.py:49-52,58),
+ * which the Triton pair _first8c/_emit8c (throughput/ivf8c_kern.py:2-36) also implements.
+ *   P work items (pcell, pblk, ps, pe) = _static_blocks (src/s1cell.py:161-168): item p covers the rows
+ *   [32 pblk, 32 pblk + 32) of [ps, pe), the rows of cell pcell; Z i8 [N, 256], zs f32 [N] in the same row
+ *   order; (qid, coff, ccnt, qcp) = pairs_fast's lists (throughput/enginei8.py:11-16): the pairs of cell c
+ *   are qoff = coff[c] .. qoff + ccnt[c] - 1 with query qid[pair] and centre term qcp[pair].
+ *   For every pair of the item's cell: acc = sum_j q8[q][j] * Z[n][j] (int32), est = fmaf((float)acc * qs[q],
+ *   zs[n], qcp[pair]) for the rows n of the item.
+ *   mode 0: bmc[pair * MB + pblk - ps / 32] = max over the item's rows (fmaxf from -1e30); other entries are
+ *     left as they are (the caller pre-fills -1e30, as the reference does). t0, cnt, bval, bpos unused.
+ *   mode 1: every (q, n) with est >= t0[q] increments cnt[q]; the first CAP of a query are stored at
+ *     bval[q*CAP + idx], bpos[q*CAP + idx] = n (any order). cnt zeroed by the caller. bmc unused.
+ * R is 256, as the reference's kernel fixes it. One wave per item: a compatibility entry; the engine's own
+ * path (fvs_i8_scan below) groups a cell's blocks into items of eight, which the one-block list cannot
+ * express, and writes block maxima by query instead of by pair.
+ */
+int fvs_i8_scan_civf8(int32_t mode, int32_t P, const int8_t *q8, const float *qs, const int32_t *qid,
+                      const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk,
+                      const int32_t *ps, const int32_t *pe, const int8_t *Z, const float *zs, const float *qcp,
+                      const float *t0, int32_t *cnt, float *bval, int32_t *bpos, float *bmc, int32_t CAP, int32_t MB,
+                      void *stream);
+
+/*
+ * int8 stage-1 scan on MFMA (a9, a11), the engine's grouped form of fvs_i8_scan_civf8 (same estimates and
+ * emitted sets; throughput/civf8.py:89-91, throughput/ivf8c_kern.py:2-36), plus qrank/n1 so that the first
+ * pass writes each query's block maxima straight into its own row.
  *   One workgroup per item p < P: a cell and up to 256 consecutive rows of it (pcell, prow, ps, pe: the
  *   cell, the item's first row, and the cell's first and end row; the item covers rows
  *   [max(prow, ps), min(prow + 256, pe)) as eight 32-row blocks starting at prow). Mode 0: prow is a

@@ -63,6 +63,9 @@ def test_argument_checks_need_no_gpu(L):
     # zero-sized batches are valid no-ops
     assert L.fvs_select(n, n, n, 0, 16, 8, 0, 0.0, n, n, n, n, n) == 0
     assert L.fvs_i8_scan(1, 0, *[n] * 12, 100, 256, *[n] * 6, 1, 1, 1, n) == 0
+    assert L.fvs_i8_scan_civf8(2, 10, *[n] * 17, 1, 1, n) == E_ARG                    # bad mode
+    assert L.fvs_i8_scan_civf8(0, 10, *[n] * 17, 1, 1, n) == E_ARG                    # null buffers
+    assert L.fvs_i8_scan_civf8(1, 0, *[n] * 17, 1, 1, n) == 0                         # no items
 
 
 def test_wrappers_refuse_cpu_tensors(L):
@@ -73,6 +76,34 @@ def test_wrappers_refuse_cpu_tensors(L):
         _lib.route_topk(QM, 4)
     with pytest.raises((RuntimeError, ValueError, TypeError)):
         _lib.fill_u32(torch.zeros(8, dtype=torch.int32), 0)
+
+
+def test_civf8_seam_checks_before_launch(L):
+    """fanarvse_paper_amd.civf8.launch keeps the reference's argument list (throughput/civf8.py:89-91) and
+    refuses wrong shapes and host tensors before anything is launched."""
+    import inspect
+
+    from fanarvse_paper_amd import civf8
+
+    names = list(inspect.signature(civf8.launch).parameters)
+    assert names == ["mode", "P", "q8", "qs", "qid", "coff", "ccnt", "pcell", "pblk", "ps", "pe", "Z", "zs", "qcp",
+                     "t0", "cnt", "bval", "bpos", "bmc", "CAP", "MB"]
+    i32 = lambda n: torch.zeros(n, dtype=torch.int32)
+    f32 = lambda *s: torch.zeros(*s)
+    B, N, P = 4, 64, 2
+    args = dict(mode=0, P=P, q8=torch.zeros((B, 256), dtype=torch.int8), qs=f32(B), qid=i32(8), coff=i32(3),
+                ccnt=i32(3), pcell=i32(P), pblk=i32(P), ps=i32(P), pe=i32(P),
+                Z=torch.zeros((N, 256), dtype=torch.int8), zs=f32(N), qcp=f32(8), t0=f32(1), cnt=i32(1),
+                bval=f32(1), bpos=i32(1), bmc=f32(8, 3), CAP=1, MB=3)
+    with pytest.raises(ValueError):  # host tensors: no CPU fallback
+        civf8.launch(**args)
+    for k, v in (("Z", torch.zeros((N, 128), dtype=torch.int8)), ("bmc", f32(8, 2)), ("mode", 2), ("P", 3),
+                 ("zs", f32(N - 1)), ("qcp", f32(7))):
+        with pytest.raises(ValueError):
+            civf8.launch(**{**args, k: v})
+    with pytest.raises(ValueError):  # mode 1: emit buffers of B * CAP
+        civf8.launch(**{**args, "mode": 1, "t0": f32(B), "cnt": i32(B), "bval": f32(B, 5), "bpos": i32(B * 5),
+                        "CAP": 4})
 
 
 def test_no_packed_fp32_in_device_code():

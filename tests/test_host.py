@@ -153,3 +153,32 @@ def test_emit_buffer_rule():
     assert emit_buffer(2000, 200) == (1 << 29) // 16000
     assert emit_buffer(1 << 20, 400) == 6400            # never below the reference's size
     assert emit_buffer(2000, 5000) == 80000             # nor capped below it for large K
+
+
+def test_encode_uniform_reference_signature():
+    """s2lut.encode_uniform(code, host16, order, c, seed) re-encodes `code`'s tiers with uniform codebooks
+    (throughput/s2lut.py:18-29): the records equal those of the table-level encoder on the same inputs, the
+    other entries of `code` are kept, and `code` itself is not modified."""
+    X = datagen.gen(1200, 128, 8, 0.7, seed=3)
+    c = X[:500].float().mean(0)
+    lam, V = s2lut.pca_basis(X, c)
+    TS = s2lut.allocate(lam, int(2.5 * X.shape[1]))
+    order = torch.randperm(X.shape[0], generator=torch.Generator().manual_seed(0)).to(torch.int32)
+    lloyd = s2lut.encode_lloyd(X, order, c, V, TS, seed=0)
+    lloyd["extra"] = 7
+    keys = set(lloyd)
+    u = s2lut.encode_uniform(lloyd, X, order, c, seed=0)
+    want = s2lut.encode_uniform_tiers(X, order, c, V, TS, seed=0)
+    assert torch.equal(u["rec"], want["rec"]) and u["deltas"] == want["deltas"]
+    assert u["extra"] == 7 and u["kind"] == "uniform" and u["TS"] == TS
+    assert set(lloyd) == keys and lloyd["kind"] == "lloyd"
+
+
+def test_sorted_cells_from_offsets():
+    """build_codes derives each sorted position's cell from the offsets when s1 has no `cell` table, as
+    the reference does (throughput/enginei8.py:21)."""
+    off = np.array([0, 3, 3, 7, 10], np.int64)
+    s1 = dict(off=off, means16=torch.zeros(4, 8, dtype=torch.float16))
+    assert index.sorted_cells(s1).tolist() == [0, 0, 0, 2, 2, 2, 2, 3, 3, 3]
+    s1["cell"] = torch.arange(10)
+    assert index.sorted_cells(s1).tolist() == list(range(10))

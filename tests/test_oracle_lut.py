@@ -143,7 +143,7 @@ def test_encoder_records_decode_to_the_uniform_code():
     c = X.float().mean(0)
     lam, V = s2lut.pca_basis(X, c, n=512)
     order = torch.arange(512, dtype=torch.int32)
-    code = s2lut.encode_uniform(X, order, c, V, TS)
+    code = s2lut.encode_uniform_tiers(X, order, c, V, TS)
     rec = code["rec"].numpy()
     toff, soff = code["toff"], code["soff"]
     Zc = ((X.float() - c) @ V).numpy().astype(np.float64)

@@ -71,7 +71,7 @@ def test_stage2_code_round_trip(tmp_path):
     lam, V = s2lut.pca_basis(X, c)
     TS = s2lut.allocate(lam, int(2.5 * 64))
     order = torch.randperm(1500, generator=torch.Generator().manual_seed(2)).to(torch.int32)
-    codes = dict(lloyd=s2lut.encode_lloyd(X, order, c, V, TS, seed=0), uniform=s2lut.encode_uniform(X, order, c, V, TS))
+    codes = dict(lloyd=s2lut.encode_lloyd(X, order, c, V, TS, seed=0), uniform=s2lut.encode_uniform_tiers(X, order, c, V, TS))
     p = str(tmp_path / "c.fvs")
     store.save(p, **codes)
     same(codes, store.load(p))
