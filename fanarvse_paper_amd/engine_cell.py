@@ -35,6 +35,7 @@ class EngineS:
     BN = 32
     M = None          # emit buffer size; None = index.emit_buffer(B, K)
     TINY = 8          # batches up to TINY keep fp32 stage-1 operands (src/engine_cell.py:48)
+    SMALL_CAP = 8192  # their emit buffer in search(): search_small's CAP (src/s1small_cell.py:29)
 
     def __init__(self, s1, code, H=None):
         self.s1, self.code, self.H = s1, code, H
@@ -54,24 +55,29 @@ class EngineS:
         if int(s1["off_t"][-1]) != s1["words"].shape[0]:
             raise ValueError("EngineS: cell offsets do not match the code rows")
 
-    def _params(self, K, nprobe, rho_override=None, M_override=None, B=None):
+    def _params(self, K, nprobe, rho_override=None, M_override=None, B=None, lean=False):
+        """(M, n1, r). M: a batch of at most TINY queries in search() keeps the reference's buffer, because
+        its overflowing queries are redone with other operand precision (fp16, while the main pass keeps
+        fp32), so the buffer size decides which arithmetic gives their candidates. Elsewhere the main pass
+        and the fallback share one precision and a larger buffer (index.emit_buffer) changes no result."""
         NC = len(self.s1["off"]) - 1
         N = self.s1["words"].shape[0]
-        M = M_override or self.M or index.emit_buffer(B, K)
+        small = B is not None and B <= self.TINY and not lean
+        M = M_override or self.M or (self.SMALL_CAP if small else index.emit_buffer(B, K))
         beta, rho = (1.1, 0.75) if K <= 400 else (0.7, 0.5)
         if rho_override:
             beta, rho = 1.5, rho_override
         n1 = min(max(int(np.ceil(beta * K / (N / NC / self.BN + 1))), 1), nprobe)
         return M, n1, int(np.ceil(rho * K))
 
-    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None, half=True):
+    def stage1(self, Qr, QM, probe, K, rho_override=None, M_override=None, half=True, lean=False):
         """Threshold-and-emit over the trellis codes (src/s1cell.py:176-195). Returns (pos, ok). half: fp16
-        dot operands (src/s1cell.py:127,131-132)."""
+        dot operands (src/s1cell.py:127,131-132); lean: the latency path's buffer rule (_params)."""
         s1 = self.s1
         NC = len(s1["off"]) - 1
         B = Qr.shape[0]
         dev = Qr.device
-        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override, B)
+        M, n1, r = self._params(K, probe.shape[1], rho_override, M_override, B, lean)
         L = int(s1["L"])
         scratch = _lib.pairs_scratch(B, NC, dev)
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch)
@@ -106,12 +112,12 @@ class EngineS:
         self._est, self._sd = est, sd
         return _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
 
-    def _gpu(self, Qb, K, z, nprobe, k):
+    def _gpu(self, Qb, K, z, nprobe, k, lean=False):
         if self.H is None:
             raise RuntimeError("EngineS.H (fp16 vectors in id order) must be set before searching")
         Qr, QC, QM, Zq = self._dense(Qb)
         probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe)
-        pos, ok = self.stage1(Qr, QM, probe, K, half=len(Qb) > self.TINY)
+        pos, ok = self.stage1(Qr, QM, probe, K, half=len(Qb) > self.TINY, lean=lean)
         ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq, probe)
 
@@ -128,7 +134,7 @@ class EngineS:
             hb = torch.empty((B, k + 1) if host else (B,), dtype=torch.int64 if host else torch.bool, pin_memory=True)
 
             def run():
-                outs = self._gpu(qs, K, z, nprobe, k)
+                outs = self._gpu(qs, K, z, nprobe, k, lean=host and B == 1)
                 if host:
                     _lib.pack_ids(outs[0], outs[1], hb)  # one launch writes the pinned buffer directly
                 else:
