@@ -30,6 +30,7 @@ SIGNATURES = {
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
     "fvs_pairs_scratch_bytes": [I64, I32],
+    "fvs_pairs_noalloc": [P, I64, I32, I32, I32, P, P, P, P, P, P, P, P, P],
     "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan_civf8": [I32, I32] + [P] * 17 + [I32, I32, P],
@@ -213,6 +214,22 @@ def pairs(probe, n, NC, QM, mnorm, scratch=None, qadd=None):
                            _dev(qid, torch.int32, "qid"), _dev(qrank, torch.int32, "qrank"),
                            _dev(qcp, torch.float32, "qcp"), _stream()), "fvs_pairs")
     return qid, qrank, coff, ccnt, qcp
+
+
+def pairs_noalloc(probe, n, NC, QM, mnorm, out, qadd=None):
+    """pairs() through fvs_pairs_noalloc: the library's static scratch instead of a caller buffer, and the
+    caller's output tensors out = (qid [B*n], qrank [B*n], coff [NC], ccnt [NC], qcp [B*n]); nothing is
+    allocated on the device by this call."""
+    B, npr = probe.shape
+    if QM.shape != (B, NC):
+        raise ValueError("pairs_noalloc: QM shape")
+    qid, qrank, coff, ccnt, qcp = out
+    _check(lib().fvs_pairs_noalloc(_dev(probe, torch.int32, "probe"), B, npr, n, NC, _dev(QM, torch.float16, "QM"),
+                                   _opt(mnorm, torch.float32, "mnorm", (NC,)), _opt(qadd, torch.float32, "qadd", (B,)),
+                                   _dev(ccnt, torch.int32, "ccnt", (NC,)), _dev(coff, torch.int32, "coff", (NC,)),
+                                   _dev(qid, torch.int32, "qid", (B * n,)), _dev(qrank, torch.int32, "qrank", (B * n,)),
+                                   _dev(qcp, torch.float32, "qcp", (B * n,)), _stream()), "fvs_pairs_noalloc")
+    return out
 
 
 def pairs2(probe, n1, NC, QM, mnorm, scratch=None, qadd=None):

@@ -19,7 +19,15 @@
 // and score rows once to compact its queries in ascending order -- the order of the reference's
 // stable sort -- with no atomics, no per-cell sort and no column gathers. The first-pass list (the
 // first n1 probe columns) and the full list come out of one matrix (fvs_pairs2).
+#include <mutex>
+
 #include "fvs_common.h"
+
+// The allocation-free pair builder's scratch (fvs_pairs_noalloc): the rank and score matrices live in
+// this file-scope device array instead of a caller buffer. Each device that runs the library holds its
+// own copy until the process ends; host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns (the array's name is not a device address on the host).
+static __device__ __align__(256) uint8_t scratch[FVS_PAIRS_NOALLOC_SCRATCH];
 
 namespace {
 
@@ -939,6 +947,46 @@ extern "C" int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n
   if (!probe || !QM || !ccnt || !coff || !scratch || !qid || !qrank || !qcp) return FVS_E_ARG;
   const PairList la{qid, qrank, qcp, coff, (uint32_t)n};
   return pairs_impl(probe, B, npr, NC, QM, mnorm, qadd, scratch, scratch_bytes, ccnt, la, nullptr, nullptr,
+                    (hipStream_t)stream);
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, taken once per device.
+int static_scratch(void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return FVS_E_CAPACITY;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return FVS_E_ARG;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FVS_OK;
+}
+
+}  // namespace
+
+extern "C" int fvs_pairs_noalloc(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC,
+                                 const uint16_t *QM, const float *mnorm, const float *qadd, int32_t *ccnt,
+                                 int32_t *coff, int32_t *qid, int32_t *qrank, float *qcp, void *stream) {
+  if (B < 0 || NC <= 0 || n <= 0 || n > npr || n > 65535) return FVS_E_ARG;
+  if (!probe || !QM || !ccnt || !coff || !qid || !qrank || !qcp) return FVS_E_ARG;
+  if (NC > kMaxNC || 2 * matrix_bytes(B, NC) > (int64_t)FVS_PAIRS_NOALLOC_SCRATCH) return FVS_E_CAPACITY;
+  void *buf = nullptr;
+  const int e = static_scratch(&buf);
+  if (e) return e;
+  const PairList la{qid, qrank, qcp, coff, (uint32_t)n};
+  return pairs_impl(probe, B, npr, NC, QM, mnorm, qadd, buf, FVS_PAIRS_NOALLOC_SCRATCH, ccnt, la, nullptr, nullptr,
                     (hipStream_t)stream);
 }
 

@@ -120,6 +120,21 @@ int fvs_pairs(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t N
               int32_t *qid, int32_t *qrank, float *qcp, void *stream);
 
 /*
+ * fvs_pairs without a scratch argument, for callers that cannot allocate device memory (code under graph
+ * capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its pair
+ * lists come from torch ops. Same inputs, outputs and results as fvs_pairs; the rank and score matrices
+ * live in a static device array of FVS_PAIRS_NOALLOC_SCRATCH bytes that the library holds on each device
+ * it runs on until the process ends, so fvs_pairs_scratch_bytes(B, NC) must not exceed it (FVS_E_CAPACITY
+ * otherwise: 32 MiB covers B <= 2048 at NC = 4096). The call allocates and frees nothing. Every call on a
+ * device shares that device's array and overwrites what it reads (nothing needs clearing between calls):
+ * calls that overlap on one device race, so callers serialise them (one stream, or events).
+ */
+#define FVS_PAIRS_NOALLOC_SCRATCH (32 << 20)
+int fvs_pairs_noalloc(const int32_t *probe, int64_t B, int32_t npr, int32_t n, int32_t NC, const uint16_t *QM,
+                      const float *mnorm, const float *qadd, int32_t *ccnt, int32_t *coff, int32_t *qid,
+                      int32_t *qrank, float *qcp, void *stream);
+
+/*
  * Both pair lists of one search batch from one pass: the first-pass list of the first n1 probe columns
  * (ccnt1, coff1, qid1, qrank1, qcp1 over B*n1 pairs) and the emit list of all npr columns (ccnt, coff,
  * qid, qrank, qcp over B*npr pairs), each exactly as fvs_pairs gives it. Replaces the two pairs_fast
