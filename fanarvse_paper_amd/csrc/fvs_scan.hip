@@ -28,16 +28,14 @@
 // The item's row scales sit in LDS; rows outside the cell get a NaN scale: their estimate is NaN,
 // which never passes `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
 //
-// Emit: for each accumulator element the wave takes a ballot of `est >= t0`; the passing lanes get
-// consecutive slots of the wave's own LDS region (a wave-uniform counter, no atomics) and the other
-// lanes write to a private dummy slot, so the store needs no divergent branch. If a wave's region
-// overflows, the item's staged candidates are dropped and the item is redone on the direct path
-// (one global atomic per candidate), which is also the path of cells probed by more than kMaxQ
-// queries. Each pair of the item falls in exactly one tile, so while it emits, a lane numbers its own
-// candidates (the query of its column, its half of the rows); the per-(query, wave, half) counts go to
-// LDS at the end of the tile. At the end of the item one global atomic per (item, query) reserves the
-// query's buffer range, the counts are prefix-summed, and every staged candidate is written out at
-// base + prefix + its own number, with no per-candidate atomics.
+// Emit: for each accumulator element the wave takes a ballot of `est >= t0` (the compare's own lane
+// mask). An empty ballot costs a scalar branch; otherwise the passing lanes, under the exec mask, take
+// consecutive slots of the wave's own LDS region (a wave-uniform counter, no atomics, the overflow test
+// scalar). If a wave's region overflows, the item's staged candidates are dropped and the item is redone
+// on the direct path (one global atomic per candidate), which is also the path of cells probed by more
+// than kMaxQ queries. At the end of the item every staged candidate takes its number among its pair's
+// candidates with an LDS atomic, one global atomic per (item, query) reserves the query's buffer range,
+// and every candidate is written out at base + number, with no per-candidate global atomics.
 #include "fvs_common.h"
 
 namespace {
@@ -46,8 +44,7 @@ constexpr int kR = 256;
 constexpr int kNB = 2;       // 32-row blocks per wave
 constexpr int kCB = 4 * kNB; // 32-row blocks per work item
 constexpr int kMeta = 512;   // pairs staged in LDS at a time
-constexpr int kEW = 768;     // LDS slots per wave: kEW - 64 for candidates, 64 dummy slots
-constexpr int kCap = kEW - 64;
+constexpr int kCap = 768;    // LDS candidate slots per wave
 constexpr int kMaxQ = 1024;  // queries per cell handled by the staged emit
 
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
@@ -60,11 +57,11 @@ struct Meta {  // one (query, cell) pair of the item
 };
 
 struct EmitLds {
-  float est[4][kEW];
-  uint32_t tag[4][kEW];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | number (20-27)
-  uint8_t cnt8[kMaxQ][8];  // candidates of (pair, wave, half); then their exclusive prefix over (wave, half)
-  int qids[kMaxQ];         // the pair's query
-  int qbase[kMaxQ];        // the pair's base in its query's buffer
+  float est[4][kCap];
+  uint32_t tag[4][kCap];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | number (20-31)
+  uint32_t lcnt[kMaxQ];   // candidates of each pair in the item (the flush numbers them with LDS atomics)
+  int qids[kMaxQ];        // the pair's query
+  int qbase[kMaxQ];       // the pair's base in its query's buffer
   int n[4];
 };
 
@@ -158,7 +155,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
     if constexpr (MODE == 1) {
       if (staged)
-        for (int j = tid; j < qn; j += 256) *reinterpret_cast<uint2 *>(E->cnt8[j]) = make_uint2(0u, 0u);
+        for (int j = tid; j < qn; j += 256) E->lcnt[j] = 0u;
     }
 
     auto scan = [&](const bool direct, bool first) {
@@ -213,7 +210,6 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
             const Meta m = meta[valid ? jl : nq - 1];
             const float th = MODE == 1 && valid ? m.x : __builtin_inff();
             const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
-            int nmine = 0;  // this lane's candidates of the tile (its query, its half of the rows)
 #pragma unroll
             for (int u = 0; u < kNB; u++) {
               if (MODE == 0 && !act[u]) continue;
@@ -235,6 +231,11 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
                 if (h == 0 && valid)
                   bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + kNB * w + u - (cs >> 5))] = mx;
               } else if (!direct) {
+                // Per element: a wave ballot of est >= t0 (the compare's own mask). An empty ballot (about
+                // half of them) is a scalar branch; otherwise the passing lanes, under the exec mask, take
+                // consecutive slots of the wave's region. The region's fill is wave-uniform, so the
+                // overflow test is scalar too; the count keeps growing past kCap so that the item end
+                // sees the overflow and redoes the item on the direct path.
                 float *est = E->est[w];
                 uint32_t *tag = E->tag[w];
 #pragma unroll
@@ -242,11 +243,14 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
                   const bool pass = ev[v] >= th;
                   const uint64_t bal = __ballot(pass);
                   if (bal) {
-                    const int slot = pass ? min(ebase + fvs_lane_prefix(bal), kCap - 1) : kCap + lane;
-                    est[slot] = ev[v];
-                    tag[slot] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3)) + ((uint32_t)nmine << 20);
-                    nmine += pass ? 1 : 0;
-                    ebase += __popcll(bal);
+                    const int pop = __popcll(bal);
+                    if (ebase + pop <= kCap && pass) {
+                      // the region's fill is a scalar offset of the base; the lane adds its rank
+                      const int pre = fvs_lane_prefix(bal);
+                      (est + ebase)[pre] = ev[v];
+                      (tag + ebase)[pre] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
+                    }
+                    ebase += pop;
                   }
                 }
               } else {  // direct path
@@ -266,7 +270,6 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
                 }
               }
             }
-            if (MODE == 1 && !direct && valid) E->cnt8[c0 + jl][2 * w + h] = (uint8_t)nmine;
           };
           // one fragment set: loading the next tile ahead would hold 32 more VGPRs and cost the third
           // resident workgroup, which hides more latency than the prefetch did
@@ -294,22 +297,22 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
           __syncthreads();
           scan(true, false);
         } else {
-          // flush: per pair, the exclusive prefix of its (wave, half) counts and one global reservation of
-          // the total in its query's buffer; then every staged candidate goes to base + prefix + number
-          for (int j = tid; j < qn; j += 256) {
-            const uint2 c2 = *reinterpret_cast<const uint2 *>(E->cnt8[j]);
-            uint32_t run = 0, lo = 0, hi = 0;
+          // flush: every staged candidate takes its number among its pair's candidates with an LDS atomic,
+          // then one global atomic per (item, query) reserves the query's range, and every candidate goes
+          // to base + number
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-              const uint32_t c = ((k < 4 ? c2.x : c2.y) >> (8 * (k & 3))) & 0xffu;
-              if (k < 4)
-                lo |= run << (8 * k);
-              else
-                hi |= run << (8 * (k - 4));
-              run += c;  // <= 8 * 32: every exclusive prefix fits a byte
+          for (int ww = 0; ww < 4; ww++) {
+            const int nn = E->n[ww];
+            for (int k = tid; k < nn; k += 256) {
+              const uint32_t tg = E->tag[ww][k];
+              const uint32_t num = atomicAdd(&E->lcnt[(tg >> 8) & 0xfffu], 1u);  // < 256 rows per item
+              E->tag[ww][k] = tg | (num << 20);
             }
-            *reinterpret_cast<uint2 *>(E->cnt8[j]) = make_uint2(lo, hi);
-            E->qbase[j] = run ? atomicAdd(&cnt[E->qids[j]], (int)run) : 0;
+          }
+          __syncthreads();
+          for (int j = tid; j < qn; j += 256) {
+            const int c = (int)E->lcnt[j];
+            E->qbase[j] = c ? atomicAdd(&cnt[E->qids[j]], c) : 0;
           }
           __syncthreads();
 #pragma unroll
@@ -318,8 +321,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
             for (int k = tid; k < nn; k += 256) {
               const uint32_t tg = E->tag[ww][k];
               const int j = (tg >> 8) & 0xfffu;
-              const int hh = (int)(tg >> 2) & 1;  // the half of the rows: bit 2 of the row offset
-              const int idx = E->qbase[j] + (int)E->cnt8[j][2 * ww + hh] + (int)(tg >> 20);
+              const int idx = E->qbase[j] + (int)(tg >> 20);
               if (idx < CAP) {
                 const int64_t q = E->qids[j];
                 bval[q * CAP + idx] = E->est[ww][k];
