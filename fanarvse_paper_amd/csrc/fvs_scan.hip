@@ -1,23 +1,23 @@
 // int8 stage-1 scan on gfx950 MFMA (v_mfma_i32_32x32x32_i8).
 //
-// Work item = (cell, up to 256 consecutive rows of it from a first row r0), one 4-wave workgroup per
-// item; its 32-row blocks start at r0, r0 + 32, ... The first pass needs the reference's global 32-row
-// blocks (its block maxima are per global block), so its items start on a multiple of 32; the emit
-// pass, whose output does not depend on the grouping, takes items that start at the cell's first row
-// (a cell of up to 256 rows is one item, with no block straddling the cell start). Wave w keeps blocks
-// 2w and 2w+1 of the item (64 code rows) as MFMA A operands in registers for the whole item, so each
-// code byte is read from HBM once per pass. The cell's queries stream through as B operands in tiles
-// of 32:
-//   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the
-//     row scales of its 256 rows are staged in LDS up front (kMeta pairs at a time), so no global
-//     load in the tile loop depends on another;
-//   * every wave loads the B fragments of a tile straight into registers (16-byte lane loads of
-//     the query codes, served by L1/L2: the four waves of an item read the same 8 KB). The waves of
-//     an item never wait for each other inside the tile loop; they synchronise only when the pair
-//     list is staged and when candidates are flushed.
-// Two blocks per wave halve the B-fragment gathers per MFMA. One fragment set per tile (no load of
-// the next tile ahead) and emit regions sized for it keep the kernel at 168 VGPRs and 50 KB of LDS:
-// three resident workgroups per CU, whose waves hide each other's load latency.
+// Work item = (cell, up to 256 consecutive rows of it from a first row r0); its 32-row blocks start at
+// r0, r0 + 32, ... The first pass needs the reference's global 32-row blocks (its block maxima are per
+// global block), so its items start on a multiple of 32; the emit pass, whose output does not depend on
+// the grouping, takes items that start at the cell's first row (a cell of up to 256 rows is one item,
+// with no block straddling the cell start). A 4-wave workgroup runs an item; wave w keeps blocks 2w and
+// 2w+1 (64 code rows) as MFMA A operands in registers for the whole item, so each code byte is read from
+// HBM once per pass. The cell's queries stream through as B operands in tiles of 32:
+//   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the row
+//     scales of its 256 rows are staged in LDS up front (kMeta pairs at a time);
+//   * a tile's B fragments (its 32 query codes, 8 KB) are written straight into LDS by the vector memory
+//     unit (global_load_lds, no registers), in MFMA-step order so that every fragment read is one
+//     contiguous 1 KB ds_read_b128 per wave. The buffer is double-buffered and shared by the four waves:
+//     each wave requests a quarter of tile t + 1 while tile t is computed, and one barrier per tile
+//     publishes it.
+// Two blocks per wave halve the B-fragment reads per MFMA. 168 VGPRs and 52 KB of LDS give three resident
+// workgroups per CU. Both passes are persistent: a workgroup loops over items (grid = resident
+// workgroups), and the next item's pair ids, row scales and code blocks are requested as soon as the
+// current item's tile loop is done, under its flush.
 //
 // Operand layout: lane l holds row/column (l & 31) and, for MFMA step s (k-block of 32 bytes), the
 // 16 bytes at 32*s + 16*(l >> 5); A and B use the same assignment, so the contraction is exact for
@@ -33,7 +33,7 @@
 // consecutive slots of the wave's own LDS region (a wave-uniform counter, no atomics, the overflow test
 // scalar). If a wave's region overflows, the item's staged candidates are dropped and the item is redone
 // on the direct path (one global atomic per candidate), which is also the path of cells probed by more
-// than kMaxQ queries. At the end of the item every staged candidate takes its number among its pair's
+// than kMeta queries. At the end of the item every staged candidate takes its number among its pair's
 // candidates with an LDS atomic, one global atomic per (item, query) reserves the query's buffer range,
 // and every candidate is written out at base + number, with no per-candidate global atomics.
 #include "fvs_common.h"
@@ -45,7 +45,7 @@ constexpr int kNB = 2;       // 32-row blocks per wave
 constexpr int kCB = 4 * kNB; // 32-row blocks per work item
 constexpr int kMeta = 512;   // pairs staged in LDS at a time
 constexpr int kCap = 768;    // LDS candidate slots per wave
-constexpr int kMaxQ = 1024;  // queries per cell handled by the staged emit
+constexpr bool kPersistEmit = true;  // the emit pass loops over items like the first pass
 
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
@@ -59,9 +59,7 @@ struct Meta {  // one (query, cell) pair of the item
 struct EmitLds {
   float est[4][kCap];
   uint32_t tag[4][kCap];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | number (20-31)
-  uint32_t lcnt[kMaxQ];   // candidates of each pair in the item (the flush numbers them with LDS atomics)
-  int qids[kMaxQ];        // the pair's query
-  int qbase[kMaxQ];       // the pair's base in its query's buffer
+  uint32_t lcnt[kMeta];   // candidates of each pair in the item; then the pair's base in its query's buffer
   int n[4];
 };
 
@@ -75,6 +73,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     float *__restrict__ bval, int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
   __shared__ __align__(16) Meta meta[kMeta];
   __shared__ __align__(16) float zsl[32 * kCB];
+  __shared__ __align__(16) v4i bsh[2][8 * 64];  // B tiles, double-buffered: [step s][half h][query li], 16 B each
   EmitLds *E = nullptr;
   if constexpr (MODE == 1) {
     __shared__ EmitLds Es;
@@ -127,25 +126,27 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     }
   };
 
-  // the emit pass takes one item per workgroup (stride = P): a persistent emit with the next item's
-  // loads issued during the flush measured no faster, at 256 VGPRs with spills
-  const int stride = MODE == 0 ? (int)gridDim.x : P;
+  // Both passes loop over items (grid = resident workgroups, stride = grid): once an item's tile loop is
+  // done (and the emit pass knows its regions did not overflow), the next item's pair ids, row scales and
+  // code blocks are requested, so their latency runs under the flush.
+  constexpr bool persist = MODE == 0 || kPersistEmit;
+  const int stride = persist ? (int)gridDim.x : P;
   int p = blockIdx.x;
   Item cur = item_at(p);
-  if constexpr (MODE == 1) {
+  if constexpr (!persist) {
     if (cur.qn == 0) return;
   }
   prefetch(cur);
   while (p < P) {
-    const Item nxt = MODE == 0 ? item_at(p + stride) : Item{P, 0, 0, 0, 0, 0, 0};
+    const Item nxt = persist ? item_at(p + stride) : Item{P, 0, 0, 0, 0, 0, 0};
     if (cur.qn == 0) {
-      if constexpr (MODE == 0) prefetch(nxt);
+      if constexpr (persist) prefetch(nxt);
       cur = nxt;
       p += stride;
       continue;
     }
     const int qn = cur.qn, qoff = cur.qoff, cs = cur.cs;
-    const bool staged = MODE == 1 && qn <= kMaxQ;
+    const bool staged = MODE == 1 && qn <= kMeta;  // one pair chunk: meta holds the pairs until the flush
     const int row0 = cur.r0;  // first row of the item
     if (tid < 32 * kCB) zsl[tid] = zr;
     bool act[kNB];
@@ -180,21 +181,33 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
             m.qcp = qcp[pidx];
             m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
             meta[j] = m;
-            if (MODE == 1 && !direct) E->qids[c0 + j] = q;
           }
         }
         __syncthreads();
 
-        if (any) {
-          const int ntiles = (nq + 31) / 32;
-          // B fragments of a tile: lane (li, h) reads bytes 32*s + 16*h of the code of the tile's query li
-          auto load = [&](v4i (&b)[8], int tile) {
-            const int jr = min(tile * 32 + li, nq - 1);
-            const v4i *src = reinterpret_cast<const v4i *>(q8 + (int64_t)meta[jr].qid * kR + h * 16);
+        const int ntiles = (nq + 31) / 32;
+        // B tile t: the fragments of the tile's 32 queries in MFMA step order, written straight into LDS by
+        // the vector memory unit (global_load_lds, 16 B per lane at base + 16 * lane). Wave w requests steps
+        // 2w and 2w + 1 of tile t + 1 while tile t is computed; one barrier per tile publishes it.
+        auto request = [&](int tile) {
+          const int jr = min(tile * 32 + li, nq - 1);
+          const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
 #pragma unroll
-            for (int s = 0; s < 8; s++) b[s] = src[2 * s];
-          };
-          auto compute = [&](const v4i (&b)[8], int t) {
+          for (int k = 0; k < 2; k++) {
+            const int s = 2 * w + k;
+            __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&bsh[tile & 1][s * 64],
+                                             16, 0, 0);
+          }
+        };
+        auto published = [&]() {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's requests have landed in LDS
+          __syncthreads();
+        };
+        {
+          auto compute = [&](int t) {
+            v4i b[8];
+#pragma unroll
+            for (int s = 0; s < 8; s++) b[s] = bsh[t & 1][s * 64 + lane];
             v16i acc[kNB];
 #pragma unroll
             for (int u = 0; u < kNB; u++) {
@@ -271,15 +284,14 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
               }
             }
           };
-          // one fragment set: loading the next tile ahead would hold 32 more VGPRs and cost the third
-          // resident workgroup, which hides more latency than the prefetch did
+          request(0);
+          published();
           for (int t = 0; t < ntiles; t++) {
-            v4i b[8];
-            load(b, t);
-            compute(b, t);
+            if (t + 1 < ntiles) request(t + 1);  // the other buffer: every wave has left tile t - 1
+            if (any) compute(t);
+            published();
           }
         }
-        __syncthreads();
       }
     };
 
@@ -289,6 +301,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     } else {
       scan(!staged, true);
       if (!staged) {
+        prefetch(nxt);
       } else {
         // a wave whose region overflowed: drop the staged candidates and redo the item on the direct path
         if (lane == 0) E->n[w] = ebase;
@@ -296,7 +309,9 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
         if (E->n[0] > kCap || E->n[1] > kCap || E->n[2] > kCap || E->n[3] > kCap) {
           __syncthreads();
           scan(true, false);
+          prefetch(nxt);
         } else {
+          prefetch(nxt);  // the code blocks are no longer needed: the next item's loads run under the flush
           // flush: every staged candidate takes its number among its pair's candidates with an LDS atomic,
           // then one global atomic per (item, query) reserves the query's range, and every candidate goes
           // to base + number
@@ -312,7 +327,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
           __syncthreads();
           for (int j = tid; j < qn; j += 256) {
             const int c = (int)E->lcnt[j];
-            E->qbase[j] = c ? atomicAdd(&cnt[E->qids[j]], c) : 0;
+            E->lcnt[j] = c ? (uint32_t)atomicAdd(&cnt[meta[j].qid], c) : 0u;
           }
           __syncthreads();
 #pragma unroll
@@ -321,9 +336,9 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
             for (int k = tid; k < nn; k += 256) {
               const uint32_t tg = E->tag[ww][k];
               const int j = (tg >> 8) & 0xfffu;
-              const int idx = E->qbase[j] + (int)(tg >> 20);
+              const int idx = (int)E->lcnt[j] + (int)(tg >> 20);
               if (idx < CAP) {
-                const int64_t q = E->qids[j];
+                const int64_t q = meta[j].qid;
                 bval[q * CAP + idx] = E->est[ww][k];
                 bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
               }
@@ -331,8 +346,9 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
           }
         }
       }
+      __syncthreads();  // the flush has read the LDS tables before the next item's staging rewrites them
     }
-    if constexpr (MODE == 1) break;
+    if constexpr (!persist) break;
     cur = nxt;
     p += stride;
   }
@@ -456,10 +472,9 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // first pass: three resident workgroups per CU, each looping over items with the next item's loads in
-  // flight during the current one; emit: one workgroup per item (a persistent emit with the next item's
-  // loads in flight during the flush measured no faster)
-  const unsigned grid = mode == 0 ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
+  // both passes: three resident workgroups per CU, each looping over items with the next item's loads in
+  // flight during the current one
+  const unsigned grid = (mode == 0 || kPersistEmit) ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, prow, ps,
