@@ -34,6 +34,10 @@ SIGNATURES = {
     "fvs_pairs2": [P, I64, I32, I32, I32, P, P, P, P, I64] + [P] * 10 + [P],
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan_civf8": [I32, I32] + [P] * 17 + [I32, I32, P],
+    "fvs_quantize_i8": [P, I64, I32, P, P, P, P],
+    "fvs_dense_pack": [P, I64, I32, I64, I32, P, P],
+    "fvs_dense_threshold": [P, I64, I32, I32, P, P, P],
+    "fvs_dense_scan": [I32, P, P, I64, I64, P, P, I64, I64, I32, P, P, P, P, I32, P, P],
     "fvs_i8_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, P, P, P, P, I32, I32, I32, P],
     "fvs_threshold": [P, P, I32, P, I32, I64, I32, I32, I32, P, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
@@ -475,3 +479,67 @@ def tiered_score(pos, qc, Zq, code, ncnt=None):
                                   _opt(ncnt, torch.int32, "ncnt", (B,)), B, K, _dev(est, torch.float32, "est"),
                                   _dev(sd, torch.float32, "sd"), _stream()), "fvs_tiered_score")
     return est, sd
+
+
+# --------------------------------------------------------------------------- routing-free scan (brute force)
+DENSE_QT, DENSE_NT = 128, 256  # query and row tile of fvs_dense_scan
+
+
+def round_up(n, m):
+    return -(-n // m) * m
+
+
+def quantize_i8(z, half=False, q=None, scale=None):
+    """(q int8 [n, R], scale [n]): per-row int8 code with scale max|z|/127 (throughput/brute.py:46-47, :51-52);
+    the scale is f32, or fp16 (nearest even) when half. q and scale may be given (views into larger buffers)."""
+    n, R = z.shape
+    q = _empty((n, R), torch.int8, z.device) if q is None else q
+    sdt = torch.float16 if half else torch.float32
+    scale = _empty((n,), sdt, z.device) if scale is None else scale
+    sp = _dev(scale, sdt, "scale", (n,))
+    _check(lib().fvs_quantize_i8(_dev(z, torch.float32, "z"), n, R, _dev(q, torch.int8, "q", (n, R)),
+                                 P(None) if half else sp, sp if half else P(None), _stream()), "fvs_quantize_i8")
+    return q, scale
+
+
+def dense_pack(X, npad, Rp=None, out=None):
+    """Fragment-tiled copy (fvs_dense_pack) of X int8 [n, R], zero-padded to npad rows and Rp columns (default:
+    R rounded up to 128): a flat int8 tensor of npad * Rp bytes."""
+    n, R = X.shape
+    Rp = round_up(R, 128) if Rp is None else Rp
+    T = _empty((npad * Rp,), torch.int8, X.device) if out is None else out
+    if T.numel() != npad * Rp:
+        raise ValueError("dense_pack: output size")
+    _check(lib().fvs_dense_pack(_dev(X, torch.int8, "X") if n else P(None), n, R, npad, Rp, _dev(T, torch.int8, "T"),
+                                _stream()), "fvs_dense_pack")
+    return T
+
+
+def dense_threshold(S, r, cnt=None):
+    """t0 [B] = r-th largest of each row of S f32 [B, n] (throughput/brute.py:59); zeroes cnt [B] if given."""
+    B, n = S.shape
+    t0 = _empty((B,), torch.float32, S.device)
+    _check(lib().fvs_dense_threshold(_dev(S, torch.float32, "S"), B, n, r, _dev(t0, torch.float32, "t0"),
+                                     _opt(cnt, torch.int32, "cnt", (B,)), _stream()), "fvs_dense_threshold")
+    return t0
+
+
+def dense_scan(mode, Qt, qs, B, Zt, zs, N, R, t0=None, cnt=None, bval=None, bpos=None, CAP=1, out=None):
+    """Routing-free int8 scan (throughput/brute.py:7-35): mode 0 fills out f32 [B, N] with the scores, mode 1
+    emits every (q, n) with est >= t0[q] into bval / bpos [B, CAP] and counts them in cnt [B]. Qt / Zt: packed
+    codes (dense_pack) of Bpad / Npad rows; qs and t0 hold Bpad values and zs (fp16) Npad values."""
+    Bpad = Qt.numel() // R
+    Npad = Zt.numel() // R
+    if Qt.numel() != Bpad * R or Zt.numel() != Npad * R or Bpad < B or Npad < N:
+        raise ValueError("dense_scan: packed code sizes")
+    if qs.numel() < Bpad or zs.numel() < Npad or (mode == 1 and t0.numel() < Bpad):
+        raise ValueError("dense_scan: qs, t0 need Bpad values and zs Npad values")
+    if mode == 0 and (out is None or out.shape != (B, N)):
+        raise ValueError("dense_scan: out must be [B, N]")
+    if mode == 1 and (bval.shape != (B, CAP) or bpos.shape != (B, CAP) or cnt.shape != (B,)):
+        raise ValueError("dense_scan: emit buffers must be [B, CAP]")
+    f32, i32 = torch.float32, torch.int32
+    _check(lib().fvs_dense_scan(mode, _dev(Qt, torch.int8, "Qt"), _dev(qs, f32, "qs"), B, Bpad, _dev(Zt, torch.int8, "Zt"),
+                                _dev(zs, torch.float16, "zs"), N, Npad, R, _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"),
+                                _opt(bval, f32, "bval"), _opt(bpos, i32, "bpos"), CAP, _opt(out, f32, "out"),
+                                _stream()), "fvs_dense_scan")

@@ -283,6 +283,47 @@ int fvs_refine_rows(const float *est, const uint8_t *flag, const int32_t *aslot,
                     const int64_t *roff, const int32_t *ids, const uint16_t *rows, const float *Q, int64_t B,
                     int32_t K, int32_t d, int32_t k, int32_t *I, float *scores, int32_t *reads, void *stream);
 
+/* ============================================================ routing-free scan (brute force)
+ * The reference's routing-free stage 1 (throughput/brute.py:10-51, throughput/cbrute.py:22-64): every query's
+ * int8 code against every stored code, with a sample-derived threshold. */
+
+/*
+ * int8 codes of rows (throughput/brute.py:46-47 for the stored rows, :50-52 for queries, any width R): for each
+ * row r of z f32 [n, R], a = max(max_j |z[r][j]|, 1e-12f) / 127.0f and q[r][j] = clamp(rintf(z[r][j] / a),
+ * -127, 127); scale[r] = a (f32) and scale16[r] = a rounded to fp16 (nearest even), each skipped when NULL.
+ */
+int fvs_quantize_i8(const float *z, int64_t n, int32_t R, int8_t *q, float *scale, uint16_t *scale16, void *stream);
+
+/*
+ * Fragment-tiled copy of a code matrix X i8 [n, R] (row-major), zero-padded to npad rows and Rp columns: the
+ * layout fvs_dense_scan reads. The 1 KB block (rb, s) at T + (rb * Rp/32 + s) * 1024 holds, for lane
+ * 32 h + li (0..63), the 16 bytes X[32 rb + li][32 s + 16 h .. + 15] (zero past row n or column R).
+ * R a multiple of 16; Rp >= R a multiple of 32; npad >= n a multiple of 32; X and T 16-byte aligned.
+ * T holds npad * Rp bytes.
+ */
+int fvs_dense_pack(const int8_t *X, int64_t n, int32_t R, int64_t npad, int32_t Rp, int8_t *T, void *stream);
+
+/*
+ * Sample threshold of the routing-free scan (throughput/brute.py:59: t0 = scores.topk(r, 1).values[:, -1]):
+ * t0[q] = the r-th largest of S f32 [B, n] row q, 1 <= r <= n; cnt[q] = 0 when cnt is not NULL (the emit
+ * pass's counters).
+ */
+int fvs_dense_threshold(const float *S, int64_t B, int32_t n, int32_t r, float *t0, int32_t *cnt, void *stream);
+
+/*
+ * Dense int8 scan on MFMA: est[q][n] = ((float)acc * qs[q]) * (float)zs[n] (two products in this order), with
+ * acc = sum_j Q[q][j] * Z[n][j] exact in int32 (Qt, Zt: fvs_dense_pack layout of the query and stored codes,
+ * Bpad and Npad rows). Replaces brute.py's _scan (throughput/brute.py:7-35): mode 0 writes the dense scores
+ * out f32 [B, N] (its MODE 0, used on the threshold sample); mode 1 is its MODE 1: every (q, n) with
+ * est >= t0[q] increments cnt[q] (zeroed by the caller) and the first CAP of a query are stored at
+ * bval[q*CAP + idx] = est, bpos[q*CAP + idx] = n (in no particular order).
+ *   qs f32 and (mode 1) t0 f32 hold Bpad entries, zs fp16 holds Npad entries (entries past B and N are read,
+ *   never used). R (the packed width Rp) a multiple of 128; Bpad a multiple of 128; Npad a multiple of 256.
+ */
+int fvs_dense_scan(int32_t mode, const int8_t *Qt, const float *qs, int64_t B, int64_t Bpad, const int8_t *Zt,
+                   const uint16_t *zs, int64_t N, int64_t Npad, int32_t R, const float *t0, int32_t *cnt, float *bval,
+                   int32_t *bpos, int32_t CAP, float *out, void *stream);
+
 /* ============================================================ trellis engine (latency mode)
  * The default engine of the reference (src/engine_cell.py:70-102 EngineS, src/engine3.py:135-175 Engine8):
  * cell-residual bitshift-trellis codes in stage 1 and the Lloyd-Max tiered code in stage 2. */

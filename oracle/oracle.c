@@ -347,6 +347,67 @@ void or_select(const float *bval, const int32_t *bpos, const int32_t *cnt, int64
   }
 }
 
+/* ---------------------------------------------------------------- routing-free dense scan
+ * throughput/brute.py:46-47, :51-52   codes: a = max(max|z|, 1e-12) / 127, clamp(rint(z / a), -127, 127)
+ * throughput/brute.py:16-17           est = (float)acc * qs[q] * (float)zs[n], two products left to right
+ * throughput/brute.py:31-37           emit every (q, n) with est >= t0[q]
+ * The emitted list is kept in canonical order (est descending, n ascending), truncated to M; cnt is the
+ * full count. */
+void or_quantize_rows(const float *z, int64_t n, int R, int8_t *q, float *scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < n; r++) quant_row(z + r * R, R, q + r * R, scale + r);
+}
+
+static inline int32_t dot_i8(const int8_t *a, const int8_t *b, int R) {
+  int32_t acc = 0;
+  for (int j = 0; j < R; j++) acc += (int32_t)a[j] * (int32_t)b[j];
+  return acc;
+}
+
+static inline float dense_est(const int8_t *q, float qsv, const int8_t *z, uint16_t zsv, int R) {
+  return ((float)dot_i8(q, z, R) * qsv) * h2f(zsv);
+}
+
+void or_dense_scores(const int8_t *Q, const float *qs, int64_t B, const int8_t *Z, const uint16_t *zs, int64_t N, int R,
+                     float *out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t q = 0; q < B; q++)
+    for (int64_t n = 0; n < N; n++) out[q * N + n] = dense_est(Q + q * R, qs[q], Z + n * R, zs[n], R);
+}
+
+void or_dense_emit(const int8_t *Q, const float *qs, int64_t B, const int8_t *Z, const uint16_t *zs, int64_t N, int R,
+                   const float *t0, int M, int32_t *cnt, float *bval, int32_t *bpos) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t q = 0; q < B; q++) {
+    int cap = 1024, c = 0;
+    uint64_t *keys = (uint64_t *)malloc(sizeof(uint64_t) * cap);
+    for (int64_t n = 0; n < N; n++) {
+      const float e = dense_est(Q + q * R, qs[q], Z + n * R, zs[n], R);
+      if (e >= t0[q]) {
+        if (c == cap) {
+          cap *= 2;
+          keys = (uint64_t *)realloc(keys, sizeof(uint64_t) * cap);
+        }
+        keys[c++] = ((uint64_t)ord32(e) << 32) | (uint64_t)(0xffffffffu - (uint32_t)n);
+      }
+    }
+    qsort(keys, (size_t)c, sizeof(uint64_t), cmp_u64_desc);
+    cnt[q] = c;
+    for (int i = 0; i < M; i++) {
+      if (i < c) {
+        const uint32_t k = (uint32_t)(keys[i] >> 32);
+        const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+        memcpy(&bval[q * M + i], &u, 4);
+        bpos[q * M + i] = (int32_t)(0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu));
+      } else {
+        bval[q * M + i] = -1e30f;
+        bpos[q * M + i] = 0;
+      }
+    }
+    free(keys);
+  }
+}
+
 /* ---------------------------------------------------------------- LUT build (a13)
  * throughput/s2lut.py:108-126  L[q, n*16+v] = sum_i Zq[q,4n+i] * bit_i(v), bit_i(v) = (v >> (3-i)) & 1;
  * qsum/qn2 per tier (throughput/s2lut.py:125). tiers: T x (start, end, bits). */

@@ -234,6 +234,62 @@ def select(bval, bpos, cnt, K, kd, delta):
     return pos, est1, ok, ncnt
 
 
+# ------------------------------------------------------------------------- routing-free dense scan
+def quantize_rows(z):
+    """(q int8 [n, R], scale f32 [n]) (throughput/brute.py:46-47, :51-52)."""
+    z = _c(z, np.float32)
+    n, R = z.shape
+    q = np.empty((n, R), np.int8)
+    a = np.empty(n, np.float32)
+    lib().or_quantize_rows(_p(z), I64(n), I32(R), _p(q), _p(a))
+    return q, a
+
+
+def dense_scores(Q, qs, Z, zs16):
+    """est f32 [B, N] = ((float)(Q @ Z.T) * qs[q]) * (float)zs16[n] (throughput/brute.py:16-17)."""
+    Q, qs, Z = _c(Q, np.int8), _c(qs, np.float32), _c(Z, np.int8)
+    zs16 = _c(np.asarray(zs16).view(np.uint16), np.uint16)
+    B, R = Q.shape
+    N = Z.shape[0]
+    out = np.empty((B, N), np.float32)
+    lib().or_dense_scores(_p(Q), _p(qs), I64(B), _p(Z), _p(zs16), I64(N), I32(R), _p(out))
+    return out
+
+
+def row_kth(S, r):
+    """The r-th largest of each row of S (throughput/brute.py:59: topk(r).values[:, -1])."""
+    S = np.asarray(S, np.float32)
+    return np.sort(S, axis=1)[:, S.shape[1] - r].copy()
+
+
+def dense_emit(Q, qs, Z, zs16, t0, M):
+    """(cnt, bval, bpos): every (q, n) with est >= t0[q] (throughput/brute.py:31-37), canonical order, first M."""
+    Q, qs, Z, t0 = _c(Q, np.int8), _c(qs, np.float32), _c(Z, np.int8), _c(t0, np.float32)
+    zs16 = _c(np.asarray(zs16).view(np.uint16), np.uint16)
+    B, R = Q.shape
+    N = Z.shape[0]
+    cnt = np.empty(B, np.int32)
+    bval = np.empty((B, M), np.float32)
+    bpos = np.empty((B, M), np.int32)
+    lib().or_dense_emit(_p(Q), _p(qs), I64(B), _p(Z), _p(zs16), I64(N), I32(R), _p(t0), I32(M), _p(cnt), _p(bval),
+                        _p(bpos))
+    return cnt, bval, bpos
+
+
+def brute_search(q, qs, Z, zs16, K, over=2.0, M=None, sidx=None, sample_every=20):
+    """throughput/brute.py:56-63 on the CPU from the codes (q, qs) of the queries and (Z, zs16) of the stored
+    rows: (pos, est, ok, cnt), pos and est in the canonical order (est descending, position ascending)."""
+    N = len(Z)
+    sidx = np.arange(0, N, sample_every) if sidx is None else np.asarray(sidx)
+    zs16 = np.asarray(zs16).view(np.uint16)
+    M = M or max(4096, 8 * K)
+    r = max(1, int(round(over * K * (len(sidx) / N))))
+    t0 = row_kth(dense_scores(q, qs, np.asarray(Z)[sidx], zs16[sidx]), r)
+    cnt, bval, bpos = dense_emit(q, qs, Z, zs16, t0, M)
+    pos, est, ok, _ = select(bval, bpos, cnt, K, 0, None)
+    return pos, est, ok.astype(bool), cnt
+
+
 def _tiers(TS):
     return np.asarray([[s, e, b] for s, e, b in TS], dtype=np.int32).reshape(-1)
 

@@ -66,6 +66,19 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_i8_scan_civf8(2, 10, *[n] * 17, 1, 1, n) == E_ARG                    # bad mode
     assert L.fvs_i8_scan_civf8(0, 10, *[n] * 17, 1, 1, n) == E_ARG                    # null buffers
     assert L.fvs_i8_scan_civf8(1, 0, *[n] * 17, 1, 1, n) == 0                         # no items
+    # routing-free dense scan: (mode, Qt, qs, B, Bpad, Zt, zs, N, Npad, R, t0, cnt, bval, bpos, CAP, out, stream)
+    assert L.fvs_dense_scan(2, n, n, 4, 128, n, n, 8, 256, 128, n, n, n, n, 1, n, n) == E_ARG   # bad mode
+    assert L.fvs_dense_scan(0, n, n, 4, 128, n, n, 8, 256, 96, n, n, n, n, 1, n, n) == E_SHAPE  # R % 128
+    assert L.fvs_dense_scan(0, n, n, 4, 64, n, n, 8, 256, 128, n, n, n, n, 1, n, n) == E_ARG    # Bpad % 128
+    assert L.fvs_dense_scan(0, n, n, 4, 128, n, n, 300, 256, 128, n, n, n, n, 1, n, n) == E_ARG  # Npad < N
+    assert L.fvs_dense_scan(0, n, n, 4, 128, n, n, 8, 256, 128, n, n, n, n, 1, n, n) == E_ARG   # null buffers
+    assert L.fvs_dense_scan(1, n, n, 0, 128, n, n, 8, 256, 128, n, n, n, n, 1, n, n) == 0       # no queries
+    assert L.fvs_dense_pack(n, 4, 40, 32, 128, n, n) == E_ARG                                    # R % 16
+    assert L.fvs_dense_pack(n, 4, 256, 32, 128, n, n) == E_ARG                                   # Rp < R
+    assert L.fvs_dense_pack(n, 40, 64, 32, 128, n, n) == E_ARG                                   # npad < n
+    assert L.fvs_dense_threshold(n, 4, 10, 11, n, n, n) == E_ARG                                 # r > n
+    assert L.fvs_dense_threshold(n, 4, 10, 0, n, n, n) == E_ARG                                  # r = 0
+    assert L.fvs_quantize_i8(n, 4, 0, n, n, n, n) == E_ARG                                       # R = 0
 
 
 def test_wrappers_refuse_cpu_tensors(L):
