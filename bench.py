@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("throughput", "latency", "host", "largek", "tier"), default="throughput",
+    ap.add_argument("--mode", choices=("throughput", "latency", "host", "largek", "tier", "dense"), default="throughput",
                     help="throughput: the headline config (EngineI8, batch 2000); latency: the trellis default "
                          "engine at batches 1/16/64 (BASELINE.json configs[2]); host: the host-resident engine "
                          "(configs[4]); largek: k=100 with the z sweep (configs[3]); tier: the default engine with "
@@ -88,6 +88,8 @@ def main():
         return tier_mode(args)
     if args.mode == "largek":
         return largek_mode(args)
+    if args.mode == "dense":
+        return dense_mode(args)
     _lib.lib()
     t = time.time()
     X = datagen.gen(args.n, args.d, args.clusters, 0.7, seed=0, device=dev)
@@ -561,6 +563,95 @@ def largek_mode(args):
            "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "int8", "data": "synthetic",
            "config": {"workload": f"large-N high-k, {n}x{d} fp16 synthetic (4096 clusters, alpha 0.5), batch {B}, "
                                   f"k={k}", "nlist": 8192}, "rows": rows}
+    print(json.dumps(out), flush=True)
+
+
+def dense_mode(args):
+    """Config 2's literal shape as a dense contraction: the routing-free Brute scan (throughput/brute.py:41-63)
+    of a 2000-query batch against all 1M stored rows with R = d = 1536 int8 codes, K = 400 candidates per query
+    from a threshold on every 20th row (over = 2), as throughput/e_brute.py:14-24 runs it. Reports the batch
+    rate, the candidates' recall of the true top 10, and the emit scan's share of the int8 MFMA peak."""
+    import numpy as np
+    import torch
+
+    from fanarvse_paper_amd import _lib, brute, datagen, index, metrics
+
+    n, d, B, k, K = args.n, args.d, args.batch, args.k, 400
+    dev = "cuda"
+    t = time.time()
+    X = datagen.gen(n, d, args.clusters, 0.7, seed=0, device=dev)
+    Q = datagen.gen(B, d, args.clusters, 0.7, seed=1, device=dev, dtype=torch.float32)
+    GT = datagen.ground_truth(X, Q, k).cpu().numpy()
+    mu = X[:200000].float().mean(0)
+    V = index.pca_int8_basis(X, R=d)
+    b = brute.Brute(X, mu, V, R=d)
+    torch.cuda.synchronize()
+    log(f"dense codes {n}x{d} built in {time.time() - t:.1f}s")
+    pos, est, ok, cnt = b.search(Q, K)
+    cand = metrics.cand_recall(pos.cpu().numpy(), GT, k)
+    for _ in range(args.warmup):
+        b.search(Q, K)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pos, est, ok, cnt = b.search(Q, K)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    emitted = round(float(cnt.float().mean()), 1)
+    log(f"Brute.search {dt * 1000:.2f} ms/batch, candidate recall@{k} {cand}, flagged {int((~ok).sum())}, "
+        f"emitted per query {emitted}")
+    # the two scans alone (HIP events on the launching stream)
+    q, qs = b.qcode(Q)
+    Qt, qsp, _ = b._pack_queries(q, qs)
+    S = torch.empty(B, len(b.sidx), device=dev)
+    t_sample = _time_launch(lambda: _lib.dense_scan(0, Qt, qsp, B, b.Zst, b.zssp, len(b.sidx), b.Rp, out=S), 5, torch)
+    r = max(1, int(round(2.0 * K * b.frac)))
+    cnt = torch.empty(B, dtype=torch.int32, device=dev)
+    t0v = _lib.dense_threshold(S, r, cnt)
+    Qt, qsp, t0p = b._pack_queries(q, qs, t0v)
+    M = max(4096, 8 * K)
+    bval = torch.empty(B, M, device=dev)
+    bpos = torch.empty(B, M, dtype=torch.int32, device=dev)
+    t_emit = _time_launch(lambda: _lib.dense_scan(1, Qt, qsp, B, b.Zt, b.zsp, n, b.Rp, t0=t0p, cnt=cnt, bval=bval,
+                                                  bpos=bpos, CAP=M), 5, torch, setup=lambda: _lib.fill_u32(cnt, 0))
+    ops_emit = 2.0 * B * n * b.Rp
+    ops_sample = 2.0 * B * len(b.sidx) * b.Rp
+    emit_tops = ops_emit / (t_emit * 1e-3) / 1e12
+    kernels = {"dense_emit": {"ms": round(t_emit, 4), "ops": ops_emit, "int8_TOPS": round(emit_tops, 1),
+                              "mfma_frac": round(emit_tops / INT8_PEAK_TOPS, 4),
+                              "emitted_per_query": emitted},
+               "dense_sample": {"ms": round(t_sample, 4), "ops": ops_sample,
+                                "int8_TOPS": round(ops_sample / (t_sample * 1e-3) / 1e12, 1)}}
+    log(f"kernels {kernels}")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as orc
+
+        Zc, zsc, qc, qsc = b.Z.cpu().numpy(), b.zs.cpu().numpy(), q.cpu().numpy(), qs.cpu().numpy()
+        t = time.perf_counter()
+        orc.brute_search(qc[:1], qsc[:1], Zc, zsc, K)
+        per_q = time.perf_counter() - t
+        nq = int(max(1, min(B, args.cpu_seconds / max(per_q, 1e-6))))
+        t = time.perf_counter()
+        orc.brute_search(qc[:nq], qsc[:nq], Zc, zsc, K)
+        cdt = time.perf_counter() - t
+        cores = len(os.sched_getaffinity(0))
+        cpu = {"value": round(nq / cdt, 2), "unit": "queries/s", "cores": min(cores, int(os.environ.get(
+            "OMP_NUM_THREADS", cores))), "kind": "port",
+            "sample": f"first {nq} queries, the oracle's scalar C restatement of the same scan, threshold and "
+                      f"top-K over the same codes"}
+        log(f"cpu baseline {cpu}")
+    out = {"metric": "routing-free dense int8 scan (2000 x 1M x 1536): queries/s; % of int8-MFMA peak",
+           "value": round(B / dt, 1), "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(dt * 1000, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int8", "data": "synthetic",
+           "config": {"workload": f"dense mode, Brute.search of {B} queries over {n}x{d} fp16 synthetic, R={d}, "
+                                  f"K={K}, over=2, sample every 20th row", "n": n, "d": d, "R": d, "batch": B,
+                      "K": K, "cand_recall@10": cand, "flagged": int((~ok).sum())},
+           "roofline": {"bound": "mfma", "achieved": round(emit_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                        "frac": round(emit_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                        "kernel": "k_dense_scan<1> (threshold-and-emit pass over all rows)"},
+           "kernels": kernels, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
 
 

@@ -11,11 +11,16 @@
 //
 // Scan: a workgroup computes 128 queries x 256 rows over the whole K dimension: four waves of 64 queries
 // x 128 rows (8 MFMA tiles, 128 accumulators per lane). Operand blocks stream through three LDS stages of
-// 4 K-steps (48 KB each); each wave requests a quarter of stage g + 2 while stage g is computed, one
-// barrier per stage. The grid is persistent (one workgroup per CU) and XCD-aware: the 32 workgroups of
-// an XCD (workgroup b runs on XCD b % 8) process 32 consecutive tiles at a time, i.e. all 16 query tiles
-// of 2 row tiles, so a row tile is read from HBM into one L2 and reused there 16 times. The pipeline
-// runs across tile boundaries, so the next tile's first stages load under the current tile's epilogue.
+// 2 K-steps (24 KB each); each wave requests a quarter of stage g + 2 while stage g is computed, one
+// barrier per stage. Two workgroups share a CU (76 KB of LDS and at most 256 registers per lane each), so
+// one workgroup's epilogue and barrier waits overlap the other's MFMAs. The grid is persistent and
+// XCD-aware: the 64 workgroups of an XCD (workgroup b runs on XCD b % 8) process 64 consecutive tiles at a
+// time, i.e. all 16 query tiles of 4 row tiles, so a row tile is read from HBM into one L2 and reused
+// there 16 times. The pipeline runs across tile boundaries, so the next tile's first stages load under the
+// current tile's epilogue.
+//
+// The LDS traffic bounds this layout: per 32 MFMAs a workgroup reads 24 KB of operands from LDS and writes
+// 12 KB into it, about 140 bytes per clock per CU at the MFMA peak.
 //
 // Epilogue (canonical): est = ((float)acc * qs[q]) * (float)zs[n] (two products, left to right);
 //   mode 0: out[q * N + n] = est;
@@ -28,7 +33,8 @@ namespace {
 
 constexpr int kQT = 128;             // queries per workgroup tile
 constexpr int kNT = 256;             // rows per workgroup tile
-constexpr int kSS = 4;               // 32-byte K steps per LDS stage
+constexpr int kSS = 2;               // 32-byte K steps per LDS stage
+constexpr int kWGCU = 2;             // workgroups resident per CU
 constexpr int kNS = 3;               // LDS stages
 constexpr int kQB = kQT / 32;        // query blocks per tile
 constexpr int kRB = kNT / 32;        // row blocks per tile
@@ -63,7 +69,7 @@ __device__ __forceinline__ int tile_requests(int w) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256, 1) void k_dense_scan(const int8_t *__restrict__ Qt, const float *__restrict__ qs,
+__global__ __launch_bounds__(256, kWGCU) void k_dense_scan(const int8_t *__restrict__ Qt, const float *__restrict__ qs,
                                                        int B, const int8_t *__restrict__ Zt,
                                                        const uint16_t *__restrict__ zs16, int N, int nsteps, int ntq,
                                                        int ntiles, int m8, const float *__restrict__ t0,
@@ -74,7 +80,7 @@ __global__ __launch_bounds__(256, 1) void k_dense_scan(const int8_t *__restrict_
   // stage layout: block row br (query blocks 0..3, then row blocks 0..7), K step s at [br][s]: the four K
   // steps of a block row are 4 KB contiguous, in LDS as in the tiled global layout, so one LDS base (M0)
   // and one global address serve all four loads with the same immediate offsets
-  __shared__ __align__(16) v4i ls0[kBR][kSS][64], ls1[kBR][kSS][64], ls2[kBR][kSS][64];  // 48 KB each
+  __shared__ __align__(16) v4i ls0[kBR][kSS][64], ls1[kBR][kSS][64], ls2[kBR][kSS][64];  // 24 KB each
   // per-tile constants, in three buffers by tile number mod 3: row scales (fp16 bits), query scales,
   // thresholds. Tile k + 2's constants are requested while other waves may still run tile k's epilogue
   // (with one stage per tile), so two buffers would not do.
@@ -117,10 +123,9 @@ __global__ __launch_bounds__(256, 1) void k_dense_scan(const int8_t *__restrict_
     for (int r = 0; r < 3; r++) {
       const int8_t *src = rsrc[r] + voff;
       lds_ptr dst = (lds_ptr)&L[3 * w + r][0][0];
+      static_assert(kSS == 2, "one load per K step of the stage");
       __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(src, dst, 16, 1024, 0);
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 2048, 0);
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 3072, 0);
     }
     if (rst == 0) {
       if (w < 2) {  // rows 128 w .. 128 w + 127: 4 bytes (two fp16) per lane
@@ -353,7 +358,7 @@ extern "C" int fvs_dense_scan(int32_t mode, const int8_t *Qt, const float *qs, i
   const int64_t ntiles = (int64_t)ntq * (Npad / kNT);
   if (ntiles > ((int64_t)1 << 30)) return FVS_E_CAPACITY;
   const int cus = fvs_cu_count();
-  const int m8 = std::max(1, cus / 8);  // workgroups per XCD
+  const int m8 = std::max(1, kWGCU * cus / 8);  // workgroups per XCD
   const dim3 grid((unsigned)(8 * m8)), block(256);
   hipStream_t st = (hipStream_t)stream;
   if (mode == 0)
