@@ -35,6 +35,7 @@ SIGNATURES = {
     "fvs_pairs": [P, I64, I32, I32, I32, P, P, P, P, P, P, I64, P, P, P, P],
     "fvs_i8_scan_civf8": [I32, I32] + [P] * 17 + [I32, I32, P],
     "fvs_quantize_i8": [P, I64, I32, P, P, P, P],
+    "fvs_route_keys": [P, P, P, I64, I32, P, P],
     "fvs_dense_pack": [P, I64, I32, I64, I32, P, P],
     "fvs_dense_threshold": [P, I64, I32, I32, P, P, P],
     "fvs_dense_scan": [I32, P, P, I64, I64, P, P, I64, I64, I32, P, P, P, P, I32, P, P],
@@ -460,6 +461,16 @@ def route_topk_scaled(QM, scale, nprobe, qadd=None):
                                        _opt(qadd, torch.float32, "qadd", (B,)), B,
                                        NC, nprobe, _dev(probe, torch.int32, "probe"), _stream()), "fvs_route_topk_scaled")
     return probe
+
+
+def route_keys(QM, scale=None, qadd=None):
+    """fp16 [B, NC] routing keys ((float)QM + qadd[q]) * scale[c], each term optional (throughput/enginei8.py:72-76)."""
+    B, NC = QM.shape
+    out = _empty((B, NC), torch.float16, QM.device)
+    _check(lib().fvs_route_keys(_dev(QM, torch.float16, "QM"), _opt(scale, torch.float32, "scale", (NC,)),
+                                _opt(qadd, torch.float32, "qadd", (B,)), B, NC, _dev(out, torch.float16, "out"),
+                                _stream()), "fvs_route_keys")
+    return out
 
 
 def tiered_score(pos, qc, Zq, code, ncnt=None):

@@ -934,6 +934,40 @@ extern "C" int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, con
   return fvs_launch_status();
 }
 
+namespace {
+// out[q][c] = fp16(((float)QM[q][c] + qadd[q]) * scale[c]), each term only when its array is given (no "+ 0",
+// which would turn -0 into +0). Four cells per thread.
+template <bool ADD, bool MUL>
+__global__ __launch_bounds__(256) void k_route_keys(const uint16_t *__restrict__ QM, const float *__restrict__ scale,
+                                                    const float *__restrict__ qadd, int64_t B, int NC,
+                                                    uint16_t *__restrict__ out) {
+  const int64_t n = B * NC;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q = i / NC;
+    const int c = (int)(i - q * NC);
+    float v = fvs_h2f(QM[i]);
+    if (ADD) v = v + qadd[q];
+    if (MUL) v = v * scale[c];
+    out[i] = fvs_f2h(v);
+  }
+}
+}  // namespace
+
+extern "C" int fvs_route_keys(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC,
+                              uint16_t *out, void *stream) {
+  if (B < 0 || NC <= 0) return FVS_E_ARG;
+  if (B == 0) return FVS_OK;
+  if (!QM || !out) return FVS_E_ARG;
+  const int64_t n = B * NC;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 16384);
+  hipStream_t st = (hipStream_t)stream;
+  if (qadd && scale) hipLaunchKernelGGL((k_route_keys<true, true>), dim3(grid), dim3(256), 0, st, QM, scale, qadd, B, NC, out);
+  else if (qadd) hipLaunchKernelGGL((k_route_keys<true, false>), dim3(grid), dim3(256), 0, st, QM, scale, qadd, B, NC, out);
+  else if (scale) hipLaunchKernelGGL((k_route_keys<false, true>), dim3(grid), dim3(256), 0, st, QM, scale, qadd, B, NC, out);
+  else hipLaunchKernelGGL((k_route_keys<false, false>), dim3(grid), dim3(256), 0, st, QM, scale, qadd, B, NC, out);
+  return fvs_launch_status();
+}
+
 extern "C" int64_t fvs_pairs_scratch_bytes(int64_t B, int32_t NC) {
   if (B < 0 || NC <= 0) return -1;
   return 2 * matrix_bytes(B, NC);  // rank matrix, then score matrix

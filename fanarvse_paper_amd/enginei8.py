@@ -9,8 +9,16 @@ buffer, an fp32 LUT and no delta rule), as in the reference. Every stage runs in
 two plain fp16 GEMMs (routing scores and the rotated tier queries) use torch's BLAS.
 
 The class attributes default to the final operating point of throughput/e_v3final.py:16,28-30
-(NROUTE, LUTF, LUTH, DELTA = 0.07, RHO = 0.6, MSZ = 3072). Variants this build does not implement
-(PROJ, K2, routing without NROUTE) raise NotImplementedError instead of silently changing results.
+(NROUTE, LUTF, LUTH, DELTA = 0.07, RHO = 0.6, MSZ = 3072). The routing and stage-2 knobs of the reference
+work as there (throughput/enginei8.py:66-86):
+  * NROUTE = False: QM = fp16(Qb) @ means16.T, cells ranked by (float)QM * inv_mnorm (rounded to fp16 when
+    ROUTE16), pair constants QM unscaled; PROJ (with NROUTE False) replaces QM by the stage-1 projection
+    fp16(QC + fp16(fp16(Qb) @ W1) @ mproj) and needs s1["W1"]; the fallback keeps the plain QM and fp32 keys;
+  * UNSORTED: the n_p probed cells in cell order instead of score order (the reference's unsorted topk
+    order is unspecified; the first n1 of them seed the threshold either way);
+  * SORTROUTE: sort-then-cut equals the sorted top-n_p under this build's (score desc, cell asc) order;
+  * K2 < K: every candidate is scored by the LUT stage, and only the K2 best go on to the delta rule
+    and the exact reads.
 """
 import math
 
@@ -102,15 +110,12 @@ class EngineI8:
     # ------------------------------------------------------------------ stages
     def _knobs(self):
         """The knob values captured work depends on: a search after a change captures new graphs."""
-        return (self.MSZ, self.BETA, self.RHO, self.DELTA, self.LUTF, self.LUTH)
+        return (self.MSZ, self.BETA, self.RHO, self.DELTA, self.LUTF, self.LUTH, self.NROUTE, self.ROUTE16,
+                self.PROJ, self.UNSORTED, self.SORTROUTE, self.K2)
 
     def _check_knobs(self):
-        if self.PROJ:
-            raise NotImplementedError("PROJ routing is not implemented")
-        if self.K2 is not None:
-            raise NotImplementedError("progressive stage 2 (K2) is not implemented")
-        if not self.NROUTE:
-            raise NotImplementedError("only NROUTE routing (normalised cell means) is implemented")
+        if self.PROJ and not self.NROUTE and "W1" not in self.s1:
+            raise ValueError("PROJ routing needs the stage-1 basis s1['W1'] (a trellis-built s1)")
 
     def _params(self, K, nprobe, rho_override=None, M_override=None):
         NC = len(self.s1["off"]) - 1
@@ -136,7 +141,8 @@ class EngineI8:
         q8, qs = (qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"]))[:2]
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
         scratch = _lib.pairs_scratch(B, NC, Qb.device)
-        pr, prn = _lib.pairs2(probe, n1, NC, QM, self.mnorm, scratch)
+        # NROUTE: QM holds normalised-mean scores, the pair constants scale them back by |m_c|
+        pr, prn = _lib.pairs2(probe, n1, NC, QM, self.mnorm if self.NROUTE else None, scratch)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=Qb.device)
         _lib.i8_scan(0, self.blocks, q8, qs, pr, self.Z, self.zs, bm=bm, MB=self.MB, n1=n1)
         cnt = torch.empty((B,), dtype=torch.int32, device=Qb.device)  # zeroed by the threshold kernel
@@ -150,9 +156,31 @@ class EngineI8:
         self._bm, self._bval, self._bpos, self._n1, self._M = bm, bval, bpos, n1, M
         return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
 
-    def _route(self, Qh, nprobe):
-        QM = Qh @ self.meansN.T
-        return QM, _lib.route_topk(QM, nprobe)
+    def _plain_qm(self, Qh):
+        """QM of the routing (NROUTE: against the normalised means; else against means16)."""
+        return Qh @ (self.meansN if self.NROUTE else self.s1["means16"]).T
+
+    def _route(self, Qh, QC, nprobe, QM=None):
+        """(QM, probe) of the main pass (throughput/enginei8.py:66-76)."""
+        if self.NROUTE:
+            QM = self._plain_qm(Qh) if QM is None else QM
+            probe = _lib.route_topk(QM, nprobe)
+        else:
+            if self.PROJ:
+                if not hasattr(self, "mproj"):
+                    s1 = self.s1
+                    self.mproj = ((s1["means16"].float() - s1["c"]) @ s1["W1"].float()).half().T.contiguous()
+                    self.W1h = s1["W1"].half().contiguous()
+                QM = _lib.route_keys((Qh @ self.W1h) @ self.mproj, None, QC)
+            elif QM is None:
+                QM = self._plain_qm(Qh)
+            if self.ROUTE16:
+                probe = _lib.route_topk(_lib.route_keys(QM, self.s1["inv_mnorm"], None), nprobe)
+            else:
+                probe = _lib.route_topk_scaled(QM, self.s1["inv_mnorm"], nprobe)
+        if self.UNSORTED:
+            probe = torch.sort(probe, dim=1).values  # cell order
+        return QM, probe
 
     def _gpu(self, Qb, K, z, nprobe, k):
         """One batch on the GPU without host synchronisation: (ok, I, reads, ids, scores, blas); blas holds the
@@ -171,7 +199,7 @@ class EngineI8:
             self._side = torch.cuda.Stream(device=Qb.device)
         prepped = torch.cuda.Event()
         prepped.record(main)
-        QM = Qh @ self.meansN.T
+        QM0 = self._plain_qm(Qh)
         self._side.wait_event(prepped)
         half = self.LUTF and self.LUTH
         with torch.cuda.stream(self._side):
@@ -179,17 +207,24 @@ class EngineI8:
             pre = _lib.lut_build(Zq, self.code["TS"], half)
         for t in (Zq, *pre):  # made on the side stream, used on this one
             t.record_stream(main)
-        probe = _lib.route_topk(QM, nprobe)
+        QM, probe = self._route(Qh, QC, nprobe, QM0)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         main.wait_stream(self._side)
         ok, I, reads, ids, scores = self._finish(Qb, Zq, QC, pos, ok, K, z, k, half=half,
                                                  ncnt=self._ncnt if self.DELTA is not None else None, pre=pre)
-        return ok, I, reads, ids, scores, (zq, QM, Zq)
+        return ok, I, reads, ids, scores, (zq, QM0, Zq)  # the fallback routes on the plain QM
 
     def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt, pre=None):
         """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95)."""
         if pre is None:
             pre = _lib.lut_build(Zq, self.code["TS"], half)
+        if self.K2 is not None and self.K2 < K:
+            # progressive stage 2 (throughput/enginei8.py:82-85): score all K, keep the K2 best by estimate
+            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None)
+            cntK = torch.full((pos.shape[0],), K, dtype=torch.int32, device=pos.device)
+            pos = _lib.select(e_all.contiguous(), pos.contiguous(), cntK, self.K2, 0, None)[0]
+            if ncnt is not None:
+                ncnt = ncnt.clamp(max=self.K2).contiguous()
         est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
         self._est, self._sd = est, sd
         ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
@@ -260,8 +295,9 @@ class EngineI8:
         qp = _lib.query_prep(Qb, self.Vr, self.s1["c"], zq)
         q8, qs, QC, Qh, _ = qp
         if QM is None:
-            QM = Qh @ self.meansN.T
-        probe = _lib.route_topk(QM, nprobe)
+            QM = self._plain_qm(Qh)
+        # the reference's fallback routes without PROJ or ROUTE16 (throughput/enginei8.py:110-112)
+        probe = _lib.route_topk(QM, nprobe) if self.NROUTE else _lib.route_topk_scaled(QM, self.s1["inv_mnorm"], nprobe)
         if Zq is None:
             Zq = s2lut.rotate(self.code, Qh)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, rho_override=1.0, M_override=65536, qp=qp, delta=None)
@@ -274,16 +310,23 @@ class EngineI8:
         Qb = Qb.float().contiguous()
         qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
         q8, qs, QC, Qh, zq = qp
-        QM, probe = self._route(Qh, nprobe)
+        QM, probe = self._route(Qh, QC, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         half = self.LUTF and self.LUTH
         ncnt = self._ncnt if self.DELTA is not None else None
         Zq = s2lut.rotate(self.code, Qh)
         pre = _lib.lut_build(Zq, self.code["TS"], half)
+        pos1 = pos
+        if self.K2 is not None and self.K2 < K:
+            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None)
+            cntK = torch.full((pos.shape[0],), K, dtype=torch.int32, device=pos.device)
+            pos = _lib.select(e_all.contiguous(), pos.contiguous(), cntK, self.K2, 0, None)[0]
+            if ncnt is not None:
+                ncnt = ncnt.clamp(max=self.K2).contiguous()
         est, sd = s2lut.score_lut(self.code, QC, pos, pre, ncnt)
         ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
         return dict(q8=q8, qs=qs, QC=QC, Qh=Qh, z=zq, QM=QM, probe=probe, bm=self._bm, n1=self._n1, M=self._M,
-                    t0=self._t0, cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, est1=self._est1, ok=ok,
+                    t0=self._t0, cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, pos1=pos1, est1=self._est1, ok=ok,
                     ncnt=self._ncnt, Zq=Zq, L=pre[0], qsum=pre[1], qn2=pre[2], est=est, sd=sd, ids=ids, I=I,
                     scores=scores, reads=reads)
 

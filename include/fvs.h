@@ -378,6 +378,16 @@ int fvs_route_topk_scaled(const uint16_t *QM, const float *scale, const float *q
                           int32_t nprobe, int32_t *probe, void *stream);
 
 /*
+ * fp16 routing keys of EngineI8's routing variants (throughput/enginei8.py:72-76):
+ * out[q][c] = fp16(((float)QM[q][c] + qadd[q]) * scale[c]) (nearest, ties to even), where the add is left out
+ * when qadd is NULL and the product when scale is NULL. ROUTE16 without NROUTE: scale = inv_mnorm, qadd = NULL
+ * ((QM.float() * inv_mnorm).half()); PROJ: scale = NULL, qadd = QC ((QC[:, None] + P.float()).half()).
+ * QM, out fp16 [B, NC]; scale f32 [NC]; qadd f32 [B].
+ */
+int fvs_route_keys(const uint16_t *QM, const float *scale, const float *qadd, int64_t B, int32_t NC, uint16_t *out,
+                   void *stream);
+
+/*
  * Lloyd-Max tiered stage 2 (a23). Replaces tiered_fused.score / _tiered_score_rec (src/tiered_fused.py:47-141).
  *   pos i32 [B, K]; qc f32 [B] = <q, c>; Zq f32 [B, D] = Qb @ VP (fp32); rec u8 [N, RB] packed records;
  *   tiers i32 [T][3] (start, end, bits) and toff i32 [T] are HOST arrays; cb f32 [T, 256]: tier t's levels

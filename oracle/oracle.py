@@ -355,6 +355,7 @@ def index_from_tables(s1, code, Z, zs, Vr, H):
     mnorm = (1.0 / s1["inv_mnorm"]).float()
     return dict(order=t(s1["order"]).astype(np.int32), off=np.asarray(s1["off"]).astype(np.int32),
                 meansN=t(meansN).view(np.uint16), mnorm=t(mnorm), c=t(s1["c"]).astype(np.float32),
+                means16=t(s1["means16"]).view(np.uint16), inv_mnorm=t(s1["inv_mnorm"]).astype(np.float32),
                 Vr=t(Vr).astype(np.float32), Z=t(Z), zs=t(zs), TS=list(TS),
                 deltas=np.array([code["deltas"][b] for _, _, b in TS], np.float32),
                 toff=np.array(code["toff"], np.int32), soff=int(code["soff"]), rec=t(code["rec"]),
@@ -367,15 +368,34 @@ def stage1(idx, q8, qs, QM16, probe, K, knobs, rho_override=None, M_override=Non
     M, n1, r = params(K, probe.shape[1], N, NC, MSZ=knobs.get("MSZ", 3072), BETA=knobs.get("BETA"),
                       RHO=knobs.get("RHO", 0.6), rho_override=rho_override, M_override=M_override)
     MB = static_blocks(idx["off"])[4]
-    bm = first_pass(q8, qs, probe[:, :n1], n1, idx["off"], idx["Z"], idx["zs"], QM16, idx["mnorm"], MB)
+    # NROUTE scores against normalised means: pair constants scaled back by |m_c|; otherwise QM as is
+    # (throughput/enginei8.py:47-48)
+    mn = idx["mnorm"] if knobs.get("NROUTE", True) else None
+    bm = first_pass(q8, qs, probe[:, :n1], n1, idx["off"], idx["Z"], idx["zs"], QM16, mn, MB)
     t0 = threshold(bm, probe, idx["off"], n1, MB, r)
-    cnt, bval, bpos = emit(q8, qs, probe, idx["off"], idx["Z"], idx["zs"], QM16, idx["mnorm"], t0, M)
+    cnt, bval, bpos = emit(q8, qs, probe, idx["off"], idx["Z"], idx["zs"], QM16, mn, t0, M)
     pos, est1, ok, ncnt = select(bval, bpos, cnt, K, min(kd, K - 1), delta)
     return dict(n1=n1, r=r, M=M, MB=MB, bm=bm, t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos, est1=est1, ok=ok,
                 ncnt=ncnt)
 
 
-def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None, fallback=True):
+def route(idx, QM16, nprobe, knobs):
+    """Probe lists of EngineI8's routing variants (throughput/enginei8.py:66-76): NROUTE ranks QM (normalised
+    means) directly; otherwise the key is (float)QM * inv_mnorm, rounded to fp16 when ROUTE16; UNSORTED
+    lists the chosen cells in cell order."""
+    if knobs.get("NROUTE", True):
+        probe = route_topk(QM16, nprobe)
+    elif knobs.get("ROUTE16", True):
+        keys = (np.asarray(QM16).view(np.float16).astype(np.float32) * idx["inv_mnorm"][None, :]).astype(np.float16)
+        probe = route_topk(keys.view(np.uint16), nprobe)
+    else:
+        probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe)
+    if knobs.get("UNSORTED", False):
+        probe = np.sort(probe, axis=1)
+    return probe
+
+
+def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None, fallback=True, QMfb16=None):
     """Every intermediate of one batch (EngineI8._gpu + _fallback). zq (f32), QM16 / Zq16 (fp16 as uint16)
     are the three BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs,
     otherwise computed here with sequential fp32 accumulation."""
@@ -386,22 +406,35 @@ def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None,
         zq = project(Q, idx["Vr"])
     q8, qs, qc, qh = query_prep(Q, idx["Vr"], idx["c"], zq)
     D = idx["TS"][-1][1]
+    nroute = knobs.get("NROUTE", True)
     if QM16 is None:
-        QM16 = fp16_gemm_nt(qh, idx["meansN"])
+        QM16 = fp16_gemm_nt(qh, idx["meansN"] if nroute else idx["means16"])
     if Zq16 is None:
         Zq16 = fp16_gemm_nn(qh, np.ascontiguousarray(idx["VP16"][:, :D]))
-    probe = route_topk(QM16, nprobe)
+    probe = route(idx, QM16, nprobe, knobs)
     s1 = stage1(idx, q8, qs, QM16, probe, K, knobs, delta=delta, kd=k - 1)
     L, qsum, qn2 = lut_build(Zq16, idx["TS"], half)
-    est, sd = lut_score(s1["pos"], qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
-                        idx["toff"], s1["ncnt"] if delta is not None else None)
-    ids, I, scores, reads = refine(est, sd, s1["pos"], idx["order"], idx["H"], Q, z, k)
+    pos, ncnt = s1["pos"], (s1["ncnt"] if delta is not None else None)
+    K2 = knobs.get("K2")
+    if K2 is not None and K2 < K:  # progressive stage 2 (throughput/enginei8.py:82-85)
+        e_all, _ = lut_score(pos, qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
+                             idx["toff"], None)
+        pos = select(e_all, pos, np.full(len(pos), K, np.int32), K2, 0, None)[0]
+        if ncnt is not None:
+            ncnt = np.minimum(ncnt, K2).astype(np.int32)
+    s1["pos2"] = pos
+    est, sd = lut_score(pos, qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
+                        idx["toff"], ncnt)
+    ids, I, scores, reads = refine(est, sd, pos, idx["order"], idx["H"], Q, z, k)
     out = dict(z=zq, q8=q8, qs=qs, qc=qc, qh=qh, QM=QM16, Zq=Zq16, probe=probe, L=L, qsum=qsum, qn2=qn2, est=est, sd=sd,
                ids=ids, I=I.copy(), scores=scores.copy(), reads=reads.copy(), cand=ids.copy(), **s1)
     bad = np.nonzero(s1["ok"] == 0)[0]
     out["bad"] = bad
     if fallback and len(bad):
-        f1 = stage1(idx, q8[bad], qs[bad], QM16[bad], probe[bad], K, knobs, rho_override=1.0, M_override=65536,
+        # the reference's fallback routes on the plain QM with fp32 keys, sorted (throughput/enginei8.py:110-112)
+        QMf = np.asarray(QM16 if QMfb16 is None else QMfb16)[bad]
+        pf = route(idx, QMf, nprobe, dict(NROUTE=nroute, ROUTE16=False))
+        f1 = stage1(idx, q8[bad], qs[bad], QMf, pf, K, knobs, rho_override=1.0, M_override=65536,
                     delta=None)
         Lf, qsf, qnf = lut_build(Zq16[bad], idx["TS"], False)
         estf, sdf = lut_score(f1["pos"], qc[bad], Lf, False, qsf, qnf, idx["rec"], idx["soff"], idx["TS"],

@@ -1,0 +1,79 @@
+"""EngineI8's routing and stage-2 knobs on the GPU against the oracle (throughput/enginei8.py:66-86): routing
+without NROUTE (fp16 or fp32 keys), UNSORTED probe order, PROJ routing over a trellis stage-1 basis, and the
+progressive stage 2 (K2). The BLAS products are shared inputs as in test_gpu_parity.py; every other result
+is bit-exact: probe lists, thresholds, counts, the stage-1 and K2 candidate lists, the stage-2 estimates
+and the final ids. The search path (graph replay and fallback) must give the eager trace's ids."""
+import numpy as np
+import pytest
+import torch
+
+from fanarvse_paper_amd import datagen, index, metrics, trellis
+from fanarvse_paper_amd.enginei8 import EngineI8
+
+pytestmark = pytest.mark.gpu
+
+K, Z_, NPROBE, KK = 175, 1.25, 24, 10
+
+
+def u16(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+def npy(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def env(oracle_mod):
+    print("\n[gpu knobs] building N=30000 d=768 NC=128 index on cuda:0", flush=True)
+    dev = "cuda"
+    X = datagen.gen(30000, 768, 64, 0.7, seed=0, device=dev)
+    Q = datagen.gen(192, 768, 64, 0.7, seed=1, device=dev, dtype=torch.float32)
+    s1, code, Z, zs, Vr = index.build_index(X, nlist=128)
+    s1["W1"] = trellis.rotation_basis(X, s1["c"], 256)  # the stage-1 basis PROJ projects through
+    idx = oracle_mod.index_from_tables(s1, code, Z, zs, Vr, X)
+    GT = npy(datagen.ground_truth(X, Q, 10))
+    return dict(X=X, Q=Q, s1=s1, code=code, Z=Z, zs=zs, Vr=Vr, idx=idx, GT=GT)
+
+
+CASES = {
+    "route16": dict(NROUTE=False, ROUTE16=True),
+    "route32_unsorted": dict(NROUTE=False, ROUTE16=False, UNSORTED=True),
+    "proj": dict(NROUTE=False, PROJ=True),
+    "k2": dict(K2=100),
+    "sortroute": dict(SORTROUTE=True),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_knob_matches_oracle(env, oracle_mod, case):
+    print(f"\n[gpu knobs] {case}", flush=True)
+    knobs = CASES[case]
+    E = EngineI8(env["s1"], env["code"], env["Z"], env["zs"], env["Vr"], H=env["X"])
+    for k_, v in knobs.items():
+        setattr(E, k_, v)
+    Q = env["Q"]
+    tr = E.trace(Q, K, Z_, NPROBE, KK)
+    torch.cuda.synchronize()
+    ok_knobs = dict(MSZ=E.MSZ, RHO=E.RHO, BETA=E.BETA, DELTA=E.DELTA, LUTF=E.LUTF, LUTH=E.LUTH, NROUTE=E.NROUTE,
+                    ROUTE16=E.ROUTE16, UNSORTED=E.UNSORTED, K2=E.K2)
+    out = oracle_mod.pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, knobs=ok_knobs, QM16=u16(tr["QM"]),
+                              Zq16=u16(tr["Zq"]), zq=npy(tr["z"]), fallback=False)
+    assert np.array_equal(npy(tr["probe"]), out["probe"])
+    if case == "route32_unsorted":
+        assert np.all(np.diff(out["probe"], axis=1) > 0)
+    assert np.array_equal(npy(tr["t0"]).view(np.uint32), out["t0"].view(np.uint32))
+    assert np.array_equal(npy(tr["cnt"]), out["cnt"])
+    ok = out["ok"] == 1
+    assert ok.mean() > 0.5
+    assert np.array_equal(npy(tr["pos1"])[ok], out["pos"][ok])
+    assert np.array_equal(npy(tr["pos"])[ok], out["pos2"][ok])
+    assert np.array_equal(npy(tr["est"])[ok].view(np.uint32), out["est"][ok].view(np.uint32))
+    assert np.array_equal(npy(tr["I"])[ok], out["I"][ok])
+    assert np.array_equal(npy(tr["reads"])[ok], out["reads"][ok])
+    if case == "k2":
+        assert tr["pos"].shape[1] == 100 and tr["pos1"].shape[1] == K
+    # the captured search gives the eager ids (the flagged queries go through the fallback)
+    I, reads, ids = E.search(Q, K, Z_, NPROBE, KK)
+    assert np.array_equal(npy(I)[ok], npy(tr["I"])[ok])
+    assert metrics.recall(npy(I), env["GT"]) >= 0.9

@@ -228,3 +228,27 @@ def test_route_topk_ties_and_signed_zero(oracle_mod):
     probe = oracle_mod.route_topk(fp16_bits(vals), 6)
     want = sorted(range(8), key=lambda c: (-float(vals[0, c]), c))[:6]
     assert probe[0].tolist() == want == [0, 2, 6, 3, 7, 1]
+
+
+def test_routing_variants_brute_force(oracle_mod):
+    """The oracle's routing variants (throughput/enginei8.py:66-76) against a numpy sort by (key desc,
+    cell asc): fp16 keys of (float)QM * inv_mnorm (ROUTE16), fp32 keys, and the cell-ordered UNSORTED list."""
+    rng = np.random.default_rng(11)
+    B, NC, npr = 40, 96, 17
+    QM = (rng.standard_normal((B, NC)) * 0.3).astype(np.float16)
+    QM[3, :20] = QM[3, 20]                       # ties
+    inv = (1.0 / (0.5 + rng.random(NC))).astype(np.float32)
+    inv[5] = inv[6]
+    idx = dict(inv_mnorm=inv)
+
+    def brute(keys):
+        return np.stack([np.lexsort((np.arange(NC), -keys[b]))[:npr] for b in range(B)]).astype(np.int32)
+
+    k16 = (QM.astype(np.float32) * inv[None, :]).astype(np.float16).astype(np.float32)
+    k32 = QM.astype(np.float32) * inv[None, :]
+    p16 = oracle_mod.route(idx, QM.view(np.uint16), npr, dict(NROUTE=False, ROUTE16=True))
+    p32 = oracle_mod.route(idx, QM.view(np.uint16), npr, dict(NROUTE=False, ROUTE16=False))
+    pu = oracle_mod.route(idx, QM.view(np.uint16), npr, dict(NROUTE=False, ROUTE16=False, UNSORTED=True))
+    assert np.array_equal(p16, brute(k16)) and np.array_equal(p32, brute(k32))
+    assert np.array_equal(pu, np.sort(brute(k32), axis=1))
+    assert not np.array_equal(p16, p32)          # the fp16 rounding changes some lists
