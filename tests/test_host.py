@@ -50,16 +50,23 @@ def test_row_chunks_cover_every_row_once():
     assert items[4] == 1 and items[5] == 2 and items[6] == 2
 
 
-def test_unimplemented_knobs_raise():
+def test_proj_knob_needs_stage1_basis():
+    """PROJ routing (NROUTE off) projects through s1["W1"]: without it the engine refuses before any work;
+    the other knobs need no extra table."""
     from fanarvse_paper_amd.enginei8 import EngineI8
 
     E = EngineI8.__new__(EngineI8)
-    for attr, val in (("PROJ", True), ("K2", 100), ("NROUTE", False)):
+    E.s1 = {}
+    E.NROUTE, E.PROJ = False, True
+    with pytest.raises(ValueError):
+        E._check_knobs()
+    E.s1 = {"W1": None}
+    E._check_knobs()
+    for attr, val in (("K2", 100), ("NROUTE", False), ("UNSORTED", True), ("SORTROUTE", True)):
         E2 = EngineI8.__new__(EngineI8)
+        E2.s1 = {}
         setattr(E2, attr, val)
-        with pytest.raises(NotImplementedError):
-            E2._check_knobs()
-    E._check_knobs()  # the default operating point is implemented
+        E2._check_knobs()
 
 
 def test_record_layout_of_the_paper_tiers():
