@@ -108,9 +108,9 @@ __global__ __launch_bounds__(256, kWGCU) void k_dense_scan(const int8_t *__restr
   const int8_t *rsrc[3] = {Qt, Qt, Qt};
   auto request = [&](v4i (&L)[kBR][kSS][64]) {
     if (rk >= my_tiles) return;
-    const int tile = (rk * 8 + x) * m8 + m;
-    const int tq = (int)((unsigned)tile % (unsigned)ntq), tn = (int)((unsigned)tile / (unsigned)ntq);
-    if (rst == 0) {
+    if (rst == 0) {  // a new tile: its coordinates (one division per tile, not per stage) and operand bases
+      const int tile = (rk * 8 + x) * m8 + m;
+      const int tq = (int)((unsigned)tile % (unsigned)ntq), tn = (int)((unsigned)tile / (unsigned)ntq);
 #pragma unroll
       for (int r = 0; r < 3; r++) {
         const int br = 3 * w + r;
@@ -128,6 +128,8 @@ __global__ __launch_bounds__(256, kWGCU) void k_dense_scan(const int8_t *__restr
       __builtin_amdgcn_global_load_lds(src, dst, 16, 1024, 0);
     }
     if (rst == 0) {
+      const int tile = (rk * 8 + x) * m8 + m;
+      const int tq = (int)((unsigned)tile % (unsigned)ntq), tn = (int)((unsigned)tile / (unsigned)ntq);
       if (w < 2) {  // rows 128 w .. 128 w + 127: 4 bytes (two fp16) per lane
         const char *src = reinterpret_cast<const char *>(zs16 + (size_t)tn * kNT + 128 * w) + 4 * lane;
         __builtin_amdgcn_global_load_lds(src, (lds_ptr)&zsl[rpar][128 * w], 4, 0, 0);
@@ -298,6 +300,56 @@ __global__ __launch_bounds__(256) void k_row_kth(const float *__restrict__ S, in
   }
 }
 
+// The same selection for rows of at most 64 K values: one 1024-thread block per query loads the row once
+// into registers (64 ordered keys per thread) and runs the four 8-bit radix passes over them, with one
+// histogram per wave in LDS (fewer collisions on the busy bins), instead of re-reading the row from
+// memory in every pass.
+constexpr int kKthNT = 1024, kKthPer = 64;
+
+__global__ __launch_bounds__(kKthNT) void k_row_kth_reg(const float *__restrict__ S, int n, int r,
+                                                        float *__restrict__ t0, int32_t *__restrict__ cnt) {
+  constexpr int NW = kKthNT / 64;
+  __shared__ int hist[NW][256];
+  __shared__ int tot[256];
+  __shared__ int sh[fvs_sh_ints(kKthNT)];
+  const int tid = threadIdx.x, w = fvs_wave_id();
+  const int64_t q = blockIdx.x;
+  const float *row = S + q * (int64_t)n;
+  uint32_t key[kKthPer];
+#pragma unroll
+  for (int j = 0; j < kKthPer; j++) {
+    const int i = j * kKthNT + tid;
+    key[j] = i < n ? fvs_ord32(row[i]) : 0u;
+  }
+  uint32_t prefix = 0, pmask = 0;
+  int k = r;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < NW * 256; i += kKthNT) (&hist[0][0])[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kKthPer; j++)
+      if (j * kKthNT + tid < n && (key[j] & pmask) == prefix) atomicAdd(&hist[w][(key[j] >> shift) & 0xff], 1);
+    __syncthreads();
+    if (tid < 256) {
+      int t = 0;
+#pragma unroll
+      for (int v = 0; v < NW; v++) t += hist[v][tid];
+      tot[tid] = t;
+    }
+    __syncthreads();
+    if (w == 0) fvs_pick_bucket<NW>(tot, sh, k);
+    __syncthreads();
+    prefix |= (uint32_t)sh[NW] << shift;
+    pmask |= 0xffu << shift;
+    k = sh[NW + 1];
+    __syncthreads();  // every thread has read sh before the next pass's bucket choice rewrites it
+  }
+  if (tid == 0) {
+    t0[q] = fvs_unord32(prefix);
+    if (cnt) cnt[q] = 0;
+  }
+}
+
 // int8 code of each row of z [n, R] (f32): scale = max(max_j |z[j]|, 1e-12f) / 127, code = clamp(rint(z / scale),
 // -127, 127), the rule of throughput/brute.py:39-41 and :46-48 for any R. One wave per row.
 __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ z, int64_t n, int R, int8_t *__restrict__ q,
@@ -338,7 +390,10 @@ extern "C" int fvs_dense_threshold(const float *S, int64_t B, int32_t n, int32_t
   if (B < 0 || n <= 0 || r <= 0 || r > n) return FVS_E_ARG;
   if (B == 0) return FVS_OK;
   if (!S || !t0) return FVS_E_ARG;
-  hipLaunchKernelGGL(k_row_kth, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, S, (int)n, (int)r, t0, cnt);
+  if (n <= kKthNT * kKthPer)
+    hipLaunchKernelGGL(k_row_kth_reg, dim3((unsigned)B), dim3(kKthNT), 0, (hipStream_t)stream, S, (int)n, (int)r, t0, cnt);
+  else
+    hipLaunchKernelGGL(k_row_kth, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, S, (int)n, (int)r, t0, cnt);
   return fvs_launch_status();
 }
 

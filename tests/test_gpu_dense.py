@@ -124,12 +124,18 @@ def test_emit_overflow_keeps_cap_valid_pairs(oracle_mod):
         assert np.array_equal(bv[i], S[i, bp[i]]) and np.all(bv[i] >= t0[i])
 
 
-def test_threshold_matches_oracle(oracle_mod):
-    print("\n[gpu dense] threshold B=300 n=5000", flush=True)
-    S = torch.randn(300, 5000, generator=torch.Generator().manual_seed(5))
+@pytest.mark.parametrize("B,n", [(300, 5000), (40, 65536), (20, 70000)])
+def test_threshold_matches_oracle(B, n, oracle_mod):
+    """Rows of up to 64 K values take the register-resident selection, longer ones the streaming one."""
+    print(f"\n[gpu dense] threshold B={B} n={n}", flush=True)
+    S = torch.randn(B, n, generator=torch.Generator().manual_seed(5))
     S[3, :100] = S[3, 100]          # ties
-    cnt = torch.full((300,), 9, dtype=torch.int32, device=dev)
-    for r in (1, 40, 5000):
+    S[4] = 0.25                     # a constant row
+    S[5, ::2] = -S[5, 1::2]         # +-x pairs, -0 and +0 included below
+    S[6, :10] = -0.0
+    S[6, 10:20] = 0.0
+    cnt = torch.full((B,), 9, dtype=torch.int32, device=dev)
+    for r in (1, 40, n):
         t0 = _lib.dense_threshold(S.to(dev), r, cnt)
         assert np.array_equal(npy(t0), oracle_mod.row_kth(S.numpy(), r))
         assert not cnt.any()
