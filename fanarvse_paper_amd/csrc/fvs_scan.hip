@@ -1,96 +1,79 @@
-// int8 stage-1 scan on gfx950 MFMA (v_mfma_i32_32x32x32_i8).
+// int8 stage-1 scans on gfx950 MFMA (v_mfma_i32_32x32x32_i8): the first pass (block maxima) and the
+// threshold-and-emit pass.
 //
 // Work item = (cell, up to 256 consecutive rows of it from a first row r0); its 32-row blocks start at
 // r0, r0 + 32, ... The first pass needs the reference's global 32-row blocks (its block maxima are per
 // global block), so its items start on a multiple of 32; the emit pass, whose output does not depend on
 // the grouping, takes items that start at the cell's first row (a cell of up to 256 rows is one item,
 // with no block straddling the cell start). A 4-wave workgroup runs an item; wave w keeps blocks 2w and
-// 2w+1 (64 code rows) as MFMA A operands in registers for the whole item, so each code byte is read from
-// HBM once per pass. The cell's queries stream through as B operands in tiles of 32:
+// 2w+1 (64 code rows) as MFMA operands in registers for the whole item, so each code byte is read from
+// HBM once per pass. The cell's queries stream through in tiles of 32:
 //   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the row
 //     scales of its 256 rows are staged in LDS up front (kMeta pairs at a time);
-//   * a tile's B fragments (its 32 query codes, 8 KB) are written straight into LDS by the vector memory
+//   * a tile's fragments (its 32 query codes, 8 KB) are written straight into LDS by the vector memory
 //     unit (global_load_lds, no registers), in MFMA-step order so that every fragment read is one
 //     contiguous 1 KB ds_read_b128 per wave. The buffer is double-buffered and shared by the four waves:
 //     each wave requests a quarter of tile t + 1 while tile t is computed, and one barrier per tile
 //     publishes it.
-// Two blocks per wave halve the B-fragment reads per MFMA. 168 VGPRs and 52 KB of LDS give three resident
-// workgroups per CU. Both passes are persistent: a workgroup loops over items (grid = resident
-// workgroups), and the next item's pair ids, row scales and code blocks are requested as soon as the
-// current item's tile loop is done, under its flush.
+// Two blocks per wave halve the fragment reads per MFMA. Both passes are persistent: a workgroup loops
+// over items (grid = resident workgroups), and the next item's pair ids, row scales and code blocks are
+// requested as soon as the current item's tile loop is done.
 //
 // Operand layout: lane l holds row/column (l & 31) and, for MFMA step s (k-block of 32 bytes), the
-// 16 bytes at 32*s + 16*(l >> 5); A and B use the same assignment, so the contraction is exact for
-// any internal k order. Accumulator layout (32x32): lane l, element v holds row
-// 8*(v/4) + 4*(l/32) + (v%4) and column (query) l%32, so each lane owns one query and 16 rows of a
-// block; the epilogue needs only per-lane scalars for the query.
+// 16 bytes at 32*s + 16*(l >> 5); both operands use the same assignment, so the contraction is exact for
+// any internal k order. Accumulator layout (32x32, D = A x B): lane l, element v holds row
+// 8*(v/4) + 4*(l/32) + (v%4) of A and column l%32 of B.
 //
 // The item's row scales sit in LDS; rows outside the cell get a NaN scale: their estimate is NaN,
 // which never passes `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
-//
-// Emit: for each accumulator element the wave takes a ballot of `est >= t0` (the compare's own lane
-// mask). An empty ballot costs a scalar branch; otherwise the passing lanes, under the exec mask, take
-// consecutive slots of the wave's own LDS region (a wave-uniform counter, no atomics, the overflow test
-// scalar). If a wave's region overflows, the item's staged candidates are dropped and the item is redone
-// on the direct path (one global atomic per candidate), which is also the path of cells probed by more
-// than kMeta queries. At the end of the item every staged candidate takes its number among its pair's
-// candidates with an LDS atomic, one global atomic per (item, query) reserves the query's buffer range,
-// and every candidate is written out at base + number, with no per-candidate global atomics.
+#include <type_traits>
+
 #include "fvs_common.h"
 
 namespace {
 
 constexpr int kR = 256;
-constexpr int kNB = 2;       // 32-row blocks per wave
-constexpr int kCB = 4 * kNB; // 32-row blocks per work item
-constexpr int kMeta = 512;   // pairs staged in LDS at a time
-constexpr int kCap = 768;    // LDS candidate slots per wave
-constexpr bool kPersistEmit = true;  // the emit pass loops over items like the first pass
+constexpr int kNB = 2;          // 32-row blocks per wave
+constexpr int kCB = 4 * kNB;    // 32-row blocks per work item
+constexpr int kMeta = 512;      // pairs staged in LDS at a time
+constexpr int kEmitWaves = 4;   // waves per emit workgroup
+constexpr int kCapE = 1536;     // LDS candidate slots per wave of the emit pass
 
+// row of accumulator element v in the 32x32 layout, for lanes of half h = l / 32
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
 struct Meta {  // one (query, cell) pair of the item
   int qid;     // query
   float qs;    // query code scale
   float qcp;   // centre term of the pair
-  float x;     // mode 1: threshold t0 of the query; mode 0: probe rank (int bits)
+  float x;     // emit pass: threshold t0 of the query; first pass: probe rank (int bits)
 };
 
-struct EmitLds {
-  float est[4][kCap];
-  uint32_t tag[4][kCap];  // row - first row of the item (bits 0-7) | pair index in the cell (8-19) | number (20-31)
-  uint32_t lcnt[kMeta];   // candidates of each pair in the item; then the pair's base in its query's buffer
-  int n[4];
-};
-
-template <int MODE>
-__global__ __launch_bounds__(256, 3) void k_i8_scan(
+// ------------------------------------------------------------------ the first pass (mode 0)
+// The code rows are the A operand and the queries the B operand, so each lane owns one query (column
+// l % 32) and 16 rows of a block; the epilogue needs only per-lane scalars for the query:
+//   bm[(q * n1 + qrank[pair]) * MB + blk - cs/32] = max over the block's rows of
+//   fmaf((float)acc * qs, zs, qcp).
+// Three workgroups per CU (at most 168 VGPRs, 25 KB of LDS).
+__global__ __launch_bounds__(256, 3) void k_i8_first(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
     const int32_t *__restrict__ pcell, const int32_t *__restrict__ prow, const int32_t *__restrict__ ps,
     const int32_t *__restrict__ pe, int P, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
-    const float *__restrict__ qcp, const float *__restrict__ t0, int32_t *__restrict__ cnt,
-    float *__restrict__ bval, int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
+    const float *__restrict__ qcp, float *__restrict__ bm, int MB, int n1) {
   __shared__ __align__(16) Meta meta[kMeta];
   __shared__ __align__(16) float zsl[32 * kCB];
-  __shared__ __align__(16) v4i bsh[2][8 * 64];  // B tiles, double-buffered: [step s][half h][query li], 16 B each
-  EmitLds *E = nullptr;
-  if constexpr (MODE == 1) {
-    __shared__ EmitLds Es;
-    E = &Es;
-  }
+  __shared__ __align__(16) v4i bsh[2][8 * 64];  // query tiles, double-buffered: [step s][half h][query li], 16 B each
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = fvs_wave_id();
   const int h = lane >> 5, li = lane & 31;
 
-  // Items p = blockIdx.x, blockIdx.x + gridDim.x, ...: right after an item's tile loop the next item's
-  // pair ids, row scales and code blocks are requested, so their latency runs under the flush.
   struct Item {
-    int p, c, qn, qoff, r0, cs, ce;  // r0: first row of the item
+    int c, qn, qoff, r0, cs, ce;  // r0: first row of the item
   };
   auto item_at = [&](int p) {
-    Item it{p, 0, 0, 0, 0, 0, 0};
+    Item it{0, 0, 0, 0, 0, 0};
     if (p < P) {
       it.c = pcell[p];
       it.r0 = prow[p];
@@ -102,7 +85,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     return it;
   };
   int pq[kMeta / 256];  // pair ids of the item's first chunk
-  float zr = 0.f;       // this thread's row scale of the item (thread < 32 * kCB)
+  float zr = 0.f;       // this thread's row scale of the item
   v4i a[kNB][8];        // this wave's blocks: the A operands
   auto prefetch = [&](const Item &it) {
     if (it.qn == 0) return;
@@ -111,7 +94,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
       const int j = tid + 256 * i;
       pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
     }
-    if (tid < 32 * kCB) {
+    {
       const int r = it.r0 + tid;
       zr = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
     }
@@ -126,229 +109,481 @@ __global__ __launch_bounds__(256, 3) void k_i8_scan(
     }
   };
 
-  // Both passes loop over items (grid = resident workgroups, stride = grid): once an item's tile loop is
-  // done (and the emit pass knows its regions did not overflow), the next item's pair ids, row scales and
-  // code blocks are requested, so their latency runs under the flush.
-  constexpr bool persist = MODE == 0 || kPersistEmit;
-  const int stride = persist ? (int)gridDim.x : P;
+  const int stride = (int)gridDim.x;
   int p = blockIdx.x;
   Item cur = item_at(p);
-  if constexpr (!persist) {
-    if (cur.qn == 0) return;
-  }
   prefetch(cur);
   while (p < P) {
-    const Item nxt = persist ? item_at(p + stride) : Item{P, 0, 0, 0, 0, 0, 0};
+    const Item nxt = item_at(p + stride);
     if (cur.qn == 0) {
-      if constexpr (persist) prefetch(nxt);
+      prefetch(nxt);
       cur = nxt;
       p += stride;
       continue;
     }
     const int qn = cur.qn, qoff = cur.qoff, cs = cur.cs;
-    const bool staged = MODE == 1 && qn <= kMeta;  // one pair chunk: meta holds the pairs until the flush
     const int row0 = cur.r0;  // first row of the item
-    if (tid < 32 * kCB) zsl[tid] = zr;
+    zsl[tid] = zr;
     bool act[kNB];
 #pragma unroll
     for (int u = 0; u < kNB; u++) act[u] = row0 + 32 * (kNB * w + u) < cur.ce;
     const bool any = act[0];
-    int ebase = 0;  // wave-uniform: used slots of this wave's emit region (may exceed kCap: overflow)
-    if constexpr (MODE == 1) {
-      if (staged)
-        for (int j = tid; j < qn; j += 256) E->lcnt[j] = 0u;
-    }
-
-    auto scan = [&](const bool direct, bool first) {
-      for (int c0 = 0; c0 < qn; c0 += kMeta) {
-        const int nq = min(kMeta, qn - c0);
-        if (c0 > 0 || !first) {
-#pragma unroll
-          for (int i = 0; i < kMeta / 256; i++) {
-            const int j = tid + 256 * i;
-            pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
-          }
-        }
+    for (int c0 = 0; c0 < qn; c0 += kMeta) {
+      const int nq = min(kMeta, qn - c0);
+      if (c0 > 0) {
 #pragma unroll
         for (int i = 0; i < kMeta / 256; i++) {
           const int j = tid + 256 * i;
-          if (j < nq) {
-            const int pidx = qoff + c0 + j;
-            const int q = pq[i];
-            Meta m;
-            m.qid = q;
-            m.qs = qs[q];
-            m.qcp = qcp[pidx];
-            m.x = MODE == 0 ? __int_as_float(qrank[pidx]) : t0[q];
-            meta[j] = m;
+          pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kMeta / 256; i++) {
+        const int j = tid + 256 * i;
+        if (j < nq) {
+          const int pidx = qoff + c0 + j;
+          const int q = pq[i];
+          Meta m;
+          m.qid = q;
+          m.qs = qs[q];
+          m.qcp = qcp[pidx];
+          m.x = __int_as_float(qrank[pidx]);
+          meta[j] = m;
+        }
+      }
+      __syncthreads();
+      const int ntiles = (nq + 31) / 32;
+      // tile t: the fragments of its 32 queries in MFMA step order, written straight into LDS; wave w
+      // requests steps 2w and 2w + 1 of tile t + 1 while tile t is computed
+      auto request = [&](int tile) {
+        const int jr = min(tile * 32 + li, nq - 1);
+        const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const int s = 2 * w + k;
+          __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&bsh[tile & 1][s * 64],
+                                           16, 0, 0);
+        }
+      };
+      auto published = [&]() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's requests have landed in LDS
+        __syncthreads();
+      };
+      auto compute = [&](int t) {
+        v4i b[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) b[s] = bsh[t & 1][s * 64 + lane];
+        v16i acc[kNB];
+#pragma unroll
+        for (int u = 0; u < kNB; u++) {
+          acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+          if (act[u]) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
           }
         }
-        __syncthreads();
-
-        const int ntiles = (nq + 31) / 32;
-        // B tile t: the fragments of the tile's 32 queries in MFMA step order, written straight into LDS by
-        // the vector memory unit (global_load_lds, 16 B per lane at base + 16 * lane). Wave w requests steps
-        // 2w and 2w + 1 of tile t + 1 while tile t is computed; one barrier per tile publishes it.
-        auto request = [&](int tile) {
-          const int jr = min(tile * 32 + li, nq - 1);
-          const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
+        const int jl = t * 32 + li;  // pair index inside the chunk
+        const bool valid = jl < nq;
+        const Meta m = meta[valid ? jl : nq - 1];
 #pragma unroll
-          for (int k = 0; k < 2; k++) {
-            const int s = 2 * w + k;
-            __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&bsh[tile & 1][s * 64],
-                                             16, 0, 0);
+        for (int u = 0; u < kNB; u++) {
+          if (!act[u]) continue;
+          float mx = -1e30f;
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
+            const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp));
           }
-        };
-        auto published = [&]() {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's requests have landed in LDS
-          __syncthreads();
-        };
-        {
-          auto compute = [&](int t) {
-            v4i b[8];
+          mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
+          if (h == 0 && valid)
+            bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + kNB * w + u - (cs >> 5))] = mx;
+        }
+      };
+      request(0);
+      published();
+      for (int t = 0; t < ntiles; t++) {
+        if (t + 1 < ntiles) request(t + 1);  // the other buffer: every wave has left tile t - 1
+        if (any) compute(t);
+        published();
+      }
+    }
+    prefetch(nxt);
+    cur = nxt;
+    p += stride;
+  }
+}
+
+// ------------------------------------------------------------------ the emit pass (mode 1)
+// Same items, waves and LDS query tiles as the first pass, with the MFMA operands swapped: the tile's 32
+// queries are the A operand and the wave's code rows the B operand, so lane l holds code row l % 32 of the
+// block and element v the query 8*(v/4) + 4*(l/32) + (v%4) of the tile. A wave ballot of one element then
+// covers two (query, 32-row block) pairs, and since the rows that pass for a query come in clusters, most
+// ballots are empty (about 9 %, against 44 % with one query per lane).
+//
+// Per element the tile loop evaluates a conservative prefilter instead of the canonical estimate. The
+// accumulators start at the bit pattern kBias of kBiasF = 1.5 * 2^23, so an accumulator read as a float
+// is F = kBiasF + acc exactly (|acc| <= 2^22 for any int8 operands), and
+//   g = fmaf(F, z, nd) >= T[q],  nd = 4z - kBiasF*z,  T[q] = (t0 - qcp)/qs - 2^-20 (|t0| + |qcp|)/qs
+// (every operation in f32). With u = 2^-24, qs > 0 and z >= 0: est = fmaf(RN(acc*qs), z, qcp) >= t0
+// implies acc*z >= (t0 - qcp)/qs - u|qcp|/qs - 3u|acc*z| >= (t0 - qcp)/qs - u|qcp|/qs - 0.75 z, while
+// F*z + nd = acc*z + 4z + e with |e| <= 1.5 z (the roundings of kBiasF*z and of nd) and g's own rounding
+// is at most u|acc*z + ...| <= 0.26 z, so g >= acc*z + 2.2 z; the rounding of T's three operations is far
+// below its 2^-20 margin. So every element whose estimate passes also passes the prefilter. (A query
+// with qs <= 0 or an overflowing T gets T = -inf, a row scale that is negative or infinite nd = +inf:
+// the prefilter then admits everything, and the exact test decides.) Per element that is one fma and one
+// compare; the two blocks' compares of an element share one branch on the pair of ballots.
+//
+// The passing elements are staged as (accumulator, tag) in the wave's LDS region. The flush computes the
+// canonical estimate of each, fmaf((float)(acc) * qs, zs, qcp), drops those below t0 (the few the
+// prefilter admits in excess), numbers the rest per pair with LDS atomics, reserves each query's range
+// with one global atomic per (item, query) and writes them out. So the emitted set and its estimates are
+// exactly those of the canonical formula; their order in a query's buffer is unspecified.
+//
+// The tile loop is software-pipelined: while the wave evaluates tile t, the 16 MFMAs of tile t + 1 are
+// issued into a second accumulator set, one between every two element tests, so the matrix core and the
+// VALU work at once (225 VGPRs, two workgroups per CU, 77 KB of LDS with 1536 staging slots per wave).
+// The item's pairs are processed in chunks of up to kMeta queries; a chunk whose candidates overflow a
+// wave's region is dropped and scanned again with half as many queries, down to 16 queries, whose
+// 16 x 64 candidates per wave always fit.
+template <int NW>
+struct EmitStage {
+  int acc[NW][kCapE];       // biased dot products of the staged elements; the estimate after the exact test
+  uint32_t tag[NW][kCapE];  // row - first row of the item (bits 0-7) | pair index (8-19) | number (20-31)
+  uint32_t lcnt[kMeta];     // candidates of each pair in the item; then the pair's base in its query's buffer
+  int n[NW];
+};
+
+// The emit pass's accumulators start at the bit pattern of kBiasF = 1.5 * 2^23, so that an accumulator
+// holding kBias + dot reads as the float kBiasF + dot exactly for |dot| <= 2^22 (any int8 operands:
+// 256 * 128 * 128 = 2^22): the prefilter needs no int-to-float conversion.
+constexpr int kBias = 0x4B400000;
+constexpr float kBiasF = 12582912.0f;
+
+__device__ __forceinline__ float emit_prefilter_T(float th, float qc, float qsv) {
+  if (!(qsv > 0.f)) return -__builtin_inff();
+  const float b = (th - qc) / qsv;
+  const float m = (fabsf(th) + fabsf(qc)) * (0x1p-20f / qsv);
+  const float T = b - m;
+  if (!(T < __builtin_inff())) return th == __builtin_inff() ? __builtin_inff() : -__builtin_inff();
+  return T;
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
+    const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
+    const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
+    const int32_t *__restrict__ prow, const int32_t *__restrict__ ps, const int32_t *__restrict__ pe, int P,
+    const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N, const float *__restrict__ qcp,
+    const float *__restrict__ t0, int32_t *__restrict__ cnt, float *__restrict__ bval, int32_t *__restrict__ bpos,
+    int CAP) {
+  constexpr int NT = 64 * NW;     // threads of the workgroup
+  constexpr int kSt = 8 / NW;     // MFMA steps of a query tile each wave requests
+  static_assert(kNB == 2, "the epilogue pairs the ballots of two blocks");
+  static_assert(NW == 4, "an item's 256 rows are one pass of four waves");
+  __shared__ __align__(16) Meta meta[kMeta];
+  __shared__ __align__(16) float Tl[kMeta + 32];
+  __shared__ __align__(16) float zsl[256];
+  __shared__ __align__(16) v4i bsh0[8 * 64];  // query tiles of even index: [step s][half h][query li], 16 B each
+  __shared__ __align__(16) v4i bsh1[8 * 64];  // query tiles of odd index
+  __shared__ EmitStage<NW> S;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = fvs_wave_id();
+  const int h = lane >> 5, li = lane & 31;
+  v16i bias;  // the first MFMA of every chain accumulates onto kBias (kept in registers, not rematerialised)
 #pragma unroll
-            for (int s = 0; s < 8; s++) b[s] = bsh[t & 1][s * 64 + lane];
-            v16i acc[kNB];
+  for (int i = 0; i < 16; i++) {
+    int b = kBias;
+    asm volatile("" : "+v"(b));
+    bias[i] = b;
+  }
+
+  struct Item {
+    int c, qn, qoff, r0, cs, ce;
+  };
+  auto item_at = [&](int p) {
+    Item it{0, 0, 0, 0, 0, 0};
+    if (p < P) {
+      it.c = pcell[p];
+      it.r0 = prow[p];
+      it.cs = ps[p];
+      it.ce = pe[p];
+      it.qn = ccnt[it.c];
+      it.qoff = coff[it.c];
+    }
+    return it;
+  };
+  int pq[kMeta / NT];  // pair ids of the item's first chunk
+  float zr[256 / NT];  // row scales of the item's rows r0 + tid + NT i (NaN outside the cell)
+  v4i cb[kNB][8];      // this wave's code blocks: the B operands
+  auto load_cb = [&](int r0p, int ce) {
 #pragma unroll
-            for (int u = 0; u < kNB; u++) {
-              acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-              if (act[u]) {
+    for (int u = 0; u < kNB; u++) {
+      const int b0 = r0p + 32 * (kNB * w + u);
+      int64_t zr_ = (int64_t)b0 + li;
+      if (b0 >= ce || zr_ > N - 1) zr_ = N - 1;  // rows past the cell carry a NaN scale
+      const v4i *zp = reinterpret_cast<const v4i *>(Z + zr_ * kR + h * 16);
 #pragma unroll
-                for (int s = 0; s < 8; s++)
-                  acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
+      for (int s = 0; s < 8; s++) cb[u][s] = zp[2 * s];
+    }
+  };
+  auto prefetch = [&](const Item &it) {
+    if (it.qn == 0) return;
+#pragma unroll
+    for (int i = 0; i < kMeta / NT; i++) {
+      const int j = tid + NT * i;
+      pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 256 / NT; i++) {
+      const int r = it.r0 + tid + NT * i;
+      zr[i] = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
+    }
+    load_cb(it.r0, it.ce);
+  };
+
+  const int stride = (int)gridDim.x;
+  int p = blockIdx.x;
+  Item cur = item_at(p);
+  prefetch(cur);
+  while (p < P) {
+    const Item nxt = item_at(p + stride);
+    if (cur.qn == 0) {
+      prefetch(nxt);
+      cur = nxt;
+      p += stride;
+      continue;
+    }
+    const int qn = cur.qn, qoff = cur.qoff;
+    const int row0 = cur.r0;
+#pragma unroll
+    for (int i = 0; i < 256 / NT; i++) zsl[tid + NT * i] = zr[i];
+    int ebase = 0;  // wave-uniform: used slots of this wave's region (may exceed kCapE: overflow)
+    int nq = 0;     // queries of the current pair chunk
+
+    // the tile loop over the current chunk's nq pairs (staged in meta / Tl)
+    auto scan = [&]() {
+      const int ntiles = (nq + 31) / 32;
+      // tile t's fragments go to bsh0 (t even) or bsh1 (t odd): global_load_lds, 16 B per lane; wave w
+      // requests kSt of the 8 steps
+      auto request = [&](int tile, v4i *buf) {
+        const int jr = min(tile * 32 + li, nq - 1);
+        const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
+#pragma unroll
+        for (int k = 0; k < kSt; k++) {
+          const int s = kSt * w + k;
+          __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&buf[s * 64], 16,
+                                           0, 0);
+        }
+      };
+      auto published = [&]() {  // this wave's requests have landed in LDS; every wave is past the reads
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      };
+      auto load_qa = [&](v4i (&qa)[8], const v4i *buf) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) qa[s] = buf[s * 64 + lane];
+      };
+      {
+        constexpr int rp = 0;  // the item's rows are one pass: 4 waves x 2 blocks x 32 rows = 256
+        const bool any = row0 + 32 * kNB * w < cur.ce;  // the wave has rows of the cell
+        // this lane's row scale per block and the prefilter's addend; rows outside the cell have a NaN
+        // scale and never pass
+        float zl[kNB], nd[kNB];
+#pragma unroll
+        for (int u = 0; u < kNB; u++) {
+          const float z = zsl[32 * (kNB * w + u) + li];
+          const bool fin = z >= 0.f && z < __builtin_inff();
+          const float cz = kBiasF * z;
+          zl[u] = fin || z != z ? z : 0.f;
+          nd[u] = fin || z != z ? 4.f * z - cz : __builtin_inff();
+        }
+        // The epilogue of tile t over the accumulators A, with (PIPE) the MFMAs of tile t + 1 into Nx
+        // interleaved: one MFMA per element, alternating the two blocks' chains, so the matrix core works
+        // on the next tile while the wave evaluates this one.
+        auto epilogue = [&](const v16i (&A)[kNB], v16i (&Nx)[kNB], const v4i (&qa)[8], int t,
+                            auto PIPE) __attribute__((always_inline)) {
+          constexpr bool pipe = decltype(PIPE)::value;
+          const uint32_t tagt = (uint32_t)(32 * t + 4 * h) << 8;
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const float4 x = *reinterpret_cast<const float4 *>(&Tl[32 * t + 8 * g + 4 * h]);
+            const float Tg[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const int v = 4 * g + i;
+              if constexpr (pipe) {
+                const int uu = v & 1, ss = v >> 1;
+                Nx[uu] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[ss], cb[uu][ss], ss == 0 ? bias : Nx[uu], 0, 0, 0);
               }
-            }
-            const int jl = t * 32 + li;  // pair index inside the chunk
-            const bool valid = jl < nq;
-            const Meta m = meta[valid ? jl : nq - 1];
-            const float th = MODE == 1 && valid ? m.x : __builtin_inff();
-            const uint32_t tag0 = ((uint32_t)(c0 + jl) << 8) | (uint32_t)(64 * w + 4 * h);
+              // both blocks' tests of element v, then one branch for the pair of ballots
+              bool pass_[kNB];
+              uint64_t bal[kNB];
 #pragma unroll
-            for (int u = 0; u < kNB; u++) {
-              if (MODE == 0 && !act[u]) continue;
-              // estimates of the block's 16 elements; the row scales are read from LDS up front
-              float ev[16];
-#pragma unroll
-              for (int g = 0; g < 4; g++) {
-                const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
-                const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                  ev[4 * g + i] = __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp);
+              for (int u = 0; u < kNB; u++) {
+                pass_[u] = __builtin_fmaf(__int_as_float(A[u][v]), zl[u], nd[u]) >= Tg[i];
+                bal[u] = __ballot(pass_[u]);
               }
-              if (MODE == 0) {
-                float mx = -1e30f;
+              if (bal[0] | bal[1]) {
 #pragma unroll
-                for (int v = 0; v < 16; v++) mx = fmaxf(mx, ev[v]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
-                if (h == 0 && valid)
-                  bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + kNB * w + u - (cs >> 5))] = mx;
-              } else if (!direct) {
-                // Per element: a wave ballot of est >= t0 (the compare's own mask). An empty ballot (about
-                // half of them) is a scalar branch; otherwise the passing lanes, under the exec mask, take
-                // consecutive slots of the wave's region. The region's fill is wave-uniform, so the
-                // overflow test is scalar too; the count keeps growing past kCap so that the item end
-                // sees the overflow and redoes the item on the direct path.
-                float *est = E->est[w];
-                uint32_t *tag = E->tag[w];
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                  const bool pass = ev[v] >= th;
-                  const uint64_t bal = __ballot(pass);
-                  if (bal) {
-                    const int pop = __popcll(bal);
-                    if (ebase + pop <= kCap && pass) {
-                      // the region's fill is a scalar offset of the base; the lane adds its rank
-                      const int pre = fvs_lane_prefix(bal);
-                      (est + ebase)[pre] = ev[v];
-                      (tag + ebase)[pre] = tag0 + (uint32_t)(32 * u + 8 * (v >> 2) + (v & 3));
+                for (int u = 0; u < kNB; u++) {
+                  const int ro = rp + 32 * (kNB * w + u) + li;  // the lane's row, relative to the item's first row
+                  if (bal[u]) {
+                    const int pop = __popcll(bal[u]);
+                    if (ebase + pop <= kCapE && pass_[u]) {
+                      const int pre = fvs_lane_prefix(bal[u]);
+                      (S.acc[w] + ebase)[pre] = A[u][v];
+                      (S.tag[w] + ebase)[pre] = ((uint32_t)ro | tagt) + ((uint32_t)(8 * g + i) << 8);
                     }
                     ebase += pop;
                   }
                 }
-              } else {  // direct path
-                // the lane's first row of the block; the empty asm keeps the compiler from hoisting the 16
-                // per-element row ids out of the tile loop, where they would hold (and spill) 32 VGPRs
-                int rb = row0 + 32 * (kNB * w + u) + 4 * h;
-                asm volatile("" : "+v"(rb));
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                  if (ev[v] >= th) {
-                    const int idx = atomicAdd(&cnt[m.qid], 1);
-                    if (idx < CAP) {
-                      bval[(int64_t)m.qid * CAP + idx] = ev[v];
-                      bpos[(int64_t)m.qid * CAP + idx] = rb + 8 * (v >> 2) + (v & 3);
-                    }
-                  }
-                }
               }
             }
-          };
-          request(0);
-          published();
-          for (int t = 0; t < ntiles; t++) {
-            if (t + 1 < ntiles) request(t + 1);  // the other buffer: every wave has left tile t - 1
-            if (any) compute(t);
+          }
+        };
+        // tile loop, unrolled by two so that buffers and accumulator sets swap roles statically:
+        // step t: wait for tile t + 1, read its fragments, request tile t + 2 into the buffer tile t used,
+        // then evaluate tile t while the MFMAs of tile t + 1 run
+        request(0, bsh0);
+        published();
+        if (ntiles > 1) request(1, bsh1);
+        if (any) {
+          v16i accA[kNB], accB[kNB];
+          v4i qa[8];
+          load_qa(qa, bsh0);
+#pragma unroll
+          for (int s = 0; s < 8; s++)
+#pragma unroll
+            for (int u = 0; u < kNB; u++)
+              accA[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], cb[u][s], s == 0 ? bias : accA[u], 0, 0, 0);
+          for (int t = 0;; t += 2) {
+            published();  // tile t + 1 is in bsh1
+            if (t + 1 >= ntiles) {
+              epilogue(accA, accB, qa, t, std::false_type{});
+              break;
+            }
+            load_qa(qa, bsh1);
+            if (t + 2 < ntiles) request(t + 2, bsh0);
+            epilogue(accA, accB, qa, t, std::true_type{});
+            published();  // tile t + 2 is in bsh0
+            if (t + 2 >= ntiles) {
+              epilogue(accB, accA, qa, t + 1, std::false_type{});
+              break;
+            }
+            load_qa(qa, bsh0);
+            if (t + 3 < ntiles) request(t + 3, bsh1);
+            epilogue(accB, accA, qa, t + 1, std::true_type{});
+          }
+        } else {  // a wave without rows of the cell: the same barriers and requests, no compute
+          for (int t = 0;; t += 2) {
             published();
+            if (t + 1 >= ntiles) break;
+            if (t + 2 < ntiles) request(t + 2, bsh0);
+            published();
+            if (t + 2 >= ntiles) break;
+            if (t + 3 < ntiles) request(t + 3, bsh1);
           }
         }
       }
     };
 
-    if constexpr (MODE == 0) {
-      scan(true, true);
-      prefetch(nxt);
-    } else {
-      scan(!staged, true);
-      if (!staged) {
-        prefetch(nxt);
-      } else {
-        // a wave whose region overflowed: drop the staged candidates and redo the item on the direct path
-        if (lane == 0) E->n[w] = ebase;
-        __syncthreads();
-        if (E->n[0] > kCap || E->n[1] > kCap || E->n[2] > kCap || E->n[3] > kCap) {
-          __syncthreads();
-          scan(true, false);
-          prefetch(nxt);
-        } else {
-          prefetch(nxt);  // the code blocks are no longer needed: the next item's loads run under the flush
-          // flush: every staged candidate takes its number among its pair's candidates with an LDS atomic,
-          // then one global atomic per (item, query) reserves the query's range, and every candidate goes
-          // to base + number
+    // flush of the current chunk: the exact estimate of every staged element; those at or above t0 take
+    // their number among their pair's candidates (LDS atomic), one global atomic per (item, query) reserves
+    // the query's range, and every candidate goes to base + number
+    auto flush = [&]() {
 #pragma unroll
-          for (int ww = 0; ww < 4; ww++) {
-            const int nn = E->n[ww];
-            for (int k = tid; k < nn; k += 256) {
-              const uint32_t tg = E->tag[ww][k];
-              const uint32_t num = atomicAdd(&E->lcnt[(tg >> 8) & 0xfffu], 1u);  // < 256 rows per item
-              E->tag[ww][k] = tg | (num << 20);
-            }
-          }
-          __syncthreads();
-          for (int j = tid; j < qn; j += 256) {
-            const int c = (int)E->lcnt[j];
-            E->lcnt[j] = c ? (uint32_t)atomicAdd(&cnt[meta[j].qid], c) : 0u;
-          }
-          __syncthreads();
-#pragma unroll
-          for (int ww = 0; ww < 4; ww++) {
-            const int nn = E->n[ww];
-            for (int k = tid; k < nn; k += 256) {
-              const uint32_t tg = E->tag[ww][k];
-              const int j = (tg >> 8) & 0xfffu;
-              const int idx = (int)E->lcnt[j] + (int)(tg >> 20);
-              if (idx < CAP) {
-                const int64_t q = meta[j].qid;
-                bval[q * CAP + idx] = E->est[ww][k];
-                bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
-              }
-            }
+      for (int ww = 0; ww < NW; ww++) {
+        const int nn = S.n[ww];
+        for (int k = tid; k < nn; k += NT) {
+          const uint32_t tg = S.tag[ww][k];
+          const int j = (int)((tg >> 8) & 0xfffu);
+          const Meta m = meta[j];
+          const float est = __builtin_fmaf((float)(S.acc[ww][k] - kBias) * m.qs, zsl[tg & 0xffu], m.qcp);
+          if (est >= m.x) {
+            const uint32_t num = atomicAdd(&S.lcnt[j], 1u);  // < 256 rows per item
+            S.acc[ww][k] = __float_as_int(est);
+            S.tag[ww][k] = tg | (num << 20);
+          } else {
+            S.tag[ww][k] = 0xffffffffu;  // admitted by the prefilter only
           }
         }
       }
-      __syncthreads();  // the flush has read the LDS tables before the next item's staging rewrites them
+      __syncthreads();
+      for (int j = tid; j < nq; j += NT) {
+        const int c = (int)S.lcnt[j];
+        S.lcnt[j] = c ? (uint32_t)atomicAdd(&cnt[meta[j].qid], c) : 0u;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ww = 0; ww < NW; ww++) {
+        const int nn = S.n[ww];
+        for (int k = tid; k < nn; k += NT) {
+          const uint32_t tg = S.tag[ww][k];
+          if (tg == 0xffffffffu) continue;
+          const int j = (int)((tg >> 8) & 0xfffu);
+          const int idx = (int)S.lcnt[j] + (int)(tg >> 20);
+          if (idx < CAP) {
+            const int64_t q = meta[j].qid;
+            bval[q * CAP + idx] = __int_as_float(S.acc[ww][k]);
+            bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
+          }
+        }
+      }
+      __syncthreads();  // the flush has read meta and the regions before the next chunk restages them
+    };
+
+    // The item's pairs in chunks of csz queries (kMeta at first), each staged, scanned and flushed. A chunk
+    // whose candidates overflow a wave's region is dropped and scanned again with half as many queries, down
+    // to 16, whose at most 16 x 64 candidates per wave always fit.
+    bool pq_ok = true;  // pq holds the first kMeta pair ids of the item
+    for (int c0 = 0, csz = kMeta;;) {
+      nq = min(csz, qn - c0);
+      if (!(pq_ok && c0 == 0)) {
+#pragma unroll
+        for (int i = 0; i < kMeta / NT; i++) {
+          const int j = tid + NT * i;
+          pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
+        }
+      }
+      pq_ok = false;
+#pragma unroll
+      for (int i = 0; i < kMeta / NT; i++) {
+        const int j = tid + NT * i;
+        if (j < nq) {
+          const int pidx = qoff + c0 + j;
+          const int q = pq[i];
+          Meta m;
+          m.qid = q;
+          m.qs = qs[q];
+          m.qcp = qcp[pidx];
+          m.x = t0[q];
+          meta[j] = m;
+          Tl[j] = emit_prefilter_T(m.x, m.qcp, m.qs);
+          S.lcnt[j] = 0u;
+        }
+      }
+      if (tid < 32) Tl[nq + tid] = __builtin_inff();  // the last tile's missing queries pass nothing
+      ebase = 0;
+      __syncthreads();
+      scan();
+      if (lane == 0) S.n[w] = ebase;
+      __syncthreads();
+      bool over = false;
+#pragma unroll
+      for (int ww = 0; ww < NW; ww++) over = over || S.n[ww] > kCapE;
+      if (over) {  // csz >= 32 here: a 16-query chunk stages at most 16 x 64 = 1024 < kCapE per wave
+        csz >>= 1;   // the same first pair again, with half the queries
+        continue;
+      }
+      if (c0 + nq >= qn) break;  // the last chunk is flushed after the next item's loads are issued
+      flush();
+      c0 += nq;
     }
-    if constexpr (!persist) break;
+    prefetch(nxt);  // the code blocks are no longer needed: the next item's loads run under the flush
+    flush();
     cur = nxt;
     p += stride;
   }
@@ -472,17 +707,17 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // both passes: three resident workgroups per CU, each looping over items with the next item's loads in
-  // flight during the current one
-  const unsigned grid = (mode == 0 || kPersistEmit) ? (unsigned)min(P, 3 * fvs_cu_count()) : (unsigned)P;
+  // persistent grids: the first pass with three resident workgroups per CU, the emit pass with two (its
+  // software-pipelined tile loop holds two accumulator sets)
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<0>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, prow, ps,
-                       pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+    hipLaunchKernelGGL(k_i8_first, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(256), 0, st, q8, qs, qid, qrank,
+                       coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, bm, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_scan<1>, dim3(grid), dim3(256), 0, st, q8, qs, qid, qrank, coff, ccnt, pcell, prow, ps,
-                       pe, P, Z, zs, N, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+    hipLaunchKernelGGL(k_i8_emit<kEmitWaves>, dim3((unsigned)min(P, (8 / kEmitWaves) * fvs_cu_count())),
+                       dim3(64 * kEmitWaves), 0, st, q8, qs, qid, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, t0,
+                       cnt, bval, bpos, CAP);
   }
   return fvs_launch_status();
 }

@@ -266,6 +266,19 @@ class EngineI8:
             self.nbad2 += int((~ok2[:nb]).sum())
         return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
 
+    def warm_fallbacks(self, B, K, z, nprobe, k, upto=64):
+        """Capture the fallback graphs of 1, 2, 4, ... `upto` flagged rows of an already searched (B, K, z,
+        nprobe, k) ahead of time, so that no later search pays a capture (tens of milliseconds)."""
+        key = (B, K, float(z), nprobe, k, self._knobs())
+        if key not in self.graphs:
+            raise KeyError("warm_fallbacks: search this (B, K, z, nprobe, k) once first")
+        g, qs, outs, _, _ = self.graphs[key]
+        g.replay()  # the captures' warm-up runs read the main graph's outputs
+        nbp = 1
+        while nbp <= upto:
+            self._fallback_graph(key, qs, outs[5], nbp)
+            nbp *= 2
+
     def _fallback_graph(self, key, qs, blas, nbp):
         """The captured fallback of nbp rows gathered (by `sel`) from the main graph's query and BLAS
         buffers; it is replayed right after the main graph, so those hold the batch's values."""
