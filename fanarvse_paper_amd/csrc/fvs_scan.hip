@@ -368,9 +368,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
       const int ntiles = (nq + 31) / 32;
       // tile t's fragments go to bsh0 (t even) or bsh1 (t odd): global_load_lds, 16 B per lane; wave w
       // requests kSt of the 8 steps
-      auto request = [&](int tile, v4i *buf) {
-        const int jr = min(tile * 32 + li, nq - 1);
-        const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
+      // the query of lane li in a tile (its fragments are requested with it), read from LDS ahead of the
+      // request so that the read overlaps the step's other LDS reads
+      auto req_id = [&](int tile) { return meta[min(tile * 32 + li, nq - 1)].qid; };
+      auto request_q = [&](int q, v4i *buf) {
+        const int8_t *src = q8 + (int64_t)q * kR + h * 16;
 #pragma unroll
         for (int k = 0; k < kSt; k++) {
           const int s = kSt * w + k;
@@ -378,6 +380,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
                                            0, 0);
         }
       };
+      auto request = [&](int tile, v4i *buf) { request_q(req_id(tile), buf); };
       auto published = [&]() {  // this wave's requests have landed in LDS; every wave is past the reads
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -385,6 +388,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
       auto load_qa = [&](v4i (&qa)[8], const v4i *buf) {
 #pragma unroll
         for (int s = 0; s < 8; s++) qa[s] = buf[s * 64 + lane];
+      };
+      // the prefilter thresholds of the lane's 16 queries of tile t: 32t + 8g + 4h + i, element 4g + i
+      auto load_T = [&](float (&Tv)[16], int t) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 x = *reinterpret_cast<const float4 *>(&Tl[32 * t + 8 * g + 4 * h]);
+          Tv[4 * g] = x.x;
+          Tv[4 * g + 1] = x.y;
+          Tv[4 * g + 2] = x.z;
+          Tv[4 * g + 3] = x.w;
+        }
       };
       {
         constexpr int rp = 0;  // the item's rows are one pass: 4 waves x 2 blocks x 32 rows = 256
@@ -403,14 +417,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
         // The epilogue of tile t over the accumulators A, with (PIPE) the MFMAs of tile t + 1 into Nx
         // interleaved: one MFMA per element, alternating the two blocks' chains, so the matrix core works
         // on the next tile while the wave evaluates this one.
-        auto epilogue = [&](const v16i (&A)[kNB], v16i (&Nx)[kNB], const v4i (&qa)[8], int t,
+        auto epilogue = [&](const v16i (&A)[kNB], v16i (&Nx)[kNB], const v4i (&qa)[8], const float (&Tv)[16], int t,
                             auto PIPE) __attribute__((always_inline)) {
           constexpr bool pipe = decltype(PIPE)::value;
           const uint32_t tagt = (uint32_t)(32 * t + 4 * h) << 8;
+          // Four elements of both blocks at a time: their eight tests are independent, so they issue back to
+          // back, and one branch on the OR of the eight ballots skips the group (a branch per element would
+          // make every test wait for the previous one's scalar round trip).
 #pragma unroll
           for (int g = 0; g < 4; g++) {
-            const float4 x = *reinterpret_cast<const float4 *>(&Tl[32 * t + 8 * g + 4 * h]);
-            const float Tg[4] = {x.x, x.y, x.z, x.w};
+            bool pass_[4][kNB];
+            uint64_t bal[4][kNB];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const int v = 4 * g + i;
@@ -418,23 +435,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
                 const int uu = v & 1, ss = v >> 1;
                 Nx[uu] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[ss], cb[uu][ss], ss == 0 ? bias : Nx[uu], 0, 0, 0);
               }
-              // both blocks' tests of element v, then one branch for the pair of ballots
-              bool pass_[kNB];
-              uint64_t bal[kNB];
 #pragma unroll
               for (int u = 0; u < kNB; u++) {
-                pass_[u] = __builtin_fmaf(__int_as_float(A[u][v]), zl[u], nd[u]) >= Tg[i];
-                bal[u] = __ballot(pass_[u]);
+                pass_[i][u] = __builtin_fmaf(__int_as_float(A[u][v]), zl[u], nd[u]) >= Tv[v];
+                bal[i][u] = __ballot(pass_[i][u]);
               }
-              if (bal[0] | bal[1]) {
+            }
+            if ((bal[0][0] | bal[0][1]) | (bal[1][0] | bal[1][1]) | (bal[2][0] | bal[2][1]) | (bal[3][0] | bal[3][1])) {
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
 #pragma unroll
                 for (int u = 0; u < kNB; u++) {
-                  const int ro = rp + 32 * (kNB * w + u) + li;  // the lane's row, relative to the item's first row
-                  if (bal[u]) {
-                    const int pop = __popcll(bal[u]);
-                    if (ebase + pop <= kCapE && pass_[u]) {
-                      const int pre = fvs_lane_prefix(bal[u]);
-                      (S.acc[w] + ebase)[pre] = A[u][v];
+                  if (bal[i][u]) {
+                    const int ro = rp + 32 * (kNB * w + u) + li;  // the lane's row, relative to the item's first row
+                    const int pop = __popcll(bal[i][u]);
+                    if (ebase + pop <= kCapE && pass_[i][u]) {
+                      const int pre = fvs_lane_prefix(bal[i][u]);
+                      (S.acc[w] + ebase)[pre] = A[u][4 * g + i];
                       (S.tag[w] + ebase)[pre] = ((uint32_t)ro | tagt) + ((uint32_t)(8 * g + i) << 8);
                     }
                     ebase += pop;
@@ -453,29 +470,49 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
         if (any) {
           v16i accA[kNB], accB[kNB];
           v4i qa[8];
+          float Tv[16];
           load_qa(qa, bsh0);
 #pragma unroll
           for (int s = 0; s < 8; s++)
 #pragma unroll
             for (int u = 0; u < kNB; u++)
               accA[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], cb[u][s], s == 0 ? bias : accA[u], 0, 0, 0);
-          for (int t = 0;; t += 2) {
+          // each step issues its LDS reads together (the next request's query id first, then the fragments of
+          // tile t + 1 and the thresholds of tile t) and waits once
+          int t = 0;
+          bool inB = false;  // the last tile's accumulators are accB (else accA)
+          for (;; t += 2) {
             published();  // tile t + 1 is in bsh1
-            if (t + 1 >= ntiles) {
-              epilogue(accA, accB, qa, t, std::false_type{});
-              break;
+            if (t + 1 >= ntiles) break;
+            {
+              const int rq = req_id(t + 2);
+              asm volatile("" ::: "memory");  // keep the id read first in the LDS queue
+              load_qa(qa, bsh1);
+              load_T(Tv, t);
+              if (t + 2 < ntiles) request_q(rq, bsh0);
             }
-            load_qa(qa, bsh1);
-            if (t + 2 < ntiles) request(t + 2, bsh0);
-            epilogue(accA, accB, qa, t, std::true_type{});
+            epilogue(accA, accB, qa, Tv, t, std::true_type{});
             published();  // tile t + 2 is in bsh0
             if (t + 2 >= ntiles) {
-              epilogue(accB, accA, qa, t + 1, std::false_type{});
+              inB = true;
               break;
             }
-            load_qa(qa, bsh0);
-            if (t + 3 < ntiles) request(t + 3, bsh1);
-            epilogue(accB, accA, qa, t + 1, std::true_type{});
+            {
+              const int rq = req_id(t + 3);
+              asm volatile("" ::: "memory");  // keep the id read first in the LDS queue
+              load_qa(qa, bsh0);
+              load_T(Tv, t + 1);
+              if (t + 3 < ntiles) request_q(rq, bsh1);
+            }
+            epilogue(accB, accA, qa, Tv, t + 1, std::true_type{});
+          }
+          // the last tile: no MFMAs follow
+          if (inB) {
+            load_T(Tv, t + 1);
+            epilogue(accB, accA, qa, Tv, t + 1, std::false_type{});
+          } else {
+            load_T(Tv, t);
+            epilogue(accA, accB, qa, Tv, t, std::false_type{});
           }
         } else {  // a wave without rows of the cell: the same barriers and requests, no compute
           for (int t = 0;; t += 2) {
@@ -576,6 +613,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
       for (int ww = 0; ww < NW; ww++) over = over || S.n[ww] > kCapE;
       if (over) {  // csz >= 32 here: a 16-query chunk stages at most 16 x 64 = 1024 < kCapE per wave
         csz >>= 1;   // the same first pair again, with half the queries
+        pq_ok = false;
         continue;
       }
       if (c0 + nq >= qn) break;  // the last chunk is flushed after the next item's loads are issued
