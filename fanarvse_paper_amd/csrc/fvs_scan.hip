@@ -37,7 +37,7 @@ constexpr int kNB = 2;          // 32-row blocks per wave
 constexpr int kCB = 4 * kNB;    // 32-row blocks per work item
 constexpr int kMeta = 512;      // pairs staged in LDS at a time
 constexpr int kEmitWaves = 4;   // waves per emit workgroup
-constexpr int kCapE = 1536;     // LDS candidate slots per wave of the emit pass
+constexpr int kCapE = 640;      // LDS candidate slots per wave of the emit pass
 
 // row of accumulator element v in the 32x32 layout, for lanes of half h = l / 32
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
@@ -222,44 +222,36 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 // covers two (query, 32-row block) pairs, and since the rows that pass for a query come in clusters, most
 // ballots are empty (about 9 %, against 44 % with one query per lane).
 //
-// Per element the tile loop evaluates a conservative prefilter instead of the canonical estimate. The
-// accumulators start at the bit pattern kBias of kBiasF = 1.5 * 2^23, so an accumulator read as a float
-// is F = kBiasF + acc exactly (|acc| <= 2^22 for any int8 operands), and
-//   g = fmaf(F, z, nd) >= T[q],  nd = 4z - kBiasF*z,  T[q] = (t0 - qcp)/qs - 2^-20 (|t0| + |qcp|)/qs
-// (every operation in f32). With u = 2^-24, qs > 0 and z >= 0: est = fmaf(RN(acc*qs), z, qcp) >= t0
-// implies acc*z >= (t0 - qcp)/qs - u|qcp|/qs - 3u|acc*z| >= (t0 - qcp)/qs - u|qcp|/qs - 0.75 z, while
-// F*z + nd = acc*z + 4z + e with |e| <= 1.5 z (the roundings of kBiasF*z and of nd) and g's own rounding
-// is at most u|acc*z + ...| <= 0.26 z, so g >= acc*z + 2.2 z; the rounding of T's three operations is far
-// below its 2^-20 margin. So every element whose estimate passes also passes the prefilter. (A query
-// with qs <= 0 or an overflowing T gets T = -inf, a row scale that is negative or infinite nd = +inf:
-// the prefilter then admits everything, and the exact test decides.) Per element that is one fma and one
-// compare; the two blocks' compares of an element share one branch on the pair of ballots.
+// Per element the tile loop evaluates a conservative prefilter instead of the canonical estimate:
+//   g = fmaf((float)acc, z, 2z) >= T[q],  T[q] = (t0 - qcp)/qs - 2^-20 (|t0| + |qcp|)/qs  (f32 ops).
+// With u = 2^-24, |acc| <= 2^22 (any int8 operands: 256 * 128 * 128), qs > 0 and z >= 0:
+// est = fmaf(RN(acc*qs), z, qcp) >= t0 implies acc*z >= (t0 - qcp)/qs - u|qcp|/qs - 3u|acc*z|
+// >= (t0 - qcp)/qs - u|qcp|/qs - 0.75 z, while g >= acc*z + 2z - u|acc*z + 2z| >= acc*z + 1.74 z, and the
+// rounding of T's three operations is far below its 2^-20 margin; so every element whose estimate passes
+// also passes the prefilter. (A query with qs <= 0 or an overflowing T gets T = -inf, a row scale that is
+// negative or infinite the addend +inf: the prefilter then admits everything, and the exact test
+// decides.) Per element that is a convert, an fma and a compare; the tests of four elements of both
+// blocks are made before one branch on the OR of their eight ballots skips the group.
 //
 // The passing elements are staged as (accumulator, tag) in the wave's LDS region. The flush computes the
-// canonical estimate of each, fmaf((float)(acc) * qs, zs, qcp), drops those below t0 (the few the
+// canonical estimate of each, fmaf((float)acc * qs, zs, qcp), drops those below t0 (the few the
 // prefilter admits in excess), numbers the rest per pair with LDS atomics, reserves each query's range
 // with one global atomic per (item, query) and writes them out. So the emitted set and its estimates are
 // exactly those of the canonical formula; their order in a query's buffer is unspecified.
 //
-// The tile loop is software-pipelined: while the wave evaluates tile t, the 16 MFMAs of tile t + 1 are
-// issued into a second accumulator set, one between every two element tests, so the matrix core and the
-// VALU work at once (225 VGPRs, two workgroups per CU, 77 KB of LDS with 1536 staging slots per wave).
+// Three workgroups per CU (at most 168 VGPRs, 50 KB of LDS with 640 staging slots per wave): the third
+// resident workgroup hides more of each item's fixed latencies (pair staging, first tile, flush) than
+// overlapping the next tile's MFMAs with the current epilogue inside one wave did at two per CU.
 // The item's pairs are processed in chunks of up to kMeta queries; a chunk whose candidates overflow a
 // wave's region is dropped and scanned again with half as many queries, down to 16 queries, whose
 // 16 x 64 candidates per wave always fit.
 template <int NW>
 struct EmitStage {
-  int acc[NW][kCapE];       // biased dot products of the staged elements; the estimate after the exact test
+  int acc[NW][kCapE];       // dot products of the staged elements; the estimate after the exact test
   uint32_t tag[NW][kCapE];  // row - first row of the item (bits 0-7) | pair index (8-19) | number (20-31)
   uint32_t lcnt[kMeta];     // candidates of each pair in the item; then the pair's base in its query's buffer
   int n[NW];
 };
-
-// The emit pass's accumulators start at the bit pattern of kBiasF = 1.5 * 2^23, so that an accumulator
-// holding kBias + dot reads as the float kBiasF + dot exactly for |dot| <= 2^22 (any int8 operands:
-// 256 * 128 * 128 = 2^22): the prefilter needs no int-to-float conversion.
-constexpr int kBias = 0x4B400000;
-constexpr float kBiasF = 12582912.0f;
 
 __device__ __forceinline__ float emit_prefilter_T(float th, float qc, float qsv) {
   if (!(qsv > 0.f)) return -__builtin_inff();
@@ -271,7 +263,7 @@ __device__ __forceinline__ float emit_prefilter_T(float th, float qc, float qsv)
 }
 
 template <int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
+__global__ __launch_bounds__(256, 3) void k_i8_emit(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
     const int32_t *__restrict__ prow, const int32_t *__restrict__ ps, const int32_t *__restrict__ pe, int P,
@@ -292,14 +284,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
   const int lane = tid & 63;
   const int w = fvs_wave_id();
   const int h = lane >> 5, li = lane & 31;
-  v16i bias;  // the first MFMA of every chain accumulates onto kBias (kept in registers, not rematerialised)
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    int b = kBias;
-    asm volatile("" : "+v"(b));
-    bias[i] = b;
-  }
-
   struct Item {
     int c, qn, qoff, r0, cs, ce;
   };
@@ -368,11 +352,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
       const int ntiles = (nq + 31) / 32;
       // tile t's fragments go to bsh0 (t even) or bsh1 (t odd): global_load_lds, 16 B per lane; wave w
       // requests kSt of the 8 steps
-      // the query of lane li in a tile (its fragments are requested with it), read from LDS ahead of the
-      // request so that the read overlaps the step's other LDS reads
-      auto req_id = [&](int tile) { return meta[min(tile * 32 + li, nq - 1)].qid; };
-      auto request_q = [&](int q, v4i *buf) {
-        const int8_t *src = q8 + (int64_t)q * kR + h * 16;
+      auto request = [&](int tile, v4i *buf) {
+        const int8_t *src = q8 + (int64_t)meta[min(tile * 32 + li, nq - 1)].qid * kR + h * 16;
 #pragma unroll
         for (int k = 0; k < kSt; k++) {
           const int s = kSt * w + k;
@@ -380,7 +361,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
                                            0, 0);
         }
       };
-      auto request = [&](int tile, v4i *buf) { request_q(req_id(tile), buf); };
       auto published = [&]() {  // this wave's requests have landed in LDS; every wave is past the reads
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -388,17 +368,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
       auto load_qa = [&](v4i (&qa)[8], const v4i *buf) {
 #pragma unroll
         for (int s = 0; s < 8; s++) qa[s] = buf[s * 64 + lane];
-      };
-      // the prefilter thresholds of the lane's 16 queries of tile t: 32t + 8g + 4h + i, element 4g + i
-      auto load_T = [&](float (&Tv)[16], int t) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const float4 x = *reinterpret_cast<const float4 *>(&Tl[32 * t + 8 * g + 4 * h]);
-          Tv[4 * g] = x.x;
-          Tv[4 * g + 1] = x.y;
-          Tv[4 * g + 2] = x.z;
-          Tv[4 * g + 3] = x.w;
-        }
       };
       {
         constexpr int rp = 0;  // the item's rows are one pass: 4 waves x 2 blocks x 32 rows = 256
@@ -410,16 +379,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
         for (int u = 0; u < kNB; u++) {
           const float z = zsl[32 * (kNB * w + u) + li];
           const bool fin = z >= 0.f && z < __builtin_inff();
-          const float cz = kBiasF * z;
           zl[u] = fin || z != z ? z : 0.f;
-          nd[u] = fin || z != z ? 4.f * z - cz : __builtin_inff();
+          nd[u] = fin || z != z ? z + z : __builtin_inff();
         }
-        // The epilogue of tile t over the accumulators A, with (PIPE) the MFMAs of tile t + 1 into Nx
-        // interleaved: one MFMA per element, alternating the two blocks' chains, so the matrix core works
-        // on the next tile while the wave evaluates this one.
-        auto epilogue = [&](const v16i (&A)[kNB], v16i (&Nx)[kNB], const v4i (&qa)[8], const float (&Tv)[16], int t,
-                            auto PIPE) __attribute__((always_inline)) {
-          constexpr bool pipe = decltype(PIPE)::value;
+        // the epilogue of tile t over its accumulators A
+        auto epilogue = [&](const v16i (&A)[kNB], int t) {
           const uint32_t tagt = (uint32_t)(32 * t + 4 * h) << 8;
           // Four elements of both blocks at a time: their eight tests are independent, so they issue back to
           // back, and one branch on the OR of the eight ballots skips the group (a branch per element would
@@ -431,13 +395,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const int v = 4 * g + i;
-              if constexpr (pipe) {
-                const int uu = v & 1, ss = v >> 1;
-                Nx[uu] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[ss], cb[uu][ss], ss == 0 ? bias : Nx[uu], 0, 0, 0);
-              }
 #pragma unroll
               for (int u = 0; u < kNB; u++) {
-                pass_[i][u] = __builtin_fmaf(__int_as_float(A[u][v]), zl[u], nd[u]) >= Tv[v];
+                pass_[i][u] = __builtin_fmaf((float)A[u][v], zl[u], nd[u]) >= Tl[32 * t + 8 * g + 4 * h + i];
                 bal[i][u] = __ballot(pass_[i][u]);
               }
             }
@@ -461,67 +421,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
             }
           }
         };
-        // tile loop, unrolled by two so that buffers and accumulator sets swap roles statically:
-        // step t: wait for tile t + 1, read its fragments, request tile t + 2 into the buffer tile t used,
-        // then evaluate tile t while the MFMAs of tile t + 1 run
+        // tile loop: step t requests tile t + 1 into the other buffer (every wave has passed the barrier
+        // that ended tile t - 1), computes tile t and waits for tile t + 1
         request(0, bsh0);
         published();
-        if (ntiles > 1) request(1, bsh1);
         if (any) {
-          v16i accA[kNB], accB[kNB];
+          v16i acc[kNB];
           v4i qa[8];
-          float Tv[16];
-          load_qa(qa, bsh0);
+          for (int t = 0; t < ntiles; t++) {
+            const v4i *cur_t = (t & 1) ? bsh1 : bsh0;
+            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
+            load_qa(qa, cur_t);
 #pragma unroll
-          for (int s = 0; s < 8; s++)
+            for (int s = 0; s < 8; s++)
 #pragma unroll
-            for (int u = 0; u < kNB; u++)
-              accA[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], cb[u][s], s == 0 ? bias : accA[u], 0, 0, 0);
-          // each step issues its LDS reads together (the next request's query id first, then the fragments of
-          // tile t + 1 and the thresholds of tile t) and waits once
-          int t = 0;
-          bool inB = false;  // the last tile's accumulators are accB (else accA)
-          for (;; t += 2) {
-            published();  // tile t + 1 is in bsh1
-            if (t + 1 >= ntiles) break;
-            {
-              const int rq = req_id(t + 2);
-              asm volatile("" ::: "memory");  // keep the id read first in the LDS queue
-              load_qa(qa, bsh1);
-              load_T(Tv, t);
-              if (t + 2 < ntiles) request_q(rq, bsh0);
-            }
-            epilogue(accA, accB, qa, Tv, t, std::true_type{});
-            published();  // tile t + 2 is in bsh0
-            if (t + 2 >= ntiles) {
-              inB = true;
-              break;
-            }
-            {
-              const int rq = req_id(t + 3);
-              asm volatile("" ::: "memory");  // keep the id read first in the LDS queue
-              load_qa(qa, bsh0);
-              load_T(Tv, t + 1);
-              if (t + 3 < ntiles) request_q(rq, bsh1);
-            }
-            epilogue(accB, accA, qa, Tv, t + 1, std::true_type{});
-          }
-          // the last tile: no MFMAs follow
-          if (inB) {
-            load_T(Tv, t + 1);
-            epilogue(accB, accA, qa, Tv, t + 1, std::false_type{});
-          } else {
-            load_T(Tv, t);
-            epilogue(accA, accB, qa, Tv, t, std::false_type{});
+              for (int u = 0; u < kNB; u++)
+                acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], cb[u][s], s == 0 ? (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0} : acc[u], 0, 0, 0);
+            epilogue(acc, t);
+            published();
           }
         } else {  // a wave without rows of the cell: the same barriers and requests, no compute
-          for (int t = 0;; t += 2) {
+          for (int t = 0; t < ntiles; t++) {
+            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
             published();
-            if (t + 1 >= ntiles) break;
-            if (t + 2 < ntiles) request(t + 2, bsh0);
-            published();
-            if (t + 2 >= ntiles) break;
-            if (t + 3 < ntiles) request(t + 3, bsh1);
           }
         }
       }
@@ -538,7 +460,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_i8_emit(
           const uint32_t tg = S.tag[ww][k];
           const int j = (int)((tg >> 8) & 0xfffu);
           const Meta m = meta[j];
-          const float est = __builtin_fmaf((float)(S.acc[ww][k] - kBias) * m.qs, zsl[tg & 0xffu], m.qcp);
+          const float est = __builtin_fmaf((float)S.acc[ww][k] * m.qs, zsl[tg & 0xffu], m.qcp);
           if (est >= m.x) {
             const uint32_t num = atomicAdd(&S.lcnt[j], 1u);  // < 256 rows per item
             S.acc[ww][k] = __float_as_int(est);
@@ -745,16 +667,14 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // persistent grids: the first pass with three resident workgroups per CU, the emit pass with two (its
-  // software-pipelined tile loop holds two accumulator sets)
+  // persistent grids of three resident workgroups per CU
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_i8_first, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(256), 0, st, q8, qs, qid, qrank,
                        coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, bm, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_emit<kEmitWaves>, dim3((unsigned)min(P, (8 / kEmitWaves) * fvs_cu_count())),
-                       dim3(64 * kEmitWaves), 0, st, q8, qs, qid, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, t0,
+    hipLaunchKernelGGL(k_i8_emit<kEmitWaves>, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(64 * kEmitWaves), 0, st, q8, qs, qid, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, t0,
                        cnt, bval, bpos, CAP);
   }
   return fvs_launch_status();
