@@ -6,9 +6,12 @@
 // it streams the candidate's packed record in 128-byte units (the next unit in flight while one is
 // summed), looks up two LUT entries per code byte, and folds the per-tier integer sums into the f32
 // estimate in tier order. All lanes of a wave process the same record dword at the same time, so the
-// per-dword descriptor (LUT base, plane weight, end-of-tier flag) is wave-uniform: it is read from a
-// lane register into a scalar register, the lookups of one dword hit one 64-byte table (no LDS bank
-// conflicts), and the only branch, at a tier's end, is uniform.
+// per-dword descriptor (LUT base, plane weight, end-of-tier and pair flags) is wave-uniform: the host
+// builds these descriptors once per record layout and passes them as a kernel argument, so they reach
+// scalar registers through the scalar cache; the lookups of one dword hit one 64-byte table (no LDS
+// bank conflicts), and the only branch, at a tier's end or a pair, is uniform.
+#include <type_traits>
+
 #include "fvs_common.h"
 
 namespace {
@@ -86,13 +89,26 @@ __global__ __launch_bounds__(256) void k_lut_build(const uint16_t *__restrict__ 
 
 constexpr int kScoreThreads = 256;
 constexpr int kUnit = 8;             // 16-byte chunks per pipeline unit (128 bytes of a record)
-constexpr int kUD = kUnit * 4;       // dwords per unit; lane l of a wave holds the descriptor of dword l % kUD
+constexpr int kUD = kUnit * 4;       // dwords per unit
 constexpr int kZeroBytes = 512;      // zero table after the LUT: dwords past the planes look up zeros
+constexpr int kSchedMax = 512;       // record dwords (whole units) the schedule covers: records up to 2 KiB
+constexpr int kSetupVec = 16;        // 16-byte table vectors per thread in the one-pass set-up (LW <= 16384)
 
-// Per-dword descriptors (LDS, one per dword of every unit): the LUT byte offset of the dword's first table,
-// the plane weight (shift), the tier, an end-of-tier flag, and a flag for the (scale, sigma) dword of tier t.
-constexpr uint32_t kMetaLast = 1u << 24;
-constexpr uint32_t kMetaPair = 1u << 25;
+// Schedule: one descriptor per record dword, the same for every record and query, built on the host and
+// passed as a kernel argument. Kernel arguments are read through the scalar cache, so a dword's descriptor
+// arrives in a scalar register with no vector instruction.
+//   bits 0-2   plane weight (shift); bits 3-5 are zero, so the word itself is a 64-bit shift amount
+//   bit 6      the dword ends a tier or is a (scale, sigma) pair: the one flag the summing loop tests
+//   bit 7      ends a tier
+//   bit 8      is the (scale, sigma) pair of the next tier in order
+//   bits 9-16  byte offset of the dword's 512-byte table group in LDS (the zero table past the planes)
+constexpr uint32_t kSchedSpecial = 1u << 6;
+constexpr uint32_t kSchedLast = 1u << 7;
+constexpr uint32_t kSchedPair = 1u << 8;
+constexpr uint32_t kSchedBase = 0x1fe00u;
+struct ScoreSched {
+  uint32_t d[kSchedMax];
+};
 
 struct RecUnit {
   uint4 c[kUnit];
@@ -111,8 +127,9 @@ __device__ __forceinline__ uint32_t unit_word(const RecUnit &b, int k) {
   return (k & 3) == 0 ? c.x : (k & 3) == 1 ? c.y : (k & 3) == 2 ? c.z : c.w;
 }
 
-// The 8 LUT entries of one record dword: byte j's high nibble indexes the table at lb + 128 j, its low
-// nibble the table at lb + 128 j + 64 (tables of 16 int32 = 64 bytes, nibble * 4 = byte offset).
+// The 8 LUT entries of one record dword x whose 512-byte table group starts at byte lb: byte j's high
+// nibble indexes the table at lb + 128 j, its low nibble the table at lb + 128 j + 64 (tables of 16 int32
+// = 64 bytes, nibble * 4 = byte offset).
 __device__ __forceinline__ void lookup8(const char *lutb, uint32_t x, uint32_t lb, int32_t (&v)[8]) {
   uint32_t xh = (x >> 2) & 0x3c3c3c3cu, xl = (x << 2) & 0x3c3c3c3cu;
   // opaque to the optimiser, so each byte stays a byte-select operand of the address add (SDWA) instead
@@ -125,164 +142,149 @@ __device__ __forceinline__ void lookup8(const char *lutb, uint32_t x, uint32_t l
   }
 }
 
-template <bool HALF>
+template <bool HALF, int TT>
 __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     const int32_t *__restrict__ pos, const float *__restrict__ qc, const void *__restrict__ Lin, int LW,
-    const float *__restrict__ qsum, const float *__restrict__ qn2, const uint8_t *__restrict__ rec, int RB, int soff,
-    TierArgs ta, const int32_t *__restrict__ ncnt, int64_t N, int64_t B, int K, float *__restrict__ est,
-    float *__restrict__ sdo) {
+    const float *__restrict__ qsum, const float *__restrict__ qn2, const uint8_t *__restrict__ rec, int RB, int U,
+    TierArgs ta, ScoreSched sched, const int32_t *__restrict__ ncnt, int64_t N, int64_t B, int K,
+    float *__restrict__ est, float *__restrict__ sdo) {
+  // the table comes first in LDS (no static LDS), so a schedule offset is an LDS address as it stands
   extern __shared__ int32_t smem[];
-  int32_t *lut = smem;                                                  // [LW] fixed-point table + zero table
-  const int nw = soff / 4;                                              // plane dwords
-  const int U = (nw + ta.T + kUD - 1) / kUD;                            // units per record (planes + pairs)
-  uint32_t *meta = reinterpret_cast<uint32_t *>(smem + LW + kZeroBytes / 4);  // [U * kUD]
-  float *tf = reinterpret_cast<float *>(meta + U * kUD);                // [T][4]: delta, mid, qsum, qn2
-  int64_t *acct = reinterpret_cast<int64_t *>(tf + 4 * FVS_MAX_TIERS);  // [T][threads] tier sums
-  uint32_t *ssw = reinterpret_cast<uint32_t *>(acct + ta.T * kScoreThreads);  // [T][threads] (scale, sigma)
-  int32_t *rows = reinterpret_cast<int32_t *>(ssw + ta.T * kScoreThreads);  // [K]
-  __shared__ float red[kScoreThreads / FVS_WAVE];
-  __shared__ int sexp;
+  int32_t *lut = smem;                                                  // [LW] fixed-point tables + zero table
+  float *tf = reinterpret_cast<float *>(smem + LW + kZeroBytes / 4);    // [T][4]: delta, mid, qsum, qn2
+  float *red = tf + 4 * FVS_MAX_TIERS;                                  // [waves] exponent reduction
+  int32_t *rows = reinterpret_cast<int32_t *>(red + kScoreThreads / FVS_WAVE);  // [K]
 
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
   const int T = ta.T;
 
-  // 1. fixed-point exponent of this query's table (vectorised passes over the table)
-  float m = 0.f;
-  if (HALF) {
-    const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
-#pragma unroll 4
-    for (int i = tid; i < LW / 8; i += kScoreThreads) {
-      const uint4 v = L4[i];
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  // 1. every global read of the set-up is issued at once: the query's table (one pass, held in registers),
+  //    its candidate rows, its tier constants, and the first unit of this lane's first record
+  const int nvec = HALF ? LW / 8 : LW / 4;  // 16-byte vectors of the table: 8 halves or 4 floats each
+  const uint4 *L4 = reinterpret_cast<const uint4 *>(Lin) + q * nvec;
+  uint4 lv[kSetupVec];
 #pragma unroll
-      for (int u = 0; u < 4; u++)
-        m = fmaxf(m, fmaxf(fabsf(fvs_h2f((uint16_t)(w4[u] & 0xffffu))), fabsf(fvs_h2f((uint16_t)(w4[u] >> 16)))));
-    }
-  } else {
-    const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
-#pragma unroll 4
-    for (int i = tid; i < LW / 4; i += kScoreThreads) {
-      const float4 v = L4[i];
-      m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
+  for (int c = 0; c < kSetupVec; c++)
+    if (tid + kScoreThreads * c < nvec) lv[c] = L4[tid + kScoreThreads * c];
+  const int lim = ncnt ? min(ncnt[q], K) : K;
+  for (int i = tid; i < K; i += kScoreThreads)
+    rows[i] = (int32_t)min(max((int64_t)pos[q * (int64_t)K + i], (int64_t)0), N - 1);
+  float tq0 = 0.f, tq1 = 0.f;
+  if (tid < T) {
+    tq0 = qsum[(int64_t)tid * B + q];
+    tq1 = qn2[(int64_t)tid * B + q];
   }
+  const int RB16 = RB / 16;
+  RecUnit ub0, ub1;
+  {
+    const int64_t r0 = tid < lim ? min(max((int64_t)pos[q * (int64_t)K + tid], (int64_t)0), N - 1) : 0;
+    load_unit(ub0, rec, r0, RB16, 0);
+  }
+
+  // 2. fixed-point exponent of the table, then the integer table, zero table and per-tier constants
+  constexpr int kPer = HALF ? 8 : 4;  // entries per vector
+  auto entry = [&](const uint4 &v, int u) {  // entry u of a vector (u static)
+    const int d = HALF ? u >> 1 : u;
+    const uint32_t x = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+    return HALF ? fvs_h2f((uint16_t)((u & 1) ? x >> 16 : x & 0xffffu)) : __uint_as_float(x);
+  };
+  float m = 0.f;
+#pragma unroll
+  for (int c = 0; c < kSetupVec; c++)
+    if (tid + kScoreThreads * c < nvec) {
+#pragma unroll
+      for (int u = 0; u < kPer; u++) m = fmaxf(m, fabsf(entry(lv[c], u)));
+    }
   m = fvs_wave_max(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
-  // candidate rows of this query, staged while the reduction settles
-  const int lim = ncnt ? min(ncnt[q], K) : K;
-  for (int i = tid; i < K; i += kScoreThreads) rows[i] = (int32_t)min(max((int64_t)pos[q * (int64_t)K + i], (int64_t)0), N - 1);
   __syncthreads();
-  if (tid == 0) {
+  int s;
+  {
     float mm = red[0];
 #pragma unroll
     for (int w = 1; w < kScoreThreads / FVS_WAVE; w++) mm = fmaxf(mm, red[w]);
     int E = 0;
     (void)frexpf(mm, &E);
-    sexp = max(0, E - 3);
+    s = max(0, E - 3);
   }
-  __syncthreads();
-  const int s = sexp;
-
-  // 2. integer LUT, zero table, per-dword descriptors, per-tier constants
-  if (HALF) {
-    const uint4 *L4 = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(Lin) + q * LW);
-#pragma unroll 4
-    for (int i = tid; i < LW / 8; i += kScoreThreads) {
-      const uint4 v = L4[i];
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        lut[8 * i + 2 * u] = (int32_t)rintf(ldexpf(fvs_h2f((uint16_t)(w4[u] & 0xffffu)), 24 - s));
-        lut[8 * i + 2 * u + 1] = (int32_t)rintf(ldexpf(fvs_h2f((uint16_t)(w4[u] >> 16)), 24 - s));
-      }
-    }
-  } else {
-    const float4 *L4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Lin) + q * LW);
-#pragma unroll 4
-    for (int i = tid; i < LW / 4; i += kScoreThreads) {
-      const float4 v = L4[i];
-      lut[4 * i + 0] = (int32_t)rintf(ldexpf(v.x, 24 - s));
-      lut[4 * i + 1] = (int32_t)rintf(ldexpf(v.y, 24 - s));
-      lut[4 * i + 2] = (int32_t)rintf(ldexpf(v.z, 24 - s));
-      lut[4 * i + 3] = (int32_t)rintf(ldexpf(v.w, 24 - s));
+  for (int c = 0; c < kSetupVec; c++) {
+    const int i = tid + kScoreThreads * c;
+    if (i < nvec) {
+#pragma unroll
+      for (int u = 0; u < kPer; u++) lut[kPer * i + u] = (int32_t)rintf(ldexpf(entry(lv[c], u), 24 - s));
     }
   }
   for (int i = tid; i < kZeroBytes / 4; i += kScoreThreads) lut[LW + i] = 0;
-  for (int w = tid; w < U * kUD; w += kScoreThreads) {
-    uint32_t d = (uint32_t)LW * 4u;  // past the planes: the zero table, weight 1, never the end of a tier
-    if (w >= nw && w < nw + T) d |= kMetaPair | ((uint32_t)(w - nw) << 20);
-    if (w < nw) {
-      const int byte = 4 * w;
-      for (int t = 0; t < T; t++) {
-        const int len = ta.bits[t] * ta.kb[t];
-        if (byte >= ta.toff[t] && byte < ta.toff[t] + len) {
-          const int rel = byte - ta.toff[t];
-          const int p = rel / ta.kb[t];
-          const int j0 = rel - p * ta.kb[t];
-          const uint32_t base = (uint32_t)(ta.loff[t] + 32 * j0) * 4u;  // byte offset in the table
-          const uint32_t shift = (uint32_t)(ta.bits[t] - 1 - p);
-          const uint32_t last = (byte + 4 == ta.toff[t] + len) ? kMetaLast : 0u;
-          d = base | (shift << 17) | last | ((uint32_t)t << 20);
-        }
-      }
-    }
-    meta[w] = d;
-  }
 #pragma unroll
   for (int t = 0; t < FVS_MAX_TIERS; t++) {
     if (t < T && tid == t) {
       tf[4 * t + 0] = ta.delta[t];
       tf[4 * t + 1] = ta.mid[t];
-      tf[4 * t + 2] = qsum[(int64_t)t * B + q];
-      tf[4 * t + 3] = qn2[(int64_t)t * B + q];
+      tf[4 * t + 2] = tq0;
+      tf[4 * t + 3] = tq1;
     }
   }
   __syncthreads();
 
-  // 3. candidates: lane `tid` scores slots tid, tid + threads, ...; each record is streamed in units of
-  //    kUnit 16-byte chunks, double-buffered in registers, and the lookups of dword k + 1 are issued
-  //    before the entries of dword k are summed
-  const int RB16 = RB / 16;
+  // 3. candidates: lane `tid` scores slots tid, tid + 256, ...; each record is streamed in units of kUnit
+  //    16-byte chunks, double-buffered in registers, and the lookups of dword k + 1 are issued before the
+  //    entries of dword k are summed. The tier sums and (scale, sigma) words stay in registers: tiers end,
+  //    and their pairs come, in tier order, so each is shifted into a register queue of TT entries, where
+  //    tier t ends up at position TT - 1 - t.
   const int nround = (K + kScoreThreads - 1) / kScoreThreads;
-  const int S = nround * U;
   const char *lutb = reinterpret_cast<const char *>(lut);
   const float qcq = qc[q];
-  const int lane = tid & (FVS_WAVE - 1);
-  RecUnit ub0, ub1;
   int64_t acc = 0;
+  int64_t tsum[TT];
+  uint32_t tss[TT];
+#pragma unroll
+  for (int t = 0; t < TT; t++) {
+    tsum[t] = 0;
+    tss[t] = 0u;
+  }
   // every step issues the same unconditional loads (the last one reloads its own unit), so the wait
   // before a unit is summed never has to drain the prefetch of the next one
-  auto row_of = [&](int m) {
-    const int r = rows[min(m, K - 1)];
-    return m < lim ? r : 0;
+  auto row_of = [&](int mm) {
+    const int r = rows[min(mm, K - 1)];
+    return mm < lim ? r : 0;
   };
-  auto step = [&](int sq, const RecUnit &cur, RecUnit &nxt) {
-    const int i = sq / U, u = sq - i * U;
+  // step (i, u): sum unit u of the record of slot tid + 256 i; (ni, nu): the next step, prefetched
+  auto step = [&](int i, int u, int ni, int nu, const RecUnit &cur, RecUnit &nxt) {
     const int mm = tid + kScoreThreads * i;
-    const uint32_t mv = meta[u * kUD + (lane & (kUD - 1))];
-    {
-      const int sq1 = min(sq + 1, S - 1);
-      const int i1 = sq1 / U, u1 = sq1 - i1 * U;
-      load_unit(nxt, rec, row_of(tid + kScoreThreads * i1), RB16, u1);
-    }
+    // the unit's descriptors, fetched together: one scalar-load wait per unit (it also waits for LDS)
+    uint32_t sd[kUD];
+#pragma unroll
+    for (int k = 0; k < kUD; k++) sd[k] = sched.d[u * kUD + k];
+#pragma unroll
+    for (int k = 0; k < kUD; k++) asm volatile("" : "+s"(sd[k]));
+    load_unit(nxt, rec, row_of(tid + kScoreThreads * ni), RB16, nu);
     // wave-uniform: skip waves whose lanes are all past the candidate list
     if (kScoreThreads * i + (tid & ~(FVS_WAVE - 1)) < lim) {
       int32_t va[8], vb[8];
-      lookup8(lutb, unit_word(cur, 0), __builtin_amdgcn_readlane(mv, 0) & 0x1ffffu, va);
+      lookup8(lutb, unit_word(cur, 0), sd[0] & kSchedBase, va);
 #pragma unroll
       for (int k = 0; k < kUD; k++) {
         int32_t(&vc)[8] = (k & 1) ? vb : va;
         int32_t(&vn)[8] = (k & 1) ? va : vb;
-        if (k + 1 < kUD) lookup8(lutb, unit_word(cur, k + 1), __builtin_amdgcn_readlane(mv, k + 1) & 0x1ffffu, vn);
-        const uint32_t mt = __builtin_amdgcn_readlane(mv, k);
+        if (k + 1 < kUD) lookup8(lutb, unit_word(cur, k + 1), sd[k + 1] & kSchedBase, vn);
+        const uint32_t dk = sd[k];
         const int32_t part = vc[0] + vc[1] + vc[2] + vc[3] + vc[4] + vc[5] + vc[6] + vc[7];
-        acc += (int64_t)part << ((mt >> 17) & 7u);
-        if (mt & kMetaLast) {
-          acct[((mt >> 20) & 7u) * kScoreThreads + tid] = acc;
-          acc = 0;
+        acc += (int64_t)part << (dk & 63u);
+        if (dk & kSchedSpecial) {
+          if (dk & kSchedLast) {
+#pragma unroll
+            for (int t = TT - 1; t > 0; t--) tsum[t] = tsum[t - 1];
+            tsum[0] = acc;
+            acc = 0;
+          }
+          if (dk & kSchedPair) {
+#pragma unroll
+            for (int t = TT - 1; t > 0; t--) tss[t] = tss[t - 1];
+            tss[0] = unit_word(cur, k);
+          }
         }
-        if (mt & kMetaPair) ssw[((mt >> 20) & 7u) * kScoreThreads + tid] = unit_word(cur, k);
       }
     }
     if (u == U - 1 && mm < K) {
@@ -293,26 +295,78 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
       } else {
         float e = qcq, var = 0.f;
 #pragma unroll
-        for (int t = 0; t < FVS_MAX_TIERS; t++) {
-          if (t < T) {
-            float a = ldexpf((float)acct[t * kScoreThreads + tid], s - 24);
-            a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
-            const uint32_t sw = ssw[t * kScoreThreads + tid];
-            const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
-            e = __builtin_fmaf(a, sc, e);
-            var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
-          }
+        for (int t = 0; t < TT; t++) {  // tier t sits at queue position TT - 1 - t
+          float a = ldexpf((float)tsum[TT - 1 - t], s - 24);
+          a = tf[4 * t] * __builtin_fmaf(-tf[4 * t + 1], tf[4 * t + 2], a);
+          const uint32_t sw = tss[TT - 1 - t];
+          const float sc = fvs_h2f((uint16_t)(sw & 0xffffu)), sg = fvs_h2f((uint16_t)(sw >> 16));
+          e = __builtin_fmaf(a, sc, e);
+          var = __builtin_fmaf(tf[4 * t + 3] * sg, sg, var);
         }
         est[o] = e;
         sdo[o] = sqrtf(var);
       }
     }
   };
-  load_unit(ub0, rec, row_of(tid), RB16, 0);
+  const int S = nround * U;
+  int ci = 0, cu = 0;  // the step about to run
+  auto advance = [&](int &i, int &u) {
+    if (++u == U) {
+      u = 0;
+      ++i;
+    }
+  };
   for (int sq = 0; sq < S; sq += 2) {
-    step(sq, ub0, ub1);
-    if (sq + 1 < S) step(sq + 1, ub1, ub0);
+    int ni = ci, nu = cu;
+    advance(ni, nu);
+    if (sq + 1 >= S) {  // the last step reloads its own unit
+      ni = ci;
+      nu = cu;
+    }
+    step(ci, cu, ni, nu, ub0, ub1);
+    if (sq + 1 < S) {
+      int mi = ni, mu = nu;
+      advance(mi, mu);
+      if (sq + 2 >= S) {
+        mi = ni;
+        mu = nu;
+      }
+      step(ni, nu, mi, mu, ub1, ub0);
+      ci = mi;
+      cu = mu;
+    }
   }
+}
+
+// The schedule of a record layout (see ScoreSched): plane dwords look up their tier's tables with the
+// plane's weight, the T (scale, sigma) dwords after the planes and the padding up to whole units look up
+// the zero table with weight 1.
+int build_sched(const TierArgs &ta, int nw, int U, int LW, ScoreSched *sc) {
+  if (U * kUD > kSchedMax) return FVS_E_CAPACITY;
+  const uint32_t zero = (uint32_t)LW * 4u;
+  if ((zero & ~kSchedBase) != 0) return FVS_E_SHAPE;
+  for (int w = 0; w < U * kUD; w++) {
+    uint32_t d = zero;
+    if (w >= nw && w < nw + ta.T) d |= kSchedSpecial | kSchedPair;
+    if (w < nw) {
+      const int byte = 4 * w;
+      for (int t = 0; t < ta.T; t++) {
+        const int len = ta.bits[t] * ta.kb[t];
+        if (byte >= ta.toff[t] && byte < ta.toff[t] + len) {
+          const int rel = byte - ta.toff[t];
+          const int p = rel / ta.kb[t];
+          const int j0 = rel - p * ta.kb[t];
+          const uint32_t base = (uint32_t)(ta.loff[t] + 32 * j0) * 4u;  // byte offset of the dword's table group
+          if ((base & ~kSchedBase) != 0) return FVS_E_SHAPE;
+          d = base | (uint32_t)(ta.bits[t] - 1 - p);
+          if (byte + 4 == ta.toff[t] + len) d |= kSchedSpecial | kSchedLast;
+        }
+      }
+    }
+    sc->d[w] = d;
+  }
+  for (int w = U * kUD; w < kSchedMax; w++) sc->d[w] = zero;
+  return FVS_OK;
 }
 
 int fill_tiers(int T, const int32_t *tiers, const float *deltas, const int32_t *toff, TierArgs *ta, int D_limit) {
@@ -356,7 +410,8 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
                              const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB,
                              int32_t soff, int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff,
                              const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream) {
-  if (B < 0 || K <= 0 || N <= 0 || LW <= 0 || LW > 16384 || LW % 16 != 0) return FVS_E_ARG;
+  // LW = 16 entries per 4 coordinates, in whole 512-byte table groups (tiers are whole 32-coordinate blocks)
+  if (B < 0 || K <= 0 || N <= 0 || LW <= 0 || LW > 16384 || LW % 128 != 0) return FVS_E_ARG;
   if (RB <= 0 || RB % 16 != 0 || soff <= 0 || soff % 4 != 0) return FVS_E_ARG;
   if (!toff || !deltas) return FVS_E_ARG;
   TierArgs ta;
@@ -373,15 +428,34 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
   if (K > 4096) return FVS_E_CAPACITY;
   const int units = (soff / 4 + T + kUD - 1) / kUD;
-  const size_t shm = (size_t)LW * 4 + kZeroBytes + (size_t)units * kUD * 4 + 4 * FVS_MAX_TIERS * 4 +
-                     (size_t)kScoreThreads * T * (8 + 4) + (size_t)K * 4;
+  ScoreSched sched;
+  e = build_sched(ta, soff / 4, units, LW, &sched);
+  if (e) return e;
+  const size_t shm = (size_t)LW * 4 + kZeroBytes + 4 * FVS_MAX_TIERS * 4 + kScoreThreads / FVS_WAVE * 4 +
+                     (size_t)K * 4;
   if (shm > 160 * 1024 - 64) return FVS_E_CAPACITY;
   hipStream_t st = (hipStream_t)stream;
+  // one instantiation per tier count, so the tier queues have a static size
+  auto launch = [&](auto HALF_, auto TT_) {
+    hipLaunchKernelGGL((k_lut_score<decltype(HALF_)::value, decltype(TT_)::value>), dim3((unsigned)B),
+                       dim3(kScoreThreads), shm, st, pos, qc, L, LW, qsum, qn2, rec, RB, units, ta, sched, ncnt, N, B,
+                       K, est, sd);
+  };
+  auto by_t = [&](auto HALF_) {
+    switch (T) {
+      case 1: launch(HALF_, std::integral_constant<int, 1>{}); break;
+      case 2: launch(HALF_, std::integral_constant<int, 2>{}); break;
+      case 3: launch(HALF_, std::integral_constant<int, 3>{}); break;
+      case 4: launch(HALF_, std::integral_constant<int, 4>{}); break;
+      case 5: launch(HALF_, std::integral_constant<int, 5>{}); break;
+      case 6: launch(HALF_, std::integral_constant<int, 6>{}); break;
+      case 7: launch(HALF_, std::integral_constant<int, 7>{}); break;
+      default: launch(HALF_, std::integral_constant<int, 8>{}); break;
+    }
+  };
   if (half)
-    hipLaunchKernelGGL(k_lut_score<true>, dim3((unsigned)B), dim3(kScoreThreads), shm, st, pos, qc, L, LW, qsum, qn2,
-                       rec, RB, soff, ta, ncnt, N, B, K, est, sd);
+    by_t(std::true_type{});
   else
-    hipLaunchKernelGGL(k_lut_score<false>, dim3((unsigned)B), dim3(kScoreThreads), shm, st, pos, qc, L, LW, qsum,
-                       qn2, rec, RB, soff, ta, ncnt, N, B, K, est, sd);
+    by_t(std::false_type{});
   return fvs_launch_status();
 }
