@@ -5,7 +5,9 @@ Same entry points and knobs as the reference (throughput/enginei8.py:29-122):
     I, reads, cand_ids = E.search(Qb, K, z, nprobe, k)
 The search is one hipGraph replay per (B, K, z, nprobe, k) followed by one host synchronisation on
 the exactness flags; flagged queries are recomputed by _fallback (rho = 1, beta = 1.5, a 65,536-entry
-buffer, an fp32 LUT and no delta rule), as in the reference. Every stage runs in libfvs kernels; the
+buffer, an fp32 LUT and no delta rule), as in the reference. A serving loop can keep the GPU busy
+through that synchronisation with submit / collect: two captured instances per key take turns, so
+batch i + 1 is queued before batch i's flags are read. Every stage runs in libfvs kernels; the
 two plain fp16 GEMMs (routing scores and the rotated tier queries) use torch's BLAS.
 
 The class attributes default to the final operating point of throughput/e_v3final.py:16,28-30
@@ -103,6 +105,8 @@ class EngineI8:
         self.meansN = (s1["means16"].float() * s1["inv_mnorm"][:, None]).half().contiguous()
         self.mnorm = (1.0 / s1["inv_mnorm"]).float().contiguous()
         self.graphs = {}
+        self._slot = {}      # key -> the graph instance (0 or 1) the next submit uses
+        self._pending = set()  # (key, instance) submitted and not yet collected
         self._side = None  # stream for the stage-2 tables (default priority)
         self.nbad = 0
         self.nbad2 = 0
@@ -234,12 +238,17 @@ class EngineI8:
     def search(self, Qb, K, z, nprobe, k, ret_est=False, ret_scores=False):
         """(I [B,k] ids, reads [B], cand_ids [B,K]) (+ scores [B,k] when ret_scores): the exact scores of
         the picks read in full precision, the stage-2 estimates of the surely-in ones."""
-        Qb = Qb.float().contiguous()
-        B = len(Qb)
-        key = (B, K, float(z), nprobe, k, self._knobs())
-        if key not in self.graphs:
+        return self.collect(self.submit(Qb, K, z, nprobe, k), ret_scores=ret_scores)
+
+    def _graph(self, key, inst, Qb):
+        """The captured search of `key`, instance `inst` (0 or 1): (graph, its query buffer, its outputs,
+        the pinned exactness flags, the event recorded after its replay). Captured on first use, with Qb
+        as the query values of the capture's runs."""
+        gk = (key, inst)
+        if gk not in self.graphs:
+            _, K, z, nprobe, k, _ = key
             qs = Qb.clone()
-            okh = torch.empty((B,), dtype=torch.bool, pin_memory=True)
+            okh = torch.empty((len(Qb),), dtype=torch.bool, pin_memory=True)
 
             def run():
                 outs = self._gpu(qs, K, z, nprobe, k)
@@ -247,42 +256,73 @@ class EngineI8:
                 return outs
 
             g, outs = capture(run)
-            self.graphs[key] = (g, qs, outs, okh.numpy(), torch.cuda.Event())
-        g, qs, (ok, I, nr, ids, sc, blas), okh, done = self.graphs[key]
+            self.graphs[gk] = (g, qs, outs, okh.numpy(), torch.cuda.Event())
+        return self.graphs[gk]
+
+    def submit(self, Qb, K, z, nprobe, k):
+        """Queue the search of one batch and return its ticket without waiting for the GPU. Successive
+        submits of one (B, K, z, nprobe, k) alternate between two graph instances, so at most two batches
+        of a key are in flight: a third submit before the first is collected raises RuntimeError."""
+        Qb = Qb.float().contiguous()
+        key = (len(Qb), K, float(z), nprobe, k, self._knobs())
+        inst = self._slot.get(key, 0)
+        if (key, inst) in self._pending:
+            raise RuntimeError("EngineI8.submit: two batches of this shape are in flight; collect the older one first")
+        g, qs, (ok, I, nr, ids, sc, blas), okh, done = self._graph(key, inst, Qb)
+        self._slot[key] = inst ^ 1
         qs.copy_(Qb)
         g.replay()
         done.record()
-        I, nr, ids, sc = _fresh(I, nr, ids, sc)  # runs while the host reads the flags
+        I, nr, ids, sc = _fresh(I, nr, ids, sc)  # the caller's copies, queued behind the replay
+        self._pending.add((key, inst))
+        return (key, inst, I, nr, ids, sc)
+
+    def collect(self, ticket, ret_scores=False):
+        """Wait for a submitted batch, recompute its flagged queries, and return what search returns."""
+        key, inst, I, nr, ids, sc = ticket
+        if (key, inst) not in self._pending:
+            raise RuntimeError("EngineI8.collect: this ticket was already collected")
+        g, qs, outs, okh, done = self.graphs[(key, inst)]
+        blas = outs[5]
         done.synchronize()
         if not okh.all():
             bad = np.nonzero(~okh)[0].astype(np.int64)
             nb = len(bad)
             self.nbad += nb
-            fg, sel, (a, b, c, s, ok2) = self._fallback_graph(key, qs, blas, padded_rows(nb))
+            fg, sel, (a, b, c, s, ok2) = self._fallback_graph(key, inst, qs, blas, padded_rows(nb))
             sel.copy_(torch.from_numpy(np.concatenate([bad, np.full(padded_rows(nb) - nb, bad[-1], np.int64)])))
             fg.replay()
-            bd = torch.from_numpy(bad).to(Qb.device)
+            bd = torch.from_numpy(bad).to(qs.device)
             I[bd], nr[bd], ids[bd], sc[bd] = a[:nb], b[:nb], c[:nb], s[:nb]
             self.nbad2 += int((~ok2[:nb]).sum())
+        # the instance is free again only now: its flags and fallback inputs are read above
+        self._pending.discard((key, inst))
         return (I, nr, ids, sc) if ret_scores else (I, nr, ids)
 
     def warm_fallbacks(self, B, K, z, nprobe, k, upto=64):
         """Capture the fallback graphs of 1, 2, 4, ... `upto` flagged rows of an already searched (B, K, z,
-        nprobe, k) ahead of time, so that no later search pays a capture (tens of milliseconds)."""
+        nprobe, k), for both graph instances, ahead of time, so that no later search pays a capture (tens
+        of milliseconds)."""
         key = (B, K, float(z), nprobe, k, self._knobs())
-        if key not in self.graphs:
+        if (key, 0) not in self.graphs and (key, 1) not in self.graphs:
             raise KeyError("warm_fallbacks: search this (B, K, z, nprobe, k) once first")
-        g, qs, outs, _, _ = self.graphs[key]
-        g.replay()  # the captures' warm-up runs read the main graph's outputs
-        nbp = 1
-        while nbp <= upto:
-            self._fallback_graph(key, qs, outs[5], nbp)
-            nbp *= 2
+        if self._pending:
+            raise RuntimeError("warm_fallbacks: collect the submitted batches first")
+        seed = self.graphs[(key, 0) if (key, 0) in self.graphs else (key, 1)][1]
+        for inst in (0, 1):
+            g, qs, outs, _, _ = self._graph(key, inst, seed)
+            qs.copy_(seed)
+            g.replay()  # the captures' warm-up runs read the main graph's outputs
+            nbp = 1
+            while nbp <= upto:
+                self._fallback_graph(key, inst, qs, outs[5], nbp)
+                nbp *= 2
 
-    def _fallback_graph(self, key, qs, blas, nbp):
-        """The captured fallback of nbp rows gathered (by `sel`) from the main graph's query and BLAS
-        buffers; it is replayed right after the main graph, so those hold the batch's values."""
-        fkey = ("fb", key, nbp)
+    def _fallback_graph(self, key, inst, qs, blas, nbp):
+        """The captured fallback of nbp rows gathered (by `sel`) from instance inst's query and BLAS
+        buffers; it is replayed after that instance's replay (and at most the other instance's), so those
+        hold the batch's values."""
+        fkey = ("fb", key, inst, nbp)
         if fkey not in self.graphs:
             sel = torch.zeros(nbp, dtype=torch.int64, device=qs.device)
             _, K, z, nprobe, k, _ = key

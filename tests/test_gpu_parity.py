@@ -172,6 +172,36 @@ def test_fallback_matches_oracle(env, oracle_mod):
     assert np.array_equal(npy(sc).view(np.uint32), out["scores"].view(np.uint32))
 
 
+def test_pipelined_submit_collect_matches_search(env):
+    """Two batches in flight, each with flagged queries (so the first batch's fallback runs after the
+    second batch's graph is queued), give the same results as one search at a time."""
+    E, Q = env["E"], env["Q"]
+    A, Bq = Q[:64].contiguous(), Q[64:128].contiguous()
+    old = E.MSZ
+    E.MSZ = K + 8
+    try:
+        ref = [E.search(x, K, Z_, NPROBE, KK, ret_scores=True) for x in (A, Bq)]
+        torch.cuda.synchronize()
+        nb0 = E.nbad
+        for rep in range(2):
+            ta = E.submit(A, K, Z_, NPROBE, KK)
+            tb = E.submit(Bq, K, Z_, NPROBE, KK)
+            with pytest.raises(RuntimeError):
+                E.submit(A, K, Z_, NPROBE, KK)  # a third batch of the shape while two are in flight
+            ra = E.collect(ta, ret_scores=True)
+            rb = E.collect(tb, ret_scores=True)
+            with pytest.raises(RuntimeError):
+                E.collect(ta)
+            torch.cuda.synchronize()
+            for got, want in ((ra, ref[0]), (rb, ref[1])):
+                for g, w in zip(got, want):
+                    assert np.array_equal(npy(g), npy(w)), f"rep {rep}"
+        assert E.nbad > nb0
+    finally:
+        E.MSZ = old
+        E.graphs.clear()
+
+
 def test_recall_and_pinned_host_rows(env):
     E, Q = env["E"], env["Q"]
     I, reads, ids = E.search(Q, K, Z_, NPROBE, KK)
