@@ -245,9 +245,82 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
   return prefix;
 }
 
+__device__ __forceinline__ uint64_t fvs_shfl_xor_u64(uint64_t x, int j) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, j, FVS_WAVE);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j, FVS_WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Sorts s[0..kk) (unique 64-bit keys) descending in place, kk <= 2 NT, with blockDim.x == NT. Wave w sorts
+// the run s[128 w, 128 w + 128) in registers (two keys per lane, element e * 64 + lane; a bitonic network
+// whose exchanges within a lane are register moves and across lanes shuffles; missing keys are 0, which
+// sorts last and equals any real key of 0, so the sorted values are the same either way) and writes it
+// back in place. Each key's final index is then its index in its own run plus, for every other run, the
+// number of that run's keys above it (a binary search in the sorted run).
+template <int NT>
+__device__ void fvs_block_sort_desc_u64(uint64_t *s, int kk) {
+  const int lane = threadIdx.x & (FVS_WAVE - 1), w = threadIdx.x / FVS_WAVE;
+  const int nreal = min(128, kk - 128 * w);  // keys in this wave's run (<= 0: no run)
+  uint64_t v[2];
+#pragma unroll
+  for (int e = 0; e < 2; e++) v[e] = e * 64 + lane < nreal ? s[128 * w + e * 64 + lane] : 0ull;
+  if (nreal > 0) {
+#pragma unroll
+    for (int k = 2; k <= 128; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        if (j == 64) {  // the pair (lane, 64 + lane): the lower index takes the larger key
+          const uint64_t hi = v[0] > v[1] ? v[0] : v[1], lo = v[0] > v[1] ? v[1] : v[0];
+          v[0] = hi;
+          v[1] = lo;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            const uint64_t p = fvs_shfl_xor_u64(v[e], j);
+            const int i = e * 64 + lane;
+            // descending blocks where (i & k) == 0; the lower index of a pair holds the block's larger key
+            const bool take_max = ((i & k) == 0) == ((i & j) == 0);
+            const bool gt = v[e] > p;
+            v[e] = take_max == gt ? v[e] : p;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; e++)
+    if (e * 64 + lane < nreal) s[128 * w + e * 64 + lane] = v[e];
+  __syncthreads();
+  const int R = (kk + 127) / 128;
+  int r[2];
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int i = e * 64 + lane;
+    r[e] = i;
+    if (i < nreal) {
+      for (int w2 = 0; w2 < R; w2++) {
+        if (w2 == w) continue;
+        const uint64_t *run = s + 128 * w2;
+        const int len = min(128, kk - 128 * w2);
+        int idx = 0;  // keys of run w2 above v[e]: the run is descending
+#pragma unroll
+        for (int step = 128; step > 0; step >>= 1)
+          if (idx + step <= len && run[idx + step - 1] > v[e]) idx += step;
+        r[e] += idx;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 2; e++)
+    if (e * 64 + lane < nreal) s[r[e]] = v[e];
+  __syncthreads();
+}
+
 // Top-kk of n unique 64-bit keys, sorted descending, into s[0..kk) (s holds pow2_ceil(kk) keys).
-// Requires kk <= n. The kk keys above the radix bound are gathered, then each is stored at its rank
-// among them: a count of the larger keys (two keys per thread) when kk <= 2 NT, a bitonic sort above.
+// Requires kk <= n. The kk keys above the radix bound are gathered, then sorted: by counting ranks up to
+// 64 keys, as runs of 128 sorted in registers and merged by rank (fvs_block_sort_desc_u64) up to 2 NT, by
+// a bitonic sort in LDS above.
 // Block of NT threads; cnt: 1 int of LDS.
 template <int NT = 256, typename F>
 __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist, int *sh, int *cnt) {
@@ -264,21 +337,17 @@ __device__ void fvs_block_topk_u64(F key, int n, int kk, uint64_t *s, int *hist,
     }
   }
   __syncthreads();
-  if (kk <= 2 * NT) {
-    // each thread places keys t and t + NT at their ranks (a count of the larger keys; every lane reads
-    // the same address per step: a broadcast)
+  if (kk <= 64) {
+    // a few keys: each thread < kk places its key at its rank, a count of the larger keys (every lane
+    // reads the same address per step: a broadcast)
     const uint64_t m0 = threadIdx.x < kk ? s[threadIdx.x] : 0ull;
-    const uint64_t m1 = threadIdx.x + NT < kk ? s[threadIdx.x + NT] : 0ull;
-    int r0 = 0, r1 = 0;
-    for (int t = 0; t < kk; t++) {
-      const uint64_t x = s[t];
-      r0 += x > m0 ? 1 : 0;
-      r1 += x > m1 ? 1 : 0;
-    }
+    int r0 = 0;
+    for (int t = 0; t < kk; t++) r0 += s[t] > m0 ? 1 : 0;
     __syncthreads();
     if (threadIdx.x < kk) s[r0] = m0;
-    if (threadIdx.x + NT < kk) s[r1] = m1;
     __syncthreads();
+  } else if (kk <= 2 * NT) {
+    fvs_block_sort_desc_u64<NT>(s, kk);
   } else {
     fvs_block_bitonic<uint64_t, true>(s, P);
   }
