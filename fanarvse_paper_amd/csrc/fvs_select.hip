@@ -5,6 +5,7 @@ namespace {
 
 constexpr int kMaxK = 4096;     // LDS capacity of the sorted top-K (dynamic)
 constexpr int kMaxN1 = 4096;
+constexpr int kStageT = 8192;   // threshold keys (n1 x MB) staged in LDS once; more are read per pass
 
 __device__ __forceinline__ int cell_blocks(const int32_t *off, int c) {
   const int s = off[c], e = off[c + 1];
@@ -17,12 +18,15 @@ constexpr int kSmallB = 64;
 
 // One block of NT threads per query. Valid values: bm[q][j][b], j < n1, b < blocks(probe[q][j]).
 // A probe id outside [0, NC) reads no offsets: its cell counts as empty, and the query's t0 becomes 1e30,
-// so its emit pass keeps nothing and its exactness flag (K <= cnt) is cleared.
+// so its emit pass keeps nothing and its exactness flag (K <= cnt) is cleared. With `staged`, the n1 x MB
+// keys are read from global memory once into LDS and the radix passes run over LDS.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, const int32_t *__restrict__ probe,
                                                   int npr, const int32_t *__restrict__ off, int NC, int n1, int MB,
-                                                  int r, float *__restrict__ t0, int32_t *__restrict__ cnt) {
-  __shared__ int nb[kMaxN1];
+                                                  int r, int staged, float *__restrict__ t0, int32_t *__restrict__ cnt) {
+  extern __shared__ uint32_t tdyn[];  // [n1] block counts, then [n1 x MB] keys when staged
+  int *nb = reinterpret_cast<int *>(tdyn);
+  uint32_t *keys = tdyn + n1;
   __shared__ int hist[256];
   __shared__ int sh[fvs_sh_ints(NT)];
   const int64_t q = blockIdx.x;
@@ -49,7 +53,15 @@ __global__ __launch_bounds__(NT) void k_threshold(const float *__restrict__ bm, 
   };
   const int kk = any_bad ? 0 : min(min(r, n), nv);
   float out = 1e30f;
-  if (kk > 0) out = fvs_unord32(fvs_block_kth<uint32_t, NT>(key, n, kk, hist, sh));
+  if (kk > 0) {
+    if (staged) {
+      for (int i = threadIdx.x; i < n; i += NT) keys[i] = key(i);
+      __syncthreads();
+      out = fvs_unord32(fvs_block_kth<uint32_t, NT>([&](int i) { return keys[i]; }, n, kk, hist, sh));
+    } else {
+      out = fvs_unord32(fvs_block_kth<uint32_t, NT>(key, n, kk, hist, sh));
+    }
+  }
   if (threadIdx.x == 0) {
     t0[q] = out;
     if (cnt) cnt[q] = 0;  // the emit pass's counter, zeroed here instead of by a fill launch
@@ -150,12 +162,15 @@ extern "C" int fvs_threshold(const float *bm, const int32_t *probe, int32_t npr,
   if ((int64_t)n1 * MB > (int64_t)1 << 30) return FVS_E_ARG;
   if (B == 0) return FVS_OK;
   if (!bm || !probe || !off || !t0) return FVS_E_ARG;
+  const int64_t n = (int64_t)n1 * MB;
+  const int staged = n <= kStageT ? 1 : 0;
+  const size_t shm = 4 * ((size_t)n1 + (staged ? (size_t)n : 0));
   if (B <= kSmallB)
-    hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), 0, (hipStream_t)stream, bm, probe, npr, off, NC,
-                       n1, MB, r, t0, cnt);
+    hipLaunchKernelGGL(k_threshold<1024>, dim3((unsigned)B), dim3(1024), shm, (hipStream_t)stream, bm, probe, npr, off,
+                       NC, n1, MB, r, staged, t0, cnt);
   else
-    hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, bm, probe, npr, off, NC,
-                       n1, MB, r, t0, cnt);
+    hipLaunchKernelGGL(k_threshold<256>, dim3((unsigned)B), dim3(256), shm, (hipStream_t)stream, bm, probe, npr, off, NC,
+                       n1, MB, r, staged, t0, cnt);
   return fvs_launch_status();
 }
 
