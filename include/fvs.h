@@ -238,6 +238,9 @@ int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int
  *   qsum, qn2 f32 [T, B]; rec u8 [N, RB]: tier t plane p at toff[t] + p*(d_t/8), then (scale, sigma)
  *   fp16 pairs per tier at soff + 4t; tiers i32 [T][3], deltas f32 [T], toff i32 [T] are HOST arrays.
  *   ncnt i32 [B] or NULL (score all K). est, sd f32 [B, K]; slots m >= ncnt[q] get (-1e30, 0).
+ *   Limits: LW % 128 == 0 (whole 512-byte table groups; LW = 4 d for tiers of whole 32-coordinate
+ *   blocks), K <= 4096, and the record's plane and pair dwords, rounded up to 32, at most 512
+ *   (FVS_E_CAPACITY otherwise: the per-dword schedule travels as a 2 KiB kernel argument).
  * Canonical arithmetic: each LUT entry is turned into the integer fx = rint(L * 2^(24-s)), with
  * s = max(0, E - 3) where max|L| of the query = f * 2^E, f in [0.5, 1) (frexp); the tier sums
  *   A_t = sum_p 2^(b-1-p) sum_j (fx[hi nibble] + fx[lo nibble]) are exact integers. Then, in f32:

@@ -81,6 +81,25 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_quantize_i8(n, 4, 0, n, n, n, n) == E_ARG                                       # R = 0
 
 
+def test_lut_score_layout_checks_need_no_gpu(L):
+    """fvs_lut_score refuses a table width that is not whole 512-byte groups, and a record whose per-dword
+    schedule (passed as a kernel argument) would exceed 512 dwords, before any launch: host buffers stand
+    in for the device pointers, which are never touched."""
+    E_ARG, E_CAP = -1, -3
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+
+    def call(LW, D, bits, RB):
+        tiers = (ctypes.c_int32 * 3)(0, D, bits)
+        deltas = (ctypes.c_float * 1)(1.0)
+        soff = D * bits // 8
+        toff = (ctypes.c_int32 * 1)(0)
+        return L.fvs_lut_score(p, p, p, 1, LW, p, p, p, 10, RB, soff, 1, tiers, deltas, toff, None, 1, 10, p, p, None)
+
+    assert call(LW=1552, D=388, bits=4, RB=208) == E_ARG      # LW % 128 (tiers are whole 32-coordinate blocks)
+    assert call(LW=16384, D=4096, bits=4, RB=2064) == E_CAP   # 513 dwords of planes and pair: past 512
+
+
 def test_wrappers_refuse_cpu_tensors(L):
     from fanarvse_paper_amd import _lib
 
