@@ -48,3 +48,27 @@ def test_select_matches_oracle(oracle_mod, K, M, B):
             if g.dtype == np.float32:
                 g, w = g.view(np.uint32), w.view(np.uint32)
             assert np.array_equal(g, w), (name, kd, delta)
+
+
+@pytest.mark.parametrize("B", [37, 80])          # 1024-thread blocks (batches <= 64), 256-thread blocks
+@pytest.mark.parametrize("n1,MB", [(51, 35), (300, 40)])  # n1 x MB = 1,785 (keys staged in LDS), 12,000 (read per pass)
+def test_threshold_matches_oracle(oracle_mod, n1, MB, B):
+    """t0 from the first-pass block maxima, against the oracle, with the keys staged in LDS and with them
+    read from global memory in each radix pass (more than 8,192 keys per query); runs of tied maxima and
+    cells shorter than MB blocks, including empty ones."""
+    print(f"\n[gpu threshold] B={B} n1={n1} MB={MB}", flush=True)
+    rng = np.random.default_rng(n1 * 7 + B)
+    NC = 700
+    rows = rng.integers(0, 32 * (MB - 2), NC)
+    rows[:5] = 0  # empty cells
+    off = np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)
+    npr = n1 + 3
+    probe = np.stack([rng.permutation(NC)[:npr] for _ in range(B)]).astype(np.int32)
+    bm = rng.standard_normal((B, n1, MB)).astype(np.float32)
+    bm[::2] = np.round(bm[::2] * 4) / 4  # ties
+    for r in (1, 240, 3000):
+        got = _lib.threshold(torch.from_numpy(bm).cuda(), torch.from_numpy(probe).cuda(), torch.from_numpy(off).cuda(),
+                             n1, MB, r)
+        torch.cuda.synchronize()
+        want = oracle_mod.threshold(bm, probe, off, n1, MB, r)
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32)), r
