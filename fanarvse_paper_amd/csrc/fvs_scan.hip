@@ -243,8 +243,8 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 // resident workgroup hides more of each item's fixed latencies (pair staging, first tile, flush) than
 // overlapping the next tile's MFMAs with the current epilogue inside one wave did at two per CU.
 // The item's pairs are processed in chunks of up to kMeta queries; a chunk whose candidates overflow a
-// wave's region is dropped and scanned again with half as many queries, down to 16 queries, whose
-// 16 x 64 candidates per wave always fit.
+// wave's region is dropped and scanned again with half as many queries, down to 8 queries, whose
+// 8 x 64 = 512 candidates per wave always fit in its 640 slots.
 template <int NW>
 struct EmitStage {
   int acc[NW][kCapE];       // dot products of the staged elements; the estimate after the exact test
@@ -273,6 +273,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
   constexpr int NT = 64 * NW;     // threads of the workgroup
   constexpr int kSt = 8 / NW;     // MFMA steps of a query tile each wave requests
   static_assert(kNB == 2, "the epilogue pairs the ballots of two blocks");
+  static_assert(8 * 64 <= kCapE, "an 8-query chunk must fit a wave's region");
   static_assert(NW == 4, "an item's 256 rows are one pass of four waves");
   __shared__ __align__(16) Meta meta[kMeta];
   __shared__ __align__(16) float Tl[kMeta + 32];
@@ -496,7 +497,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
 
     // The item's pairs in chunks of csz queries (kMeta at first), each staged, scanned and flushed. A chunk
     // whose candidates overflow a wave's region is dropped and scanned again with half as many queries, down
-    // to 16, whose at most 16 x 64 candidates per wave always fit.
+    // to 8, whose at most 8 x 64 = 512 candidates per wave always fit in kCapE = 640 slots.
     bool pq_ok = true;  // pq holds the first kMeta pair ids of the item
     for (int c0 = 0, csz = kMeta;;) {
       nq = min(csz, qn - c0);
@@ -533,7 +534,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
       bool over = false;
 #pragma unroll
       for (int ww = 0; ww < NW; ww++) over = over || S.n[ww] > kCapE;
-      if (over) {  // csz >= 32 here: a 16-query chunk stages at most 16 x 64 = 1024 < kCapE per wave
+      if (over) {  // csz >= 16 here: an 8-query chunk stages at most 8 x 64 = 512 <= kCapE per wave
         csz >>= 1;   // the same first pair again, with half the queries
         pq_ok = false;
         continue;
