@@ -4,7 +4,7 @@
 Workload: 1M x 1536 fp16 unit vectors from the 1,024-cluster power-law generator, a batch of 2,000
 queries, k = 10. A step is one search of the whole batch (hipGraph replay of route -> int8 stage 1 ->
 LUT stage 2 -> error bars -> exact refine, plus the exactness-flag sync and any fallback), submitted
-two deep through EngineI8.submit / collect so the next batch is queued before the flag sync.
+through EngineI8.submit / collect with NINST (3) batches in flight, each on its own stream.
 The operating point is the fastest (n_p, K) of --points whose recall@10 reaches --target.
 
 Prints one JSON line: value = queries/s of the whole job (inputs resident in HBM), the roofline of the
@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=2000)
     ap.add_argument("--k", type=int, default=10)
     ap.add_argument("--z", type=float, default=1.25)
+    ap.add_argument("--inflight", type=int, default=0,
+                    help="batches in flight through EngineI8.submit / collect (0: the engine's NINST)")
     ap.add_argument("--points", default="352:175:3072,512:300:4096,768:400:4096,1024:400:4096",
                     help="n_p:K:M operating points (the reference's grid, throughput/e_v3final.py:31)")
     ap.add_argument("--target", type=float, default=0.99)
@@ -110,6 +112,8 @@ def main():
     torch.cuda.synchronize()
     log(f"index built in {time.time() - t:.1f}s: tiers {code['TS']} record {code['RB']} B")
     E = EngineI8(s1, code, Z, zs, Vr, H=X)
+    if args.inflight > 0:
+        E.NINST = args.inflight
 
     # ---- operating point: fastest point reaching the recall target on the tuning draw
     pts = [tuple(int(v) for v in p.split(":")) for p in args.points.split(",")]
@@ -119,7 +123,7 @@ def main():
         E.nbad = 0
         I, reads, ids = E.search(Qt, K, args.z, nprobe, args.k)
         rec = metrics.recall(I.cpu().numpy(), GTt, args.k)
-        pipelined(E, [Qt, Qt], K, args.z, nprobe, args.k)  # captures the second graph instance
+        pipelined(E, [Qt] * E.NINST, K, args.z, nprobe, args.k)  # captures the other graph instances
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         pipelined(E, [Qt] * 3, K, args.z, nprobe, args.k)
@@ -137,9 +141,9 @@ def main():
     nprobe, K = best["nprobe"], best["K"]
     E.MSZ = best["M"]
 
-    # ---- timed region: batches submitted two deep (the next batch is queued before the previous one's
+    # ---- timed region: batches submitted NINST deep (the next batches run before the previous one's
     # exactness flags are read on the host), as a serving loop runs them
-    pipelined(E, [Q] * max(args.warmup, 2), K, args.z, nprobe, args.k)
+    pipelined(E, [Q] * max(args.warmup, E.NINST), K, args.z, nprobe, args.k)  # every instance captured
     E.nbad = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -199,12 +203,12 @@ def main():
 
 
 def pipelined(E, batches, K, z, nprobe, k):
-    """Search the batches in order with two in flight (EngineI8.submit / collect): batch i + 1 is queued
+    """Search the batches in order with E.NINST in flight (EngineI8.submit / collect): batch i + 1 is queued
     on the GPU before batch i's exactness flags are read. Returns the last batch's (I, reads, ids)."""
     tickets, res = [], None
     for Qb in batches:
         tickets.append(E.submit(Qb, K, z, nprobe, k))
-        if len(tickets) == 2:
+        if len(tickets) == E.NINST:
             res = E.collect(tickets.pop(0))
     while tickets:
         res = E.collect(tickets.pop(0))

@@ -6,8 +6,9 @@ Same entry points and knobs as the reference (throughput/enginei8.py:29-122):
 The search is one hipGraph replay per (B, K, z, nprobe, k) followed by one host synchronisation on
 the exactness flags; flagged queries are recomputed by _fallback (rho = 1, beta = 1.5, a 65,536-entry
 buffer, an fp32 LUT and no delta rule), as in the reference. A serving loop can keep the GPU busy
-through that synchronisation with submit / collect: two captured instances per key take turns, so
-batch i + 1 is queued before batch i's flags are read. Every stage runs in libfvs kernels; the
+through that synchronisation with submit / collect: NINST (3) captured instances per key take turns,
+each replayed on its own stream, so the next batches run on the GPU alongside batch i while batch i's
+flags are read. Every stage runs in libfvs kernels; the
 two plain fp16 GEMMs (routing scores and the rotated tier queries) use torch's BLAS.
 
 The class attributes default to the final operating point of throughput/e_v3final.py:16,28-30
@@ -38,9 +39,10 @@ def pairs_fast(probe, NC, QM, scale=None):
     return qid, coff, ccnt, qcp, qrank
 
 
-def capture(fn):
+def capture(fn, stream=None):
     """Run fn three times on a side stream (allocations and lazy set-up happen there), then capture one
-    more run into a hipGraph. Returns (graph, fn's outputs)."""
+    more run into a hipGraph (on `stream` when given: the library GEMMs' workspaces belong to the stream
+    they are captured on). Returns (graph, fn's outputs)."""
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(st):
@@ -48,7 +50,7 @@ def capture(fn):
             fn()
     torch.cuda.current_stream().wait_stream(st)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=stream):
         outs = fn()
     return g, outs
 
@@ -89,6 +91,7 @@ class EngineI8:
     DELTA = 0.07
     LUTH = True
     CB = 8  # 32-row blocks per stage-1 work item (the kernel stages 4 at a time in LDS)
+    NINST = 3  # graph instances per search shape: batches that submit / collect keep in flight
 
     def __init__(self, s1, code, Z, zs, Vr, H=None):
         if self.BN != 32:
@@ -241,9 +244,12 @@ class EngineI8:
         return self.collect(self.submit(Qb, K, z, nprobe, k), ret_scores=ret_scores)
 
     def _graph(self, key, inst, Qb):
-        """The captured search of `key`, instance `inst` (0 or 1): (graph, its query buffer, its outputs,
-        the pinned exactness flags, the event recorded after its replay). Captured on first use, with Qb
-        as the query values of the capture's runs."""
+        """The captured search of `key`, instance `inst` (0 .. NINST - 1): (graph, its query buffer, its outputs,
+        the pinned exactness flags, the event recorded after its replay and output copies, the stream it
+        is replayed on). Captured on first use, with Qb as the query values of the capture's runs.
+        The instances of a key may run at the same time: each has its own buffers (its own graph memory
+        pool) and is captured on streams of its own, main branch and side branch, so that the library
+        GEMMs of two instances do not share a workspace."""
         gk = (key, inst)
         if gk not in self.graphs:
             _, K, z, nprobe, k, _ = key
@@ -255,25 +261,36 @@ class EngineI8:
                 okh.copy_(outs[0], non_blocking=True)  # the flags reach the host inside the graph
                 return outs
 
-            g, outs = capture(run)
-            self.graphs[gk] = (g, qs, outs, okh.numpy(), torch.cuda.Event())
+            side = self._side
+            self._side = torch.cuda.Stream(device=qs.device)  # the instance's side branch
+            try:
+                g, outs = capture(run, stream=torch.cuda.Stream(device=qs.device))
+            finally:
+                self._side = side
+            self.graphs[gk] = (g, qs, outs, okh.numpy(), torch.cuda.Event(), torch.cuda.Stream(device=qs.device))
         return self.graphs[gk]
 
     def submit(self, Qb, K, z, nprobe, k):
         """Queue the search of one batch and return its ticket without waiting for the GPU. Successive
-        submits of one (B, K, z, nprobe, k) alternate between two graph instances, so at most two batches
-        of a key are in flight: a third submit before the first is collected raises RuntimeError."""
+        submits of one (B, K, z, nprobe, k) cycle through NINST graph instances, so at most NINST batches
+        of a key are in flight: one more submit before the oldest is collected raises RuntimeError."""
         Qb = Qb.float().contiguous()
         key = (len(Qb), K, float(z), nprobe, k, self._knobs())
         inst = self._slot.get(key, 0)
         if (key, inst) in self._pending:
-            raise RuntimeError("EngineI8.submit: two batches of this shape are in flight; collect the older one first")
-        g, qs, (ok, I, nr, ids, sc, blas), okh, done = self._graph(key, inst, Qb)
-        self._slot[key] = inst ^ 1
-        qs.copy_(Qb)
-        g.replay()
-        done.record()
-        I, nr, ids, sc = _fresh(I, nr, ids, sc)  # the caller's copies, queued behind the replay
+            raise RuntimeError("EngineI8.submit: NINST batches of this shape are in flight; collect the oldest first")
+        g, qs, (ok, I, nr, ids, sc, blas), okh, done, st = self._graph(key, inst, Qb)
+        self._slot[key] = (inst + 1) % self.NINST
+        cur = torch.cuda.current_stream()
+        st.wait_stream(cur)  # the caller's batch, and the instance's last use by the caller, are complete
+        with torch.cuda.stream(st):
+            qs.copy_(Qb)
+            g.replay()
+            I, nr, ids, sc = _fresh(I, nr, ids, sc)  # the caller's copies, queued behind the replay
+            done.record()
+        Qb.record_stream(st)
+        for t in (I, nr, ids, sc):  # made on the instance's stream, used on the caller's
+            t.record_stream(cur)
         self._pending.add((key, inst))
         return (key, inst, I, nr, ids, sc)
 
@@ -282,7 +299,7 @@ class EngineI8:
         key, inst, I, nr, ids, sc = ticket
         if (key, inst) not in self._pending:
             raise RuntimeError("EngineI8.collect: this ticket was already collected")
-        g, qs, outs, okh, done = self.graphs[(key, inst)]
+        g, qs, outs, okh, done, st = self.graphs[(key, inst)]
         blas = outs[5]
         done.synchronize()
         if not okh.all():
@@ -290,10 +307,14 @@ class EngineI8:
             nb = len(bad)
             self.nbad += nb
             fg, sel, (a, b, c, s, ok2) = self._fallback_graph(key, inst, qs, blas, padded_rows(nb))
-            sel.copy_(torch.from_numpy(np.concatenate([bad, np.full(padded_rows(nb) - nb, bad[-1], np.int64)])))
-            fg.replay()
-            bd = torch.from_numpy(bad).to(qs.device)
-            I[bd], nr[bd], ids[bd], sc[bd] = a[:nb], b[:nb], c[:nb], s[:nb]
+            cur = torch.cuda.current_stream()
+            st.wait_stream(cur)
+            with torch.cuda.stream(st):  # behind the instance's own work, beside the other instance's
+                sel.copy_(torch.from_numpy(np.concatenate([bad, np.full(padded_rows(nb) - nb, bad[-1], np.int64)])))
+                fg.replay()
+                bd = torch.from_numpy(bad).to(qs.device)
+                I[bd], nr[bd], ids[bd], sc[bd] = a[:nb], b[:nb], c[:nb], s[:nb]
+            cur.wait_stream(st)
             self.nbad2 += int((~ok2[:nb]).sum())
         # the instance is free again only now: its flags and fallback inputs are read above
         self._pending.discard((key, inst))
@@ -304,13 +325,14 @@ class EngineI8:
         nprobe, k), for both graph instances, ahead of time, so that no later search pays a capture (tens
         of milliseconds)."""
         key = (B, K, float(z), nprobe, k, self._knobs())
-        if (key, 0) not in self.graphs and (key, 1) not in self.graphs:
+        have = [i for i in range(self.NINST) if (key, i) in self.graphs]
+        if not have:
             raise KeyError("warm_fallbacks: search this (B, K, z, nprobe, k) once first")
         if self._pending:
             raise RuntimeError("warm_fallbacks: collect the submitted batches first")
-        seed = self.graphs[(key, 0) if (key, 0) in self.graphs else (key, 1)][1]
-        for inst in (0, 1):
-            g, qs, outs, _, _ = self._graph(key, inst, seed)
+        seed = self.graphs[(key, have[0])][1]
+        for inst in range(self.NINST):
+            g, qs, outs, _, _, _ = self._graph(key, inst, seed)
             qs.copy_(seed)
             g.replay()  # the captures' warm-up runs read the main graph's outputs
             nbp = 1

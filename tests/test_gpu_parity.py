@@ -173,33 +173,46 @@ def test_fallback_matches_oracle(env, oracle_mod):
 
 
 def test_pipelined_submit_collect_matches_search(env):
-    """Two batches in flight, each with flagged queries (so the first batch's fallback runs after the
-    second batch's graph is queued), give the same results as one search at a time."""
+    """NINST batches in flight, each with flagged queries (so a batch's fallback runs while the later
+    batches' graphs run), give the same results as one search at a time; so do NINST full batches whose
+    graph instances run at the same time, each on its own stream. One more submit of the shape, or a
+    second collect of a ticket, raises."""
     E, Q = env["E"], env["Q"]
-    A, Bq = Q[:64].contiguous(), Q[64:128].contiguous()
+    n = E.NINST
+    assert 2 <= n <= 4
+    batches = [Q[64 * i:64 * (i + 1)].contiguous() for i in range(n)]
     old = E.MSZ
     E.MSZ = K + 8
     try:
-        ref = [E.search(x, K, Z_, NPROBE, KK, ret_scores=True) for x in (A, Bq)]
+        ref = [E.search(x, K, Z_, NPROBE, KK, ret_scores=True) for x in batches]
         torch.cuda.synchronize()
         nb0 = E.nbad
         for rep in range(2):
-            ta = E.submit(A, K, Z_, NPROBE, KK)
-            tb = E.submit(Bq, K, Z_, NPROBE, KK)
+            tickets = [E.submit(x, K, Z_, NPROBE, KK) for x in batches]
             with pytest.raises(RuntimeError):
-                E.submit(A, K, Z_, NPROBE, KK)  # a third batch of the shape while two are in flight
-            ra = E.collect(ta, ret_scores=True)
-            rb = E.collect(tb, ret_scores=True)
+                E.submit(batches[0], K, Z_, NPROBE, KK)  # one more batch of the shape than instances
+            res = [E.collect(t, ret_scores=True) for t in tickets]
             with pytest.raises(RuntimeError):
-                E.collect(ta)
+                E.collect(tickets[0])
             torch.cuda.synchronize()
-            for got, want in ((ra, ref[0]), (rb, ref[1])):
+            for got, want in zip(res, ref):
                 for g, w in zip(got, want):
                     assert np.array_equal(npy(g), npy(w)), f"rep {rep}"
         assert E.nbad > nb0
     finally:
         E.MSZ = old
         E.graphs.clear()
+    # the whole query set, n different batches in flight at once
+    full = [torch.roll(Q, 37 * i, 0).contiguous() for i in range(n)]
+    ref = [E.search(x, K, Z_, NPROBE, KK, ret_scores=True) for x in full]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        tickets = [E.submit(x, K, Z_, NPROBE, KK) for x in full]
+        res = [E.collect(t, ret_scores=True) for t in tickets]
+        torch.cuda.synchronize()
+        for got, want in zip(res, ref):
+            for g, w in zip(got, want):
+                assert np.array_equal(npy(g), npy(w)), f"concurrent rep {rep}"
 
 
 def test_recall_and_pinned_host_rows(env):
