@@ -43,8 +43,8 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--d", type=int, default=1536)
     ap.add_argument("--nlist", type=int, default=4096)
@@ -164,7 +164,7 @@ def main():
 
     # ---- the same point over distinct batches (no batch is replayed, so no cross-step cache reuse of its
     # candidates' refine rows); throughput/e_dup.py:7-13 measures the duplicate-batch effect the same way
-    ndist = 10
+    ndist = 30
     distinct = [datagen.gen(args.batch, args.d, args.clusters, 0.7, seed=100 + i, device=dev, dtype=torch.float32)
                 for i in range(ndist)]
     # the fallback graphs of 1..64 flagged rows are captured ahead (a capture takes tens of ms, as a serving
