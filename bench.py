@@ -250,7 +250,8 @@ def _time_launch(fn, reps, torch, setup=None):
 
 
 def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
-    """Time the stage-1 kernels and LUT scorer of one batch and relate them to their algorithmic work."""
+    """Time the stage-1 kernels, the LUT scorer and the refine of one batch and relate them to their algorithmic
+    work."""
     s1 = E.s1
     NC = len(s1["off"]) - 1
     B = Q.shape[0]
@@ -272,6 +273,8 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     pre = (tr["L"], tr["qsum"], tr["qn2"])
     ncnt = tr["ncnt"] if E.DELTA is not None else None
     t_lut = _time_launch(lambda: _lib.lut_score(tr["pos"], tr["QC"], pre, E.code, ncnt), reps, torch)
+    t_ref = _time_launch(lambda: _lib.refine(tr["est"], tr["sd"], tr["pos"], s1["order"], E.H, Q, args.z, args.k),
+                         reps, torch)
     cal = torch.ones(CAL_BYTES // 4, dtype=torch.int32, device=Q.device)
     cal2 = torch.empty_like(cal)
     t_copy = _time_launch(lambda: cal2.copy_(cal), reps, torch)
@@ -288,6 +291,7 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     ops_first = 2.0 * R * float((sizes * ccnt_first).sum())
     scored = float(tr["ncnt"].clamp(max=K).sum()) if ncnt is not None else float(B * K)
     lut_bytes = scored * E.code["RB"]
+    ref_bytes = float(tr["reads"].sum()) * E.H.shape[1] * E.H.element_size()  # the ambiguous candidates' rows
     gbs = lambda byt, ms: byt / (ms * 1e-3) / 1e9
     tops = lambda ops, ms: ops / (ms * 1e-3) / 1e12
     emit_gbs, emit_tops = gbs(code_bytes_emit, t_emit), tops(ops_emit, t_emit)
@@ -300,6 +304,8 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
                      "GBps": round(gbs(code_bytes_first, t_first), 1), "int8_TOPS": round(tops(ops_first, t_first), 2)},
         "lut_score": {"ms": round(t_lut, 4), "bytes": lut_bytes, "GBps": round(gbs(lut_bytes, t_lut), 1),
                       "hbm_frac": round(gbs(lut_bytes, t_lut) / HBM_PEAK_GBS, 4)},
+        "refine": {"ms": round(t_ref, 4), "bytes": ref_bytes, "GBps": round(gbs(ref_bytes, t_ref), 1),
+                   "hbm_frac": round(gbs(ref_bytes, t_ref) / HBM_PEAK_GBS, 4)},
         "copy_calibration": {"ms": round(t_copy, 4), "bytes": 2.0 * CAL_BYTES,
                              "GBps": round(gbs(2.0 * CAL_BYTES, t_copy), 1)},
     }
