@@ -71,9 +71,32 @@ __device__ __forceinline__ int fvs_lane_prefix(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// x of lane (lane ^ d) for a power of two d < 64, every lane of the wave active. With d known at compile
+// time (unrolled loops) the exchange is a cross-lane move instead of an LDS permute: DPP quad permutations
+// for 1 and 2, a rotation by 8 within 16-lane rows (which is lane ^ 8), ds_swizzle's xor mode within
+// 32-lane groups for 4 and 16, and ds_bpermute for 32.
+__device__ __forceinline__ uint32_t fvs_xor_lane(uint32_t x, int d) {
+  switch (d) {
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xb1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x101f);                     // and 31, xor 4
+    case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xf, 0xf, false);  // row_ror 8
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401f);                    // and 31, xor 16
+    default: return (uint32_t)__shfl_xor((int)x, d, FVS_WAVE);
+  }
+}
+
+__device__ __forceinline__ float fvs_xor_lane_f(float x, int d) { return __uint_as_float(fvs_xor_lane(__float_as_uint(x), d)); }
+
+__device__ __forceinline__ double fvs_xor_lane_d(double x, int d) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint64_t r = ((uint64_t)fvs_xor_lane((uint32_t)(u >> 32), d) << 32) | fvs_xor_lane((uint32_t)u, d);
+  return __longlong_as_double((long long)r);
+}
+
 __device__ __forceinline__ float fvs_wave_max(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, FVS_WAVE));
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, fvs_xor_lane_f(v, o));
   return v;
 }
 
@@ -246,8 +269,8 @@ __device__ KT fvs_block_kth_set(F key, int n, int k, int *hist, int *sh) {
 }
 
 __device__ __forceinline__ uint64_t fvs_shfl_xor_u64(uint64_t x, int j) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, j, FVS_WAVE);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j, FVS_WAVE);
+  const uint32_t lo = fvs_xor_lane((uint32_t)x, j);
+  const uint32_t hi = fvs_xor_lane((uint32_t)(x >> 32), j);
   return ((uint64_t)hi << 32) | lo;
 }
 

@@ -76,8 +76,8 @@ __global__ __launch_bounds__(256) void k_lut_build(const uint16_t *__restrict__ 
       }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) {
-        s1 += __shfl_xor(s1, o, FVS_WAVE);
-        s2 += __shfl_xor(s2, o, FVS_WAVE);
+        s1 += fvs_xor_lane_d(s1, o);
+        s2 += fvs_xor_lane_d(s2, o);
       }
       if (lane == 0) {
         qsum[(int64_t)t * B + q] = (float)s1;

@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void k_query_code(const float *__restrict__ z,
     s += (double)x * (double)c[k];
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, FVS_WAVE);
+  for (int o = 32; o > 0; o >>= 1) s += fvs_xor_lane_d(s, o);
   if (lane == 0) qc[q] = (float)s;
 }
 
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void k_dense_small(const float *__restrict__ Q
       double sd = 0.0;
       for (int k = lane; k < d; k += 64) sd += (double)Q[(int64_t)b * d + k] * (double)c[k];
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) sd += __shfl_xor(sd, o, FVS_WAVE);
+      for (int o = 32; o > 0; o >>= 1) sd += fvs_xor_lane_d(sd, o);
       if (lane == 0) qc[b] = (float)sd;
     }
     return;
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void k_dense_small(const float *__restrict__ Q
     if (b < B) {
       float v = acc[b];
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, FVS_WAVE);
+      for (int o = 32; o > 0; o >>= 1) v += fvs_xor_lane_f(v, o);
       if (lane == 0) {
         if (kind == 0)
           Qr[(int64_t)b * R + row] = v;

@@ -54,7 +54,7 @@ __device__ __forceinline__ void dot_rows(const uint16_t *__restrict__ H, int d, 
       }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, FVS_WAVE);
+    for (int o = 32; o > 0; o >>= 1) acc += fvs_xor_lane_f(acc, o);
     if (lane == 0 && a0 + r < na) score[slots[a0 + r]] = acc;
   }
 }

@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave(const uin
         const bool desc = (lo & kk) == 0, first = (lo & j) == 0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const uint32_t y = __shfl_xor(x[r], j / R, FVS_WAVE);
+          const uint32_t y = fvs_xor_lane(x[r], j / R);
           x[r] = (desc == first) ? max(x[r], y) : min(x[r], y);
         }
       } else {
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(kRouteWaves * FVS_WAVE) void k_route_wave_f32(const
         const bool desc = (lo & kk) == 0, first = (lo & j) == 0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const uint64_t y = __shfl_xor(x[r], j / R, FVS_WAVE);
+          const uint64_t y = fvs_shfl_xor_u64(x[r], j / R);
           x[r] = (desc == first) ? (x[r] > y ? x[r] : y) : (x[r] < y ? x[r] : y);
         }
       } else {

@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
     if (MODE == 0) {
       float m = valid ? est : -__builtin_inff();
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, FVS_WAVE));
+      for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, fvs_xor_lane_f(m, o));
       if (lane == 0) bm[((int64_t)q * n1 + qrank[pidx]) * MB + (blk - cs / 32)] = m;
     } else {
       // one counter update per wave: slot = base + rank of the lane among the passing lanes
@@ -273,7 +273,8 @@ __global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict_
         const double z = (double)zq[tiers.start[t] + k];
         a += z * z;
       }
-      for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, FVS_WAVE);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) a += fvs_xor_lane_d(a, o);
       if (lane == 0) qn2[t] = (float)a;
     }
   }
@@ -307,7 +308,8 @@ __global__ __launch_bounds__(256) void k_tiered_score(const int32_t *__restrict_
         for (int pp = 0; pp < b; pp++) code |= (((int)pl[pp * kb + (k >> 3)] >> (7 - (k & 7))) & 1) << (b - 1 - pp);
         acc = __builtin_fmaf(cbt[code], zt[k], acc);
       }
-      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, FVS_WAVE);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) acc += fvs_xor_lane_f(acc, o);
       const uint16_t *ss = reinterpret_cast<const uint16_t *>(rw + soff + 4 * t);
       const float sc = fvs_h2f(ss[0]), sg = fvs_h2f(ss[1]);
       e = __builtin_fmaf(acc, sc, e);
