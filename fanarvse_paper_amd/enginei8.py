@@ -108,7 +108,6 @@ class EngineI8:
         self.meansN = (s1["means16"].float() * s1["inv_mnorm"][:, None]).half().contiguous()
         self.mnorm = (1.0 / s1["inv_mnorm"]).float().contiguous()
         self.graphs = {}
-        self._slot = {}      # key -> the graph instance (0 or 1) the next submit uses
         self._pending = set()  # (key, instance) submitted and not yet collected
         self._side = None  # stream for the stage-2 tables (default priority)
         self.nbad = 0
@@ -271,16 +270,16 @@ class EngineI8:
         return self.graphs[gk]
 
     def submit(self, Qb, K, z, nprobe, k):
-        """Queue the search of one batch and return its ticket without waiting for the GPU. Successive
-        submits of one (B, K, z, nprobe, k) cycle through NINST graph instances, so at most NINST batches
-        of a key are in flight: one more submit before the oldest is collected raises RuntimeError."""
+        """Queue the search of one batch and return its ticket without waiting for the GPU. A submit of one
+        (B, K, z, nprobe, k) takes the lowest-numbered of its NINST graph instances that has no batch in
+        flight, so at most NINST batches of a key are in flight (one more submit raises RuntimeError), and
+        a caller that collects each batch before the next submit (search) only ever uses instance 0."""
         Qb = Qb.float().contiguous()
         key = (len(Qb), K, float(z), nprobe, k, self._knobs())
-        inst = self._slot.get(key, 0)
-        if (key, inst) in self._pending:
-            raise RuntimeError("EngineI8.submit: NINST batches of this shape are in flight; collect the oldest first")
+        inst = next((i for i in range(self.NINST) if (key, i) not in self._pending), None)
+        if inst is None:
+            raise RuntimeError("EngineI8.submit: NINST batches of this shape are in flight; collect one first")
         g, qs, (ok, I, nr, ids, sc, blas), okh, done, st = self._graph(key, inst, Qb)
-        self._slot[key] = (inst + 1) % self.NINST
         cur = torch.cuda.current_stream()
         st.wait_stream(cur)  # the caller's batch, and the instance's last use by the caller, are complete
         with torch.cuda.stream(st):

@@ -186,6 +186,9 @@ def test_pipelined_submit_collect_matches_search(env):
     try:
         ref = [E.search(x, K, Z_, NPROBE, KK, ret_scores=True) for x in batches]
         torch.cuda.synchronize()
+        # one search at a time collects each batch before the next submit: only instance 0 is captured
+        insts = {gk[1] for gk in E.graphs if gk[0] != "fb"} | {gk[2] for gk in E.graphs if gk[0] == "fb"}
+        assert insts == {0}, insts
         nb0 = E.nbad
         for rep in range(2):
             tickets = [E.submit(x, K, Z_, NPROBE, KK) for x in batches]
