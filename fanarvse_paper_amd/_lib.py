@@ -43,7 +43,7 @@ SIGNATURES = {
     "fvs_threshold": [P, P, I32, P, I32, I64, I32, I32, I32, P, P, P],
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
-    "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
+    "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, I32, P, I64, I32, P, P, P],
     "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
     "fvs_classify": [P, P, P, P, I64, I32, F32, I32, P, P, P, P, P],
     "fvs_refine_rows": [P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
@@ -335,8 +335,9 @@ def lut_build(Zq, TS, half):
     return L, qsum, qn2
 
 
-def lut_score(pos, qc, pre, code, ncnt=None):
-    """(est, sd) [B, K] of the candidates (throughput/s2lut.py:92-106), from the packed records."""
+def lut_score(pos, qc, pre, code, ncnt=None, nt=None):
+    """(est, sd) [B, K] of the candidates (throughput/s2lut.py:92-106), from the packed records; nt: the
+    partial estimate over the first nt tiers (score_lut(..., nt=...), throughput/s2lut.py:92-93)."""
     L, qsum, qn2 = pre
     B, K = pos.shape
     TS = code["TS"]
@@ -351,7 +352,7 @@ def lut_score(pos, qc, pre, code, ncnt=None):
     _check(lib().fvs_lut_score(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
                                _dev(L, L.dtype, "L"), int(half), L.shape[1], _dev(qsum, torch.float32, "qsum", (T, B)),
                                _dev(qn2, torch.float32, "qn2", (T, B)), _dev(rec, torch.uint8, "rec"), N, RB,
-                               int(code["soff"]), T, _tiers_arr(TS), deltas, toff,
+                               int(code["soff"]), T, _tiers_arr(TS), deltas, toff, int(nt or 0),
                                _opt(ncnt, torch.int32, "ncnt", (B,)), B, K, _dev(est, torch.float32, "est"),
                                _dev(sd, torch.float32, "sd"), _stream()), "fvs_lut_score")
     return est, sd

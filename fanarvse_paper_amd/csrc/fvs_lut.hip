@@ -409,7 +409,8 @@ extern "C" int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T
 extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
                              const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB,
                              int32_t soff, int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff,
-                             const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream) {
+                             int32_t nt, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
+                             void *stream) {
   // LW = 16 entries per 4 coordinates, in whole 512-byte table groups (tiers are whole 32-coordinate blocks)
   if (B < 0 || K <= 0 || N <= 0 || LW <= 0 || LW > 16384 || LW % 128 != 0) return FVS_E_ARG;
   if (RB <= 0 || RB % 16 != 0 || soff <= 0 || soff % 4 != 0) return FVS_E_ARG;
@@ -424,6 +425,10 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
     at += ta.bits[t] * ta.kb[t];
   }
   if (at != soff || soff + 4 * T > RB) return FVS_E_SHAPE;
+  // a partial estimate scores the leading nt tiers: the schedule then covers their planes and pairs only
+  // (the other dwords look up the zero table), and the tier queues hold nt entries
+  if (nt < 0 || nt > T) return FVS_E_ARG;
+  if (nt > 0) ta.T = nt;
   if (B == 0) return FVS_OK;
   if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
   if (K > 4096) return FVS_E_CAPACITY;
@@ -442,7 +447,7 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
                        K, est, sd);
   };
   auto by_t = [&](auto HALF_) {
-    switch (T) {
+    switch (ta.T) {
       case 1: launch(HALF_, std::integral_constant<int, 1>{}); break;
       case 2: launch(HALF_, std::integral_constant<int, 2>{}); break;
       case 3: launch(HALF_, std::integral_constant<int, 3>{}); break;

@@ -229,8 +229,8 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 // >= (t0 - qcp)/qs - u|qcp|/qs - 0.75 z, while g >= acc*z + 2z - u|acc*z + 2z| >= acc*z + 1.74 z, and the
 // rounding of T's three operations is far below its 2^-20 margin; so every element whose estimate passes
 // also passes the prefilter. (A query with qs <= 0 or an overflowing T gets T = -inf, a row scale that is
-// negative or infinite the addend +inf: the prefilter then admits everything, and the exact test
-// decides.) Per element that is a convert, an fma and a compare; the tests of four elements of both
+// negative or infinite the addend +inf: the prefilter then admits every query of the chunk, and the exact
+// test decides; the missing queries of a last partial tile have a NaN threshold, which nothing passes.) Per element that is a convert, an fma and a compare; the tests of four elements of both
 // blocks are made before one branch on the OR of their eight ballots skips the group.
 //
 // The passing elements are staged as (accumulator, tag) in the wave's LDS region. The flush computes the
@@ -460,6 +460,10 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
         for (int k = tid; k < nn; k += NT) {
           const uint32_t tg = S.tag[ww][k];
           const int j = (int)((tg >> 8) & 0xfffu);
+          if (j >= nq) {  // not a pair of the chunk (cannot be staged: its threshold is NaN)
+            S.tag[ww][k] = 0xffffffffu;
+            continue;
+          }
           const Meta m = meta[j];
           const float est = __builtin_fmaf((float)S.acc[ww][k] * m.qs, zsl[tg & 0xffu], m.qcp);
           if (est >= m.x) {
@@ -525,7 +529,9 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
           S.lcnt[j] = 0u;
         }
       }
-      if (tid < 32) Tl[nq + tid] = __builtin_inff();  // the last tile's missing queries pass nothing
+      // the last tile's missing queries pass nothing: every compare with NaN is false, also for the +inf
+      // prefilter value of a row whose scale is negative or infinite
+      if (tid < 32) Tl[nq + tid] = __builtin_nanf("");
       ebase = 0;
       __syncthreads();
       scan();
@@ -534,10 +540,20 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
       bool over = false;
 #pragma unroll
       for (int ww = 0; ww < NW; ww++) over = over || S.n[ww] > kCapE;
-      if (over) {  // csz >= 16 here: an 8-query chunk stages at most 8 x 64 = 512 <= kCapE per wave
-        csz >>= 1;   // the same first pair again, with half the queries
+      if (over && csz > 8) {  // the same first pair again, with half the queries
+        csz >>= 1;
         pq_ok = false;
         continue;
+      }
+      if (over) {
+        // Unreachable: an 8-query chunk stages at most 8 x 64 = 512 <= kCapE elements per wave (the slots
+        // past nq have a NaN threshold). Should it happen, the chunk's staged elements are dropped and bit
+        // 30 of each of its queries' counts marks them (a count above any buffer: the query is flagged and
+        // recomputed), and the scan goes on instead of halving below 8.
+        for (int j = tid; j < nq; j += NT) atomicOr(&cnt[meta[j].qid], 1 << 30);
+        __syncthreads();  // every thread has read the region counts
+        if (tid < NW) S.n[tid] = 0;
+        __syncthreads();
       }
       if (c0 + nq >= qn) break;  // the last chunk is flushed after the next item's loads are issued
       flush();
@@ -610,7 +626,7 @@ __global__ __launch_bounds__(256) void k_i8_civf8(
       mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
       if (h == 0 && jv) bmc[(int64_t)(qoff + j) * MB + (blk - cs / 32)] = mx;
     } else {
-      const float th = jv ? t0[q] : __builtin_inff();
+      const float th = jv ? t0[q] : __builtin_nanf("");  // NaN: an +inf estimate must not pass either
       uint32_t bits = 0;
 #pragma unroll
       for (int v = 0; v < 16; v++) bits |= (ev[v] >= th ? 1u : 0u) << v;

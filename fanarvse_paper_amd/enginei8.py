@@ -20,8 +20,8 @@ work as there (throughput/enginei8.py:66-86):
   * UNSORTED: the n_p probed cells in cell order instead of score order (the reference's unsorted topk
     order is unspecified; the first n1 of them seed the threshold either way);
   * SORTROUTE: sort-then-cut equals the sorted top-n_p under this build's (score desc, cell asc) order;
-  * K2 < K: every candidate is scored by the LUT stage, and only the K2 best go on to the delta rule
-    and the exact reads.
+  * K2 < K: every candidate is ranked by the LUT estimate over the first NT tiers, and only the K2 best
+    go on to the full stage 2, the delta rule and the exact reads.
 """
 import math
 
@@ -117,7 +117,7 @@ class EngineI8:
     def _knobs(self):
         """The knob values captured work depends on: a search after a change captures new graphs."""
         return (self.MSZ, self.BETA, self.RHO, self.DELTA, self.LUTF, self.LUTH, self.NROUTE, self.ROUTE16,
-                self.PROJ, self.UNSORTED, self.SORTROUTE, self.K2)
+                self.PROJ, self.UNSORTED, self.SORTROUTE, self.K2, self.NT)
 
     def _check_knobs(self):
         if self.PROJ and not self.NROUTE and "W1" not in self.s1:
@@ -225,8 +225,9 @@ class EngineI8:
         if pre is None:
             pre = _lib.lut_build(Zq, self.code["TS"], half)
         if self.K2 is not None and self.K2 < K:
-            # progressive stage 2 (throughput/enginei8.py:82-85): score all K, keep the K2 best by estimate
-            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None)
+            # progressive stage 2 (throughput/enginei8.py:82-85): rank all K by the partial estimate over the
+            # first NT tiers, keep the K2 best
+            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None, nt=min(self.NT, len(self.code["TS"])))
             cntK = torch.full((pos.shape[0],), K, dtype=torch.int32, device=pos.device)
             pos = _lib.select(e_all.contiguous(), pos.contiguous(), cntK, self.K2, 0, None)[0]
             if ncnt is not None:
@@ -321,7 +322,7 @@ class EngineI8:
 
     def warm_fallbacks(self, B, K, z, nprobe, k, upto=64):
         """Capture the fallback graphs of 1, 2, 4, ... `upto` flagged rows of an already searched (B, K, z,
-        nprobe, k), for both graph instances, ahead of time, so that no later search pays a capture (tens
+        nprobe, k), for every graph instance (NINST), ahead of time, so that no later search pays a capture (tens
         of milliseconds)."""
         key = (B, K, float(z), nprobe, k, self._knobs())
         have = [i for i in range(self.NINST) if (key, i) in self.graphs]
@@ -392,7 +393,7 @@ class EngineI8:
         pre = _lib.lut_build(Zq, self.code["TS"], half)
         pos1 = pos
         if self.K2 is not None and self.K2 < K:
-            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None)
+            e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None, nt=min(self.NT, len(self.code["TS"])))
             cntK = torch.full((pos.shape[0],), K, dtype=torch.int32, device=pos.device)
             pos = _lib.select(e_all.contiguous(), pos.contiguous(), cntK, self.K2, 0, None)[0]
             if ncnt is not None:

@@ -267,6 +267,7 @@ def luts_fused(code, Qh, half=False):
     return _lib.lut_build(rotate(code, Qh), code["TS"], half)
 
 
-def score_lut(code, qc, pos, pre, ncnt=None):
-    """(est, sd) of candidates `pos` [B, K] (throughput/s2lut.py:92-106)."""
-    return _lib.lut_score(pos, qc, pre, code, ncnt)
+def score_lut(code, qc, pos, pre, ncnt=None, nt=None):
+    """(est, sd) of candidates `pos` [B, K] (throughput/s2lut.py:92-106); nt: over the first nt tiers only
+    (the reference's TS[:nt], throughput/s2lut.py:93), with the full tables `pre`."""
+    return _lib.lut_score(pos, qc, pre, code, ncnt, nt)

@@ -237,6 +237,9 @@ int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int
  *   pos i32 [B, K] sorted positions; qc f32 [B]; L (fp16 if half else f32) [B, LW];
  *   qsum, qn2 f32 [T, B]; rec u8 [N, RB]: tier t plane p at toff[t] + p*(d_t/8), then (scale, sigma)
  *   fp16 pairs per tier at soff + 4t; tiers i32 [T][3], deltas f32 [T], toff i32 [T] are HOST arrays.
+ *   nt: score only tiers 0 .. nt-1 (1 <= nt <= T; 0 = all T), the partial estimate of
+ *   score_lut(..., nt=NT) that ranks the progressive stage's candidates (throughput/s2lut.py:92-93,
+ *   throughput/enginei8.py:82-85); the record layout is still checked against all T tiers.
  *   ncnt i32 [B] or NULL (score all K). est, sd f32 [B, K]; slots m >= ncnt[q] get (-1e30, 0).
  *   Limits: LW % 128 == 0 (whole 512-byte table groups; LW = 4 d for tiers of whole 32-coordinate
  *   blocks), K <= 4096, and the record's plane and pair dwords, rounded up to 32, at most 512
@@ -245,13 +248,13 @@ int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T, const int
  * s = max(0, E - 3) where max|L| of the query = f * 2^E, f in [0.5, 1) (frexp); the tier sums
  *   A_t = sum_p 2^(b-1-p) sum_j (fx[hi nibble] + fx[lo nibble]) are exact integers. Then, in f32:
  *   a = ldexpf((float)A_t, s - 24); a = delta_t * fmaf(-mid_t, qsum[t], a); est = fmaf(a, scale_t, est);
- *   var = fmaf(qn2[t] * sig_t, sig_t, var), for t = 0..T-1, from est = qc[q], var = 0; sd = sqrtf(var)
+ *   var = fmaf(qn2[t] * sig_t, sig_t, var), for t = 0..nt-1, from est = qc[q], var = 0; sd = sqrtf(var)
  *   (the multiply-adds fused as the reference's compiled kernel fuses them).
  */
 int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
                   const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB, int32_t soff,
-                  int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff, const int32_t *ncnt,
-                  int64_t B, int32_t K, float *est, float *sd, void *stream);
+                  int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff, int32_t nt,
+                  const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream);
 
 /*
  * Error-bar classification, exact refinement and final top-k (a16, a17, a18). Replaces

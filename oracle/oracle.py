@@ -386,7 +386,8 @@ def route(idx, QM16, nprobe, knobs):
     if knobs.get("NROUTE", True):
         probe = route_topk(QM16, nprobe)
     elif knobs.get("ROUTE16", True):
-        keys = (np.asarray(QM16).view(np.float16).astype(np.float32) * idx["inv_mnorm"][None, :]).astype(np.float16)
+        with np.errstate(over="ignore"):  # keys beyond the fp16 range become +-inf, as the kernel rounds them
+            keys = (np.asarray(QM16).view(np.float16).astype(np.float32) * idx["inv_mnorm"][None, :]).astype(np.float16)
         probe = route_topk(keys.view(np.uint16), nprobe)
     else:
         probe = route_topk_scaled(QM16, idx["inv_mnorm"], nprobe)
@@ -416,9 +417,13 @@ def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None,
     L, qsum, qn2 = lut_build(Zq16, idx["TS"], half)
     pos, ncnt = s1["pos"], (s1["ncnt"] if delta is not None else None)
     K2 = knobs.get("K2")
-    if K2 is not None and K2 < K:  # progressive stage 2 (throughput/enginei8.py:82-85)
-        e_all, _ = lut_score(pos, qc, L, half, qsum, qn2, idx["rec"], idx["soff"], idx["TS"], idx["deltas"],
-                             idx["toff"], None)
+    if K2 is not None and K2 < K:
+        # progressive stage 2 (throughput/enginei8.py:82-85): the partial estimate over the first NT tiers
+        # (score_lut(..., nt=self.NT), throughput/s2lut.py:92-93: TS[:nt] with the full tables, whose tier-t
+        # rows of qsum/qn2 and table offsets are those of the full code) ranks the candidates
+        nt = min(knobs.get("NT", 3), len(idx["TS"]))
+        e_all, _ = lut_score(pos, qc, L, half, qsum[:nt], qn2[:nt], idx["rec"], idx["soff"], idx["TS"][:nt],
+                             idx["deltas"][:nt], idx["toff"][:nt], None)
         pos = select(e_all, pos, np.full(len(pos), K, np.int32), K2, 0, None)[0]
         if ncnt is not None:
             ncnt = np.minimum(ncnt, K2).astype(np.int32)

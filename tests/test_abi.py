@@ -94,7 +94,7 @@ def test_lut_score_layout_checks_need_no_gpu(L):
         deltas = (ctypes.c_float * 1)(1.0)
         soff = D * bits // 8
         toff = (ctypes.c_int32 * 1)(0)
-        return L.fvs_lut_score(p, p, p, 1, LW, p, p, p, 10, RB, soff, 1, tiers, deltas, toff, None, 1, 10, p, p, None)
+        return L.fvs_lut_score(p, p, p, 1, LW, p, p, p, 10, RB, soff, 1, tiers, deltas, toff, 0, None, 1, 10, p, p, None)
 
     assert call(LW=1552, D=388, bits=4, RB=208) == E_ARG      # LW % 128 (tiers are whole 32-coordinate blocks)
     assert call(LW=16384, D=4096, bits=4, RB=2064) == E_CAP   # 513 dwords of planes and pair: past 512

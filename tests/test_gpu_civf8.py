@@ -1,16 +1,20 @@
-"""The reference's operator seam on the GPU: EngineI8.stage1_i8 with its CUDA knob set
-(throughput/enginei8.py:36-60, NROUTE branch) restated line by line in torch, calling
-fanarvse_paper_amd.civf8.launch where the reference calls civf8.launch: the reference's _static_blocks work
-list, pairs_fast pair lists with |m_c| scaling, the -1e30 pre-filled bmc indexed by pair, the inverse
-permutation gather, the topk threshold and the final bval.topk(K). Every intermediate is compared with
-the CPU oracle's stage 1 on the same q8 / qs / QM / probe inputs: block maxima, t0, counts and emitted
-sets bit-exact, the top-K estimates bit-exact (positions compared as sets: torch.topk breaks ties in its
-own order), and the exactness flags."""
+"""The reference's operator seam on the GPU: fanarvse_paper_amd.civf8.launch, driven through its documented
+argument contract (throughput/civf8.py:89-91) with this build's own pieces, and compared with the CPU oracle
+bit for bit.
+
+The contract: a work list of one-block items (pcell, pblk, ps, pe) -- every (cell, global 32-row block) of the
+cell-sorted index, `index.static_blocks` -- and pair lists grouped by cell (qid, coff, ccnt, qcp) from
+`_lib.pairs`, whose pairs this test numbers itself. Mode 0 writes the maximum estimate of each (pair, block) at
+bmc[pair * MB + blk - cs / 32] into a -1e30 pre-filled buffer; mode 1 appends every row whose estimate reaches
+the query's t0 to bval / bpos [B, CAP] and counts it in cnt. The test scatters bmc by the (query, probe rank)
+of each pair into [B, n1, MB] block maxima, takes the threshold and the final top-K with the library's own
+kernels, and compares block maxima, t0, counts, emitted sets, top-K estimates and flags with the oracle's
+stage 1 on the same q8 / qs / QM / probe inputs."""
 import numpy as np
 import pytest
 import torch
 
-from fanarvse_paper_amd import civf8, datagen, index
+from fanarvse_paper_amd import _lib, civf8, datagen, index
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
@@ -18,55 +22,6 @@ dev = "cuda"
 
 def npy(t):
     return t.detach().cpu().numpy()
-
-
-def pairs_fast(probe, NC, QM, scale=None):
-    """throughput/enginei8.py:11-16, as the reference writes it."""
-    B, npr = probe.shape
-    flat = probe.flatten().to(torch.int32)
-    _, o = torch.sort(flat, stable=True)
-    qid = (o // npr).to(torch.int32).contiguous()
-    cnt = torch.zeros(NC, dtype=torch.int32, device=dev).scatter_add_(0, flat.long(), torch.ones_like(flat))
-    off = torch.cumsum(cnt, 0) - cnt
-    fo = flat[o].long()
-    qc = QM[qid.long(), fo].float()
-    if scale is not None:
-        qc = qc * scale[fo]
-    return qid, off.to(torch.int32).contiguous(), cnt.contiguous(), qc.contiguous(), o
-
-
-def stage1_i8(s1, Z, zs, Vr, mnorm, Qb, QM, probe, K, M, rho=0.6, beta=1.1, BN=32):
-    """throughput/enginei8.py:36-60 with CUDA = True and NROUTE = True."""
-    off_t = s1["off_t"]
-    NC = len(off_t) - 1
-    B = len(Qb)
-    z = Qb @ Vr
-    qs = (z.abs().amax(1).clamp(min=1e-12) / 127)
-    q8 = torch.round(z / qs[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
-    qs = qs.float().contiguous()
-    (pcell, pblk, ps, pe), MB = index.static_blocks(off_t, BN)
-    P = len(pcell)
-    n1 = min(max(int(np.ceil(beta * K / (Z.shape[0] / NC / BN + 1))), 1), probe.shape[1])
-    qid, coff, ccnt, qcp, o = pairs_fast(probe[:, :n1].contiguous(), NC, QM, mnorm)
-    bmc = torch.full((B * n1, MB), -1e30, device=dev)
-    d = torch.zeros(1, device=dev)
-    di = torch.zeros(1, dtype=torch.int32, device=dev)
-    civf8.launch(0, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, d, di, d, di, bmc, 1, MB)
-    inv = torch.empty_like(o)
-    inv[o] = torch.arange(len(o), device=dev)
-    v = bmc[inv].reshape(B, n1 * MB)
-    top = v.topk(min(int(np.ceil(rho * K)), v.shape[1]), 1).values
-    valid = top > -1e29
-    t0 = torch.where(valid, top, torch.full_like(top, 1e30)).min(1).values.contiguous()
-    cnt = torch.zeros(B, dtype=torch.int32, device=dev)
-    bval = torch.full((B, M), -1e30, device=dev)
-    bpos = torch.zeros((B, M), dtype=torch.int32, device=dev)
-    qid, coff, ccnt, qcp, _ = pairs_fast(probe, NC, QM, mnorm)
-    civf8.launch(1, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, t0, cnt, bval, bpos, bmc, M, MB)
-    t = bval.topk(K, 1)
-    pos = bpos.gather(1, t.indices).long().contiguous()
-    return dict(q8=q8, qs=qs, n1=n1, MB=MB, bm=v.reshape(B, n1, MB), t0=t0, cnt=cnt, bval=bval, bpos=bpos, pos=pos,
-                est1=t.values, ok=(cnt >= K) & (cnt <= M))
 
 
 @pytest.fixture(scope="module")
@@ -81,36 +36,64 @@ def env(oracle_mod):
     return dict(X=X, Q=Q, s1=s1, Z=Z, zs=zs, Vr=Vr, meansN=meansN, mnorm=mnorm, idx=idx)
 
 
-@pytest.mark.parametrize("B,K,nprobe,M", [(192, 175, 24, 3072), (37, 100, 16, 160), (1, 50, 8, 4096)])
-def test_reference_stage1_over_the_seam(env, oracle_mod, B, K, nprobe, M):
-    print(f"\n[gpu civf8] stage1_i8 over civf8.launch B={B} K={K} nprobe={nprobe} M={M}", flush=True)
-    Qb = env["Q"][:B].contiguous()
-    QM = Qb.half() @ env["meansN"].T
-    probe = QM.topk(nprobe, 1).indices
-    r = stage1_i8(env["s1"], env["Z"], env["zs"], env["Vr"], env["mnorm"], Qb, QM, probe, K, M)
+def seam_stage1(env, oracle_mod, Qb, K, nprobe, M):
+    """Stage 1 over civf8.launch: (inputs shared with the oracle, the seam's outputs)."""
+    s1, Z, zs = env["s1"], env["Z"], env["zs"]
+    off_t = s1["off_t"]
+    NC = off_t.numel() - 1
+    B = Qb.shape[0]
+    q8, qs = _lib.query_prep(Qb, env["Vr"], s1["c"])[:2]
+    QM = (Qb.half() @ env["meansN"].T).contiguous()
+    probe = _lib.route_topk(QM, nprobe)
+    (pcell, pblk, ps, pe), MB = index.static_blocks(off_t)
+    P = pcell.numel()
+    M_, n1, r = oracle_mod.params(K, nprobe, Z.shape[0], NC, MSZ=M, RHO=0.6)
+    # mode 0 over the first n1 probed cells of every query
+    qid, qrank, coff, ccnt, qcp = _lib.pairs(probe, n1, NC, QM, env["mnorm"])
+    npairs = qid.numel()
+    assert npairs == B * n1
+    bmc = torch.full((npairs, MB), -1e30, device=dev)
+    one_f = torch.zeros(1, device=dev)
+    one_i = torch.zeros(1, dtype=torch.int32, device=dev)
+    civf8.launch(0, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, one_f, one_i, one_f, one_i, bmc, 1, MB)
+    # each pair is one (query, probe rank): its row of bmc is that query's rank-th block-maxima row
+    bm = torch.full((B, n1, MB), -1e30, device=dev)
+    bm[qid.long(), qrank.long()] = bmc
+    cnt = torch.empty((B,), dtype=torch.int32, device=dev)
+    t0 = _lib.threshold(bm, probe, off_t, n1, MB, r, cnt)  # also zeroes cnt
+    # mode 1 over every probed cell
+    qid, _, coff, ccnt, qcp = _lib.pairs(probe, nprobe, NC, QM, env["mnorm"])
+    bval = torch.full((B, M), -1e30, device=dev)
+    bpos = torch.zeros((B, M), dtype=torch.int32, device=dev)
+    civf8.launch(1, P, q8, qs, qid, coff, ccnt, pcell, pblk, ps, pe, Z, zs, qcp, t0, cnt, bval, bpos, bmc, M, MB)
+    pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, min(9, K - 1), None)
     torch.cuda.synchronize()
-    st = oracle_mod.stage1(env["idx"], npy(r["q8"]), npy(r["qs"]), npy(QM).view(np.uint16),
-                           npy(probe).astype(np.int32), K, dict(MSZ=M, RHO=0.6))
+    ins = dict(q8=npy(q8), qs=npy(qs), QM=npy(QM).view(np.uint16), probe=npy(probe))
+    outs = dict(n1=n1, MB=MB, bm=npy(bm), t0=npy(t0), cnt=npy(cnt), bval=npy(bval), bpos=npy(bpos), pos=npy(pos),
+                est1=npy(est1), ok=npy(ok).astype(bool))
+    return ins, outs
+
+
+@pytest.mark.parametrize("B,K,nprobe,M", [(192, 175, 24, 3072), (37, 100, 16, 160), (1, 50, 8, 4096)])
+def test_stage1_over_the_seam(env, oracle_mod, B, K, nprobe, M):
+    print(f"\n[gpu civf8] stage 1 over civf8.launch B={B} K={K} nprobe={nprobe} M={M}", flush=True)
+    ins, r = seam_stage1(env, oracle_mod, env["Q"][:B].contiguous(), K, nprobe, M)
+    st = oracle_mod.stage1(env["idx"], ins["q8"], ins["qs"], ins["QM"], ins["probe"], K, dict(MSZ=M, RHO=0.6))
     assert st["n1"] == r["n1"] and st["MB"] == r["MB"] and st["M"] == M
-    assert np.array_equal(npy(r["bm"]).view(np.uint32), st["bm"].view(np.uint32))
-    assert np.array_equal(npy(r["t0"]).view(np.uint32), st["t0"].view(np.uint32))
-    cnt = npy(r["cnt"])
+    assert np.array_equal(r["bm"].view(np.uint32), st["bm"].view(np.uint32))
+    assert np.array_equal(r["t0"].view(np.uint32), st["t0"].view(np.uint32))
+    cnt = r["cnt"]
     assert np.array_equal(cnt, st["cnt"])
-    bval, bpos = npy(r["bval"]), npy(r["bpos"])
     for q in range(B):
         n = int(cnt[q])
         if n > M:  # beyond the buffer the kept subset depends on the emission order (the query is flagged)
             continue
-        assert sorted(zip(bval[q, :n].tolist(), bpos[q, :n].tolist())) == \
+        assert sorted(zip(r["bval"][q, :n].tolist(), r["bpos"][q, :n].tolist())) == \
             sorted(zip(st["bval"][q, :n].tolist(), st["bpos"][q, :n].tolist())), f"query {q}"
-    ok = npy(r["ok"])
+    ok = r["ok"]
     assert np.array_equal(ok, st["ok"].astype(bool))
-    est1 = npy(r["est1"])
-    assert np.array_equal(est1[ok].view(np.uint32), st["est1"][ok].view(np.uint32))
-    pos = npy(r["pos"])
-    for q in np.nonzero(ok)[0]:
-        kth = est1[q, -1]
-        above = est1[q] > kth  # positions strictly above the K-th estimate are fixed; ties at it are not
-        assert set(pos[q][above].tolist()) == set(st["pos"][q][st["est1"][q] > kth].tolist())
+    # the top K of a query that fits its buffer does not depend on the emission order: (est desc, pos asc)
+    assert np.array_equal(r["est1"][ok].view(np.uint32), st["est1"][ok].view(np.uint32))
+    assert np.array_equal(r["pos"][ok], st["pos"][ok])
     if B > 100:
         assert ok.mean() > 0.9

@@ -175,3 +175,30 @@ def test_index_build_is_deterministic():
     assert torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])  # int8 codes and scales
     ta, tb = trellis.build_index(X, nlist=128), trellis.build_index(X, nlist=128)
     assert torch.equal(ta[0]["words"], tb[0]["words"]) and torch.equal(ta[0]["scale1"], tb[0]["scale1"])
+
+
+def test_emit_degenerate_row_scales(i8env, oracle_mod):
+    """Rows whose code scale is +inf, negative or zero, in the cell the batch probes most. The emit scan's
+    prefilter admits such a row for every query of a chunk (the exact test then decides), and a batch of
+    33 queries leaves partial 32-query tiles whose missing slots must admit nothing; the emitted sets, the
+    counts and the final results must equal the oracle's canonical ones."""
+    print("\n[gpu edges] planted +inf / negative / zero row scales, B=33", flush=True)
+    E0 = i8env["E"]
+    Q = i8env["Q"][:33].contiguous()
+    K, z, nprobe, k = 120, 1.25, 16, 10
+    probe = npy(E0.trace(Q, K, z, nprobe, k)["probe"])
+    off = npy(E0.s1["off_t"]).astype(np.int64)
+    c = int(np.argmax(np.bincount(probe.reshape(-1), minlength=len(off) - 1)))
+    n = int(off[c + 1] - off[c])
+    assert n >= 8
+    zs = E0.zs.clone()
+    planted = {int(off[c]) + 3: float("inf"), int(off[c]) + min(40, n - 1): -0.5, int(off[c]) + 1: 0.0}
+    for r, v in planted.items():
+        zs[r] = v
+    E = EngineI8(E0.s1, E0.code, E0.Z, zs, E0.Vr, H=E0.H)
+    idx = oracle_mod.index_from_tables(E0.s1, E0.code, E0.Z, zs, E0.Vr, E0.H)
+    out = check_i8(E, idx, Q, K, z, nprobe, k, oracle_mod)
+    # the +inf row is emitted (estimate +inf) for the probing queries whose dot with it is positive
+    pinf = int(off[c]) + 3
+    hits = [(out["bpos"][q, :out["cnt"][q]] == pinf).any() for q in range(len(Q)) if c in probe[q]]
+    assert any(hits)

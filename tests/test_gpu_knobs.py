@@ -41,6 +41,7 @@ CASES = {
     "route32_unsorted": dict(NROUTE=False, ROUTE16=False, UNSORTED=True),
     "proj": dict(NROUTE=False, PROJ=True),
     "k2": dict(K2=100),
+    "k2_nt2": dict(K2=100, NT=2),
     "sortroute": dict(SORTROUTE=True),
 }
 
@@ -56,9 +57,15 @@ def test_knob_matches_oracle(env, oracle_mod, case):
     tr = E.trace(Q, K, Z_, NPROBE, KK)
     torch.cuda.synchronize()
     ok_knobs = dict(MSZ=E.MSZ, RHO=E.RHO, BETA=E.BETA, DELTA=E.DELTA, LUTF=E.LUTF, LUTH=E.LUTH, NROUTE=E.NROUTE,
-                    ROUTE16=E.ROUTE16, UNSORTED=E.UNSORTED, K2=E.K2)
+                    ROUTE16=E.ROUTE16, UNSORTED=E.UNSORTED, K2=E.K2, NT=E.NT)
     out = oracle_mod.pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, knobs=ok_knobs, QM16=u16(tr["QM"]),
                               Zq16=u16(tr["Zq"]), zq=npy(tr["z"]), fallback=False)
+    if case == "proj":
+        # the library part of PROJ, fp16(QC + fp16(proj)) (throughput/enginei8.py:73), against the same BLAS
+        # product recomputed here: bit-exact
+        P = npy((tr["Qh"] @ E.W1h) @ E.mproj).astype(np.float32)
+        want = (npy(tr["QC"]).astype(np.float32)[:, None] + P).astype(np.float16)
+        assert np.array_equal(u16(tr["QM"]), want.view(np.uint16))
     assert np.array_equal(npy(tr["probe"]), out["probe"])
     if case == "route32_unsorted":
         assert np.all(np.diff(out["probe"], axis=1) > 0)
@@ -71,9 +78,11 @@ def test_knob_matches_oracle(env, oracle_mod, case):
     assert np.array_equal(npy(tr["est"])[ok].view(np.uint32), out["est"][ok].view(np.uint32))
     assert np.array_equal(npy(tr["I"])[ok], out["I"][ok])
     assert np.array_equal(npy(tr["reads"])[ok], out["reads"][ok])
-    if case == "k2":
+    if case.startswith("k2"):
         assert tr["pos"].shape[1] == 100 and tr["pos1"].shape[1] == K
     # the captured search gives the eager ids (the flagged queries go through the fallback)
     I, reads, ids = E.search(Q, K, Z_, NPROBE, KK)
     assert np.array_equal(npy(I)[ok], npy(tr["I"])[ok])
-    assert metrics.recall(npy(I), env["GT"]) >= 0.9
+    # ranking the K2 by two of the four tiers (a coarser estimate than the reference's NT = 3) keeps fewer
+    # of the true neighbours: 0.870 measured against 0.9+ for the other knobs
+    assert metrics.recall(npy(I), env["GT"]) >= (0.85 if case == "k2_nt2" else 0.9)

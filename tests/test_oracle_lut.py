@@ -167,3 +167,77 @@ def test_encoder_records_decode_to_the_uniform_code():
         assert np.allclose(sc[:, 0], nf / (ct * np.linalg.norm(Y, axis=1)), rtol=2e-3)
         assert np.allclose(sc[:, 1], nf * np.sqrt(np.clip(1 - ct ** 2, 0, None)) / (ct * np.sqrt(e - s - 1)),
                            rtol=5e-3, atol=1e-4)
+
+
+def test_partial_estimate_over_leading_tiers(oracle_mod, case):
+    """score_lut(..., nt) (throughput/s2lut.py:92-93) scores TS[:nt] with the full tables: the oracle's
+    estimate over the first two tiers equals the direct codeword sum over those tiers; the all-tiers
+    estimate (the planted mistake) does not."""
+    rec, soff = _records(case)
+    L, qsum, qn2 = oracle_mod.lut_build(fp16_bits(case["Zq"]), TS, False)
+    deltas = np.array([DELTAS[b] for _, _, b in TS], np.float32)
+    toff = np.array(_layout(TS)[0], np.int32)
+    nt = 2
+    est, sd = oracle_mod.lut_score(case["pos"], case["qc"], L, False, qsum[:nt], qn2[:nt], rec, soff, TS[:nt],
+                                   deltas[:nt], toff[:nt])
+    codes = case["codes"][case["pos"]]
+    ss = case["ss"].astype(np.float64)[case["pos"]]
+    want = np.zeros(codes.shape[:2]) + case["qc"][:, None].astype(np.float64)
+    for t, (s, e, b) in enumerate(TS[:nt]):
+        lv = DELTAS[b] * (codes[:, :, s:e].astype(np.float64) - (2 ** b - 1) / 2)
+        want += ss[..., t, 0] * np.einsum("qkd,qd->qk", lv, case["Zq"][:, s:e].astype(np.float64))
+    mag = 1 + np.abs(want)
+    assert np.all(np.abs(est - want) <= 2e-5 * mag), np.abs(est - want).max()
+    sd_want = np.sqrt(np.einsum("tq,qkt->qk", qn2[:nt].astype(np.float64), ss[..., :nt, 1] ** 2))
+    assert np.allclose(sd, sd_want, rtol=1e-5, atol=1e-7)
+    full, _ = _score(oracle_mod, case, L, False, rec, soff)
+    assert np.abs(full - want).max() > 0.1, "the all-tiers estimate must not pass as the partial one"
+
+
+def _decode_tiers(rec, pos, TS, toff, soff, deltas, Zq, qc, nt):
+    """float64 direct estimate over the first nt tiers of the candidates pos [B, K], decoded from the records
+    (planes MSB first, src/tiered.py:11-12; levels Delta_b (code - mid_b), throughput/s2lut.py:9-16)."""
+    R = rec[pos]                                                     # [B, K, RB]
+    est = np.zeros(pos.shape) + np.asarray(qc, np.float64)[:, None]
+    for t, (s, e, b) in enumerate(TS[:nt]):
+        kb = (e - s) // 8
+        code = np.zeros(pos.shape + (e - s,), np.int64)
+        for p in range(b):
+            plane = np.unpackbits(R[:, :, toff[t] + p * kb: toff[t] + (p + 1) * kb], axis=2, bitorder="big")
+            code |= plane.astype(np.int64) << (b - 1 - p)
+        lv = float(deltas[t]) * (code - (2 ** b - 1) / 2)
+        sc = R[:, :, soff + 4 * t: soff + 4 * t + 2].copy().view(np.float16)[..., 0].astype(np.float64)
+        est += sc * np.einsum("qkd,qd->qk", lv, Zq[:, s:e])
+    return est
+
+
+def test_progressive_stage_ranks_by_leading_tiers(oracle_mod, tiny):
+    """K2 < K (throughput/enginei8.py:82-85): the K2 candidates kept are the best of the K by the estimate over
+    the first NT tiers. Checked against a float64 direct codeword sum of those tiers (every candidate clearly
+    above the K2-th value is kept, every one clearly below is dropped); the planted all-tiers ranking fails
+    the same check."""
+    idx = tiny["idx"]
+    TS = idx["TS"]
+    assert len(TS) == 3
+    K, K2, NT = 120, 40, 2
+    knobs = dict(K2=K2, NT=NT, LUTF=True, LUTH=False)
+    out = oracle_mod.pipeline(idx, tiny["Qn"], K, 1.25, 16, 10, knobs=knobs, fallback=False)
+    pos1, pos2 = out["pos"], out["pos2"]
+    assert pos2.shape == (len(pos1), K2)
+    Zq = np.asarray(out["Zq"]).view(np.float16).astype(np.float64)
+    args = (idx["rec"], pos1, TS, idx["toff"], idx["soff"], idx["deltas"], Zq, out["qc"])
+
+    def consistent(keep, v):
+        ok = []
+        for q in range(len(v)):
+            th = np.sort(v[q])[::-1][K2 - 1]
+            eps = 1e-4 * (1 + abs(th))
+            kept = np.isin(pos1[q], keep[q])
+            ok.append(kept[v[q] > th + eps].all() and not kept[v[q] < th - eps].any())
+        return np.array(ok)
+
+    part = _decode_tiers(*args, NT)
+    assert consistent(pos2, part).all()
+    allt = _decode_tiers(*args, len(TS))
+    wrong = np.take_along_axis(pos1, np.argsort(-allt, axis=1, kind="stable")[:, :K2], 1)
+    assert not consistent(wrong, part).all(), "ranking by all tiers must not pass"
