@@ -324,7 +324,7 @@ int fvs_dense_threshold(const float *S, int64_t B, int32_t n, int32_t r, float *
  * est >= t0[q] increments cnt[q] (zeroed by the caller) and the first CAP of a query are stored at
  * bval[q*CAP + idx] = est, bpos[q*CAP + idx] = n (in no particular order).
  *   qs f32 and (mode 1) t0 f32 hold Bpad entries, zs fp16 holds Npad entries (entries past B and N are read,
- *   never used). R (the packed width Rp) a multiple of 128; Bpad a multiple of 128; Npad a multiple of 256.
+ *   never used). R (the packed width Rp) a multiple of 64; Bpad a multiple of 128; Npad a multiple of 256.
  */
 int fvs_dense_scan(int32_t mode, const int8_t *Qt, const float *qs, int64_t B, int64_t Bpad, const int8_t *Zt,
                    const uint16_t *zs, int64_t N, int64_t Npad, int32_t R, const float *t0, int32_t *cnt, float *bval,

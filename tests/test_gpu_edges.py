@@ -202,3 +202,4 @@ def test_emit_degenerate_row_scales(i8env, oracle_mod):
     pinf = int(off[c]) + 3
     hits = [(out["bpos"][q, :out["cnt"][q]] == pinf).any() for q in range(len(Q)) if c in probe[q]]
     assert any(hits)
+
