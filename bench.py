@@ -31,6 +31,7 @@ if int(os.environ.get("GPU_MAX_HW_QUEUES", "4")) < 8:
 METRIC = "QPS @ recall@10≥0.99, 1M×1536 fp16, batch 2000; % of int8-MFMA/HBM peak"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+FP32_VALU_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMDs x 16 lanes x 2 (fma) x 2.4 GHz
 CAL_BYTES = 256 << 20  # plain device copy of known size: the HBM counter calibration dispatch
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_i8_emit.throughput_1Mx1536.traffic.md")
 EMIT_KERNEL = "k_i8_emit"
@@ -541,13 +542,59 @@ def latency_mode(args):
                            fallback_queries=(E.nbad - nbad0) // 2, timed_queries=nb * B)
                 rows.append(row)
                 log(f"latency {row}")
+    scan = trellis_scan_roofline(E, Q, args, torch, np)
+    log(f"trellis scan {scan}")
     out = {"metric": "search latency per batch (median / p99 ms), trellis default engine, 1M x 1536",
            "unit": "ms", "n_gpus": 1, "higher_is_better": False, "dtype": "f32", "data": "synthetic",
            "config": {"workload": f"latency mode, {args.n}x{args.d} fp16 synthetic, batches {args.lat_batches}, "
                                   f"k={args.k}", "nlist": args.nlist, "build_s": round(build_s, 1),
                       "gpu_bytes_per_vector": round(E.gpu_bytes(), 1)},
-           "rows": rows}
+           "rows": rows, "trellis_scan": scan}
     print(json.dumps(out), flush=True)
+
+
+def trellis_scan_roofline(E, Q, args, torch, np, point=(256, 200)):
+    """The trellis stage-1 scan (fvs_tr_scan, both passes) at batches 64 and 2000, each pass launched alone
+    back to back between HIP events: algorithmic bytes = 38 per unique probed row (9 words + fp16 scale),
+    and the dot products' fp32 work = 2 x 256 flops per (query, probed row) pair. The kernel decodes every
+    row (a table lookup per coordinate) and then runs an fma chain per query, so the vector ALU bounds it,
+    not HBM: frac_valu is the dot products' rate against MI355X's fp32 vector peak."""
+    from fanarvse_paper_amd import _lib
+
+    s1 = E.s1
+    NC = len(s1["off"]) - 1
+    nprobe, K = point
+    L = int(s1["L"])
+    off = s1["off_t"].long()
+    sizes = off[1:] - off[:-1]
+    out = {}
+    for B in (64, 2000):
+        Qb = Q[:B].contiguous()
+        tr = E.trace(Qb, K, 2.0, nprobe, args.k)
+        Qr, QM, probe = tr["Qr"], tr["QM"], tr["probe"]
+        M, n1, r = E._params(K, nprobe, B=B)
+        pr, prn = _lib.pairs2(probe, n1, NC, QM, None, _lib.pairs_scratch(B, NC, Qb.device))
+        bm = torch.empty((B, n1, E.MB), dtype=torch.float32, device=Qb.device)
+        cnt = torch.empty((B,), dtype=torch.int32, device=Qb.device)
+        bval = torch.empty((B, M), dtype=torch.float32, device=Qb.device)
+        bpos = torch.empty((B, M), dtype=torch.int32, device=Qb.device)
+        half = B > 8
+        t_first = _time_launch(lambda: _lib.tr_scan(0, E.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm,
+                                                    MB=E.MB, n1=n1, half=half), args.kernel_reps, torch)
+        t_emit = _time_launch(lambda: _lib.tr_scan(1, E.blocks, Qr, prn, s1["words"], s1["scale1"], s1["tab"], L,
+                                                   t0=tr["t0"], cnt=cnt, bval=bval, bpos=bpos, CAP=M, half=half),
+                              args.kernel_reps, torch, setup=lambda: _lib.fill_u32(cnt, 0))
+        row = {}
+        for name, ms, ccnt in (("first_pass", t_first, pr[3]), ("emit", t_emit, prn[3])):
+            c = ccnt.long()
+            byt = float((sizes * (c > 0)).sum()) * 38.0
+            flops = 2.0 * 256 * float((sizes * c).sum())
+            tfl = flops / (ms * 1e-3) / 1e12
+            row[name] = {"ms": round(ms, 4), "bytes": byt, "GBps": round(byt / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "flops": flops,
+                         "TFLOPs": round(tfl, 2), "frac_valu": round(tfl / FP32_VALU_PEAK_TFLOPS, 4)}
+        out[f"batch_{B}"] = row
+    return out
 
 
 def tier_mode(args):
@@ -637,7 +684,11 @@ PCIE_PEAK_GBS = 63.0  # PCIe Gen5 x16, one direction
 
 def host_mode(args):
     """1.28M x 768, every per-vector array in pinned host memory, batch 2000, k=10.
-    Reports queries/s, bytes per vector on the GPU and the PCIe rate of the streamed stage-1 chunks."""
+    Reports queries/s, bytes per vector on the GPU, the time of each stage of a batch (main pass, the
+    fallback of its flagged queries, and the host's share), and the PCIe rate of the streamed stage 1: the
+    first pass of the main search is bound by its chunk copies, so its bytes over its time are the rate
+    the copies reach while the scans run (first_pass_GBps); each copy timed alone between events gives
+    copy_GBps_median."""
     import numpy as np
     import torch
 
@@ -671,17 +722,40 @@ def host_mode(args):
             E.search(Q, K, z, nprobe, args.k)
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / args.steps
+        # where a batch's time goes: events at the stage boundaries of one search (main pass and fallback)
+        E.phase_events = []
+        E.search(Q, K, z, nprobe, args.k)
+        torch.cuda.synchronize()
+        phases, passes = {"main": {}, "fallback": {}}, -1
+        ev = E.phase_events
+        for (_, a), (name, b) in zip(ev[:-1], ev[1:]):
+            if name == "start":  # a fallback pass starts a new sequence of marks
+                continue
+            passes += name == "dense products and routing"
+            ph = phases["main" if passes == 0 else "fallback"]
+            ph[name] = round(ph.get(name, 0.0) + a.elapsed_time(b), 3)
+        gpu_ms = sum(sum(v.values()) for v in phases.values())
+        phases["host"] = round(dt * 1e3 - gpu_ms, 3)  # flag sync, fallback set-up, ids mapped on the host
+        pass_bytes = sum(E._block_bytes(r1 - r0) for r0, r1, _, _ in E.chunks)
+        first_ms = phases["main"].get("first pass (streamed)", 0.0)
+        E.phase_events = None
+        # the PCIe rate of the streamed copies: a search whose chunk copies are queued one by one between
+        # timing events (the same copies and scans)
         E.timing, E.copy_events, E.copied_bytes = True, [], 0
         E.search(Q, K, z, nprobe, args.k)
         torch.cuda.synchronize()
         ct = sum(a.elapsed_time(b) for a, b, _ in E.copy_events) * 1e-3
         cb = sum(x for _, _, x in E.copy_events)
+        per_copy = sorted(x / (a.elapsed_time(b) * 1e-3) / 1e9 for a, b, x in E.copy_events)
         E.timing = False
         row = dict(nprobe=nprobe, K=K, z=z, recall=rec, qps=round(B / dt, 1), ms_per_batch=round(dt * 1e3, 3),
                    reads=round(float(reads.float().mean()), 2), fallback=E.nbad,
-                   stage1_streamed_MB=round(cb / 1e6, 1), pcie_GBps=round(cb / ct / 1e9, 2),
-                   pcie_frac=round(cb / ct / 1e9 / PCIE_PEAK_GBS, 3),
-                   stream_share_of_batch=round(ct / dt, 3))
+                   stage1_MB_per_pass=round(pass_bytes / 1e6, 1),
+                   first_pass_GBps=round(pass_bytes / (first_ms * 1e-3) / 1e9, 2) if first_ms else None,
+                   first_pass_pcie_frac=round(pass_bytes / (first_ms * 1e-3) / 1e9 / PCIE_PEAK_GBS, 3) if first_ms else None,
+                   stage1_streamed_MB=round(cb / 1e6, 1), copies=len(per_copy),
+                   copy_GBps_event_timed=round(cb / ct / 1e9, 2),
+                   copy_GBps_median=round(per_copy[len(per_copy) // 2], 2), phases_ms=phases)
         rows.append(row)
         log(f"host {row}")
     out = {"metric": "QPS of the host-resident engine (< 8 B/vector on the GPU), PCIe GB/s of the streamed stage 1",

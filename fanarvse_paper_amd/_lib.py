@@ -8,6 +8,7 @@ fails.
 import ctypes
 import os
 
+import numpy as np
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -49,7 +50,9 @@ SIGNATURES = {
     "fvs_refine_rows": [P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "fvs_trellis_encode": [P, P, I64, I32, P, I32, P, I32, P, P, P],
     "fvs_tr_scan": [I32, I32, P, P, P, P, P, P, P, P, P, P, I64, I32, P, P, I32, I32, I32, P, P, P, P, P, P, I32, I32, I32,
-                    P],
+                    I32, P],
+    "fvs_tr_scan_streamed": [I32, I32, P, P, P, P, I64, P, P, P, P, P, P, P, P, P, P, I32, P, I32, I32, I32, P, P, P,
+                             P, P, P, I32, I32, I32, I32, P],
     "fvs_route_topk_scaled": [P, P, P, I64, I32, I32, P, P],
     "fvs_tiered_score": [P, P, P, I32, P, I64, I32, I32, I32, P, P, P, P, I64, I32, P, P, P],
 }
@@ -429,11 +432,12 @@ def trellis_encode(Zs, nz, tab, L, words, scale1, paths=None):
 
 
 def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1,
-            MB=1, n1=1, row0=0, half=False):
+            MB=1, n1=1, row0=0, half=False, nsplit=1):
     """Trellis stage-1 first pass (mode 0) or emit (mode 1) over the static (cell, block) items
     (src/s1cell.py:121-154 semantics with the canonical fp32 dot of include/fvs.h). words/scale1 hold index
     rows row0 .. (device or pinned host memory). half: both dot operands rounded to fp16 first (the
-    reference's tensor-core operands for batches above 8 queries)."""
+    reference's tensor-core operands for batches above 8 queries). nsplit: waves per item, each taking a
+    consecutive part of the item's queries (for launches over few items)."""
     pcell, pblk, ps, pe = blocks
     qid, qrank, coff, ccnt, qcp = pr
     P_ = pcell.shape[0]
@@ -450,7 +454,36 @@ def tr_scan(mode, blocks, Qr, pr, words, scale1, tab, L, t0=None, cnt=None, bval
                              _dev(words, i32, "words", host_ok=True), row0, W,
                              _dev(scale1, torch.float16, "scale1", (N,), host_ok=True), _dev(tab, f32, "tab", (2 ** L,)), L, R,
                              int(bool(half)), _dev(qcp, f32, "qcp"), _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"),
-                             _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1, _stream()), "fvs_tr_scan")
+                             _opt(bpos, i32, "bpos"), _opt(bm, f32, "bm"), CAP, MB, n1, int(nsplit), _stream()),
+           "fvs_tr_scan")
+
+
+def tr_scan_streamed(mode, chunk_tab, stage_h, slots, side, blocks, Qr, pr, tab, L, W, t0=None, cnt=None, bval=None,
+                     bpos=None, bm=None, CAP=1, MB=1, n1=1, half=True, nsplit=1):
+    """One streamed stage-1 pass of the host-resident engine (fvs_tr_scan_streamed): chunk_tab int64 numpy
+    [nchunks, 5] (first row, end row, first item, end item, byte offset in stage_h), stage_h pinned uint8,
+    slots two device uint8 buffers, side the copy stream; the other arguments as tr_scan's."""
+    pcell, pblk, ps, pe = blocks
+    qid, qrank, coff, ccnt, qcp = pr
+    B, R = Qr.shape
+    tab_ = np.ascontiguousarray(chunk_tab, dtype=np.int64)
+    if tab_.ndim != 2 or tab_.shape[1] != 5:
+        raise ValueError("tr_scan_streamed: chunk table must be [nchunks, 5]")
+    if mode == 0 and (bm is None or bm.numel() != B * n1 * MB):
+        raise ValueError("tr_scan_streamed: bm must hold B*n1*MB values")
+    if mode == 1 and (bval is None or bval.shape != (B, CAP) or bpos.shape != (B, CAP) or cnt.shape != (B,)):
+        raise ValueError("tr_scan_streamed: emit buffers must be [B, CAP]")
+    if slots[0].numel() != slots[1].numel():
+        raise ValueError("tr_scan_streamed: slots of different sizes")
+    f32, i32, u8 = torch.float32, torch.int32, torch.uint8
+    _check(lib().fvs_tr_scan_streamed(
+        mode, tab_.shape[0], tab_.ctypes.data_as(P), _dev(stage_h, u8, "stage_h", host_ok=True),
+        _dev(slots[0], u8, "slot0"), _dev(slots[1], u8, "slot1"), slots[0].numel(), P(side.cuda_stream),
+        _dev(Qr, f32, "Qr"), _dev(qid, i32, "qid"), _dev(qrank, i32, "qrank"), _dev(coff, i32, "coff"),
+        _dev(ccnt, i32, "ccnt"), _dev(pcell, i32, "pcell"), _dev(pblk, i32, "pblk"), _dev(ps, i32, "ps"),
+        _dev(pe, i32, "pe"), W, _dev(tab, f32, "tab", (2 ** L,)), L, R, int(bool(half)), _dev(qcp, f32, "qcp"),
+        _opt(t0, f32, "t0"), _opt(cnt, i32, "cnt"), _opt(bval, f32, "bval"), _opt(bpos, i32, "bpos"),
+        _opt(bm, f32, "bm"), CAP, MB, n1, int(nsplit), _stream()), "fvs_tr_scan_streamed")
 
 
 def route_topk_scaled(QM, scale, nprobe, qadd=None):

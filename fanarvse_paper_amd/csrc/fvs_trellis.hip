@@ -6,6 +6,7 @@
 // bits[j .. j+L) read MSB first and the decoded coordinate j is tab[state_j]. The stream is stored
 // as W = ceil((R + L - 1) / 32) 32-bit words, first bit in the most significant position.
 #include <algorithm>
+#include <mutex>
 
 #include "fvs_common.h"
 
@@ -138,6 +139,9 @@ __global__ __launch_bounds__(256) void k_trellis_encode(const float *__restrict_
 // mode 0: bm[(q*n1 + qrank)*MB + blk - cs/32] = max over the block's rows in the cell.
 // mode 1: every (q, row) with est >= t0[q] is appended to the query's buffer (one atomic each).
 // words and scale1 hold rows row0 .. of the index (a staged chunk, or the whole index with row0 = 0).
+// A launch over few items (a staged chunk of the host-resident engine) splits each item's queries into
+// nsplit consecutive parts, one wave each, so that the launch still fills the GPU; a (query, row) pair is
+// computed by exactly one wave either way, with the same arithmetic.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, const int32_t *__restrict__ qid,
                                                  const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff,
@@ -149,19 +153,23 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
                                                  int L, int half, const float *__restrict__ qcp,
                                                  const float *__restrict__ t0,
                                                  int32_t *__restrict__ cnt, float *__restrict__ bval,
-                                                 int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1) {
+                                                 int32_t *__restrict__ bpos, float *__restrict__ bm, int CAP, int MB, int n1,
+                                                 int nsplit) {
   __shared__ float stab[1 << kMaxL];
   __shared__ float4 qbuf[4][kTrR / 4];  // per wave: the query vector of the current step
   const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   const int S = 1 << L;
   for (int i = tid; i < S; i += 256) stab[i] = half ? fvs_round_h(tab[i]) : tab[i];
   __syncthreads();
-  const int p = blockIdx.x * 4 + w;
-  if (p >= P) return;
+  const int64_t u = (int64_t)blockIdx.x * 4 + w;  // work unit: item p, part `part` of its queries
+  if (u >= (int64_t)P * nsplit) return;
+  const int p = (int)(u / nsplit), part = (int)(u - (int64_t)p * nsplit);
   const int c = pcell[p];
-  const int qn = ccnt[c];
-  if (qn == 0) return;
-  const int qoff = coff[c];
+  const int qcell = ccnt[c];
+  const int qlo = (int)((int64_t)qcell * part / nsplit), qhi = (int)((int64_t)qcell * (part + 1) / nsplit);
+  const int qn = qhi - qlo;
+  if (qn <= 0) return;
+  const int qoff = coff[c] + qlo;  // this part's pairs: qoff .. qoff + qn - 1
   const int blk = pblk[p], cs = ps[p], ce = pe[p];
   const int h = lane >> 5, li = lane & 31;
   const int r = blk * 32 + li;
@@ -351,8 +359,9 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
                            const uint16_t *scale1,
                            const float *tab, int32_t L, int32_t R, int32_t half, const float *qcp, const float *t0,
                            int32_t *cnt, float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1,
-                           void *stream) {
+                           int32_t nsplit, void *stream) {
   if (R != kTrR) return FVS_E_SHAPE;
+  if (nsplit < 1 || nsplit > 64) return FVS_E_ARG;
   if (mode != 0 && mode != 1) return FVS_E_ARG;
   if (half != 0 && half != 1) return FVS_E_ARG;
   if (L < 2 || L > kMaxL || W != (R + L - 1 + 31) / 32 || W > 10 || P < 0 || row0 < 0) return FVS_E_ARG;
@@ -360,17 +369,87 @@ extern "C" int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32
   if (!Qr || !qid || !coff || !ccnt || !pcell || !pblk || !ps || !pe || !words || !scale1 || !tab || !qcp)
     return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)((P + 3) / 4));
+  const dim3 grid((unsigned)(((int64_t)P * nsplit + 3) / 4));
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<0>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1, nsplit);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_tr_scan<1>, grid, dim3(256), 0, st, Qr, qid, qrank, coff, ccnt, pcell, pblk, ps, pe, P, words,
-                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1);
+                       row0, W, scale1, tab, L, half, qcp, t0, cnt, bval, bpos, bm, CAP, MB, n1, nsplit);
   }
   return fvs_launch_status();
+}
+
+namespace {
+
+// Events that order one streamed pass (start, ready[2], done[2]), created once per device.
+hipError_t streamed_events(hipEvent_t *&ev) {
+  static std::mutex mu;
+  static hipEvent_t evs[64][5];
+  static bool made[64] = {false};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!made[dev]) {
+    for (int k = 0; k < 5; k++) {
+      e = hipEventCreateWithFlags(&evs[dev][k], hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+    }
+    made[dev] = true;
+  }
+  ev = evs[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int fvs_tr_scan_streamed(int32_t mode, int32_t nchunks, const int64_t *chunks, const uint8_t *stage_h,
+                                    uint8_t *slot0, uint8_t *slot1, int64_t slot_bytes, void *side, const float *Qr,
+                                    const int32_t *qid, const int32_t *qrank, const int32_t *coff, const int32_t *ccnt,
+                                    const int32_t *pcell, const int32_t *pblk, const int32_t *ps, const int32_t *pe,
+                                    int32_t W, const float *tab, int32_t L, int32_t R, int32_t half, const float *qcp,
+                                    const float *t0, int32_t *cnt, float *bval, int32_t *bpos, float *bm, int32_t CAP,
+                                    int32_t MB, int32_t n1, int32_t nsplit, void *stream) {
+  if (nchunks < 0) return FVS_E_ARG;
+  if (nchunks == 0) return FVS_OK;
+  if (!chunks || !stage_h || !slot0 || !slot1 || !pcell || !pblk || !ps || !pe || W <= 0) return FVS_E_ARG;
+  // every chunk's block fits a slot, and its items are a range of the work list, before anything is queued
+  for (int i = 0; i < nchunks; i++) {
+    const int64_t *c = chunks + 5 * (int64_t)i;
+    const int64_t n = c[1] - c[0];
+    if (n <= 0 || c[0] < 0 || c[2] < 0 || c[3] < c[2] || c[4] < 0) return FVS_E_ARG;
+    if (n * 4 * W + (2 * n + 15) / 16 * 16 > slot_bytes) return FVS_E_CAPACITY;
+  }
+  hipEvent_t *ev = nullptr;
+  hipError_t e = streamed_events(ev);
+  if (e != hipSuccess) return (int)e;
+  hipStream_t st = (hipStream_t)stream, sd = (hipStream_t)side;
+  // the slots' previous contents have been read by the work already queued on `stream`
+  if ((e = hipEventRecord(ev[0], st)) != hipSuccess) return (int)e;
+  if ((e = hipStreamWaitEvent(sd, ev[0], 0)) != hipSuccess) return (int)e;
+  for (int i = 0; i < nchunks; i++) {
+    const int64_t *c = chunks + 5 * (int64_t)i;
+    const int64_t r0 = c[0], n = c[1] - c[0];
+    const int i0 = (int)c[2], np = (int)(c[3] - c[2]);
+    const int slot = i & 1;
+    uint8_t *buf = slot ? slot1 : slot0;
+    const size_t nb = (size_t)(n * 4 * W + (2 * n + 15) / 16 * 16);
+    if (i >= 2 && (e = hipStreamWaitEvent(sd, ev[3 + slot], 0)) != hipSuccess) return (int)e;  // scan i-2 done
+    if ((e = hipMemcpyAsync(buf, stage_h + c[4], nb, hipMemcpyHostToDevice, sd)) != hipSuccess) return (int)e;
+    if ((e = hipEventRecord(ev[1 + slot], sd)) != hipSuccess) return (int)e;
+    if ((e = hipStreamWaitEvent(st, ev[1 + slot], 0)) != hipSuccess) return (int)e;
+    const int rc = fvs_tr_scan(mode, np, Qr, qid, qrank, coff, ccnt, pcell + i0, pblk + i0, ps + i0, pe + i0,
+                               reinterpret_cast<const uint32_t *>(buf), r0, W,
+                               reinterpret_cast<const uint16_t *>(buf + n * 4 * W), tab, L, R, half, qcp, t0, cnt,
+                               bval, bpos, bm, CAP, MB, n1, nsplit, stream);
+    if (rc != FVS_OK) return rc;
+    if ((e = hipEventRecord(ev[3 + slot], st)) != hipSuccess) return (int)e;
+  }
+  return FVS_OK;
 }
 
 extern "C" int fvs_tiered_score(const int32_t *pos, const float *qc, const float *Zq, int32_t D, const uint8_t *rec,

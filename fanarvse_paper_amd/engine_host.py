@@ -13,9 +13,10 @@ switches are kept (space_x.py:19-36):
   vp16: W1 and VP in fp16, with Qr = f32(fp16(Qb) @ W1h) and Zq = f32(fp16(Qb) @ VP16).
 The default (proj off, vp16 on, 16,384-row chunks) stays under 8 B per vector at 1.28M vectors.
 
-Stage 1 streams: the index is cut into cell-aligned chunks of about CHUNK rows; a side stream copies
-chunk i+1's words and scales into the free staging slot (hipMemcpyAsync) while the main stream scans
-chunk i (fvs_tr_scan with row0 = the chunk's first row). Stage 2 and stage 3 read their records and
+Stage 1 streams: the index is cut into cell-aligned chunks of about CHUNK rows, each stored in pinned
+memory as one contiguous block (its rows' trellis words, then their scales, padded to 16 bytes); a side
+stream copies chunk i+1's block into the free staging slot with one hipMemcpyAsync while the main stream
+scans chunk i (fvs_tr_scan with row0 = the chunk's first row). Stage 2 and stage 3 read their records and
 rows zero-copy from pinned memory. Results equal EngineS's with the projected-means routing.
 """
 import numpy as np
@@ -42,8 +43,6 @@ class SpaceX(EngineS):
         self.order_np = s1["order"].cpu().numpy()
         order = s1["order"].long()
         self.Hs = _pin(H16[order.to(H16.device)])
-        self.words_h = _pin(s1["words"])
-        self.scale1_h = _pin(s1["scale1"])
         self.proj, self.vp16 = proj, vp16
         VP = code["VP"].to(dev)
         self.code = dict(TS=code["TS"], rec=_pin(code["rec"]), RB=code["RB"], soff=code["soff"], toff=code["toff"],
@@ -54,18 +53,41 @@ class SpaceX(EngineS):
                        W1=W1.half().contiguous() if vp16 else W1, tab=s1["tab"].to(dev), L=int(s1["L"]),
                        inv_mnorm=s1["inv_mnorm"].float().to(dev), means=means)
         self.W1, self.inv_mnorm, self.means = self.s1["W1"], self.s1["inv_mnorm"], means
-        self.N = int(self.words_h.shape[0])
-        self.Wd = int(self.words_h.shape[1])
+        self.N = int(s1["words"].shape[0])
+        self.Wd = int(s1["words"].shape[1])
         self.blocks, self.MB = index.static_blocks(self.s1["off_t"], self.BN)
         self.H = self.Hs
         self.graphs = {}
         self.nbad = 0
         self._chunks()
+        self._stage_host(s1["words"], s1["scale1"])
         self.side = torch.cuda.Stream()
-        self.slots = [(torch.empty((self.chunk_rows, self.Wd), dtype=torch.int32, device=dev),
-                       torch.empty((self.chunk_rows,), dtype=torch.float16, device=dev)) for _ in range(2)]
+        self.slots = [torch.empty((self._block_bytes(self.chunk_rows),), dtype=torch.uint8, device=dev)
+                      for _ in range(2)]
         self.copied_bytes = 0
         self.copy_events = []
+        self.phase_events = None  # when a list, _run records (name, event) at each stage boundary
+        self._cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        self._np = 1  # n_p of the search in progress (sets the query-split of the chunk scans)
+
+    def _block_bytes(self, rows):
+        """Bytes of one chunk's block: rows x Wd int32 words, then rows fp16 scales, padded to 16 bytes."""
+        return rows * 4 * self.Wd + -(-rows * 2 // 16) * 16
+
+    def _stage_host(self, words, scale1):
+        """The stage-1 arrays in pinned memory, one contiguous block per chunk (words, then scales)."""
+        offs, at = [], 0
+        for r0, r1, _, _ in self.chunks:
+            offs.append(at)
+            at += self._block_bytes(r1 - r0)
+        self.block_off = offs
+        self.chunk_tab = np.array([(r0, r1, i0, i1, o) for (r0, r1, i0, i1), o in zip(self.chunks, offs)], np.int64)
+        self.stage_h = torch.empty((at,), dtype=torch.uint8, pin_memory=True)
+        w, sc = words.cpu(), scale1.cpu()
+        for (r0, r1, _, _), o in zip(self.chunks, offs):
+            n = r1 - r0
+            self.stage_h[o:o + 4 * self.Wd * n] = w[r0:r1].contiguous().view(torch.uint8).reshape(-1)
+            self.stage_h[o + 4 * self.Wd * n:o + 4 * self.Wd * n + 2 * n] = sc[r0:r1].contiguous().view(torch.uint8)
 
     def _params(self, K, nprobe, rho_override=None, M_override=None):
         NC = len(self.s1["off"]) - 1
@@ -98,31 +120,53 @@ class SpaceX(EngineS):
 
     timing = False  # when set, every chunk copy is bracketed by events (copy_events) for the PCIe rate
 
+    def _nsplit(self, items, B, NC):
+        """Waves per item of a chunk's scan: a chunk holds a few hundred items, so its launch would leave most
+        of the GPU idle at one wave per item; its queries per cell (B x n_p / NC on average, at least 16 per
+        part) are split over up to 8 waves instead (the same results)."""
+        qpc = B * self._np / max(NC, 1)
+        fill = -(-32 * self._cus // max(items, 1))  # parts for about eight workgroups per CU
+        return int(max(1, min(8, fill, qpc // 16)))
+
     def _scan_streamed(self, mode, Qr, pr, **kw):
-        """One stage-1 pass over every chunk, copies on the side stream overlapped with the scans."""
+        """One stage-1 pass over every chunk, copies on the side stream overlapped with the scans: one library
+        call (fvs_tr_scan_streamed) queues every chunk's copy and scan; with `timing` set, the same steps are
+        queued from here with every copy bracketed by timing events."""
+        nsplit = self._nsplit(max(i1 - i0 for _, _, i0, i1 in self.chunks), Qr.shape[0], pr[2].numel())
+        if not self.timing:
+            _lib.tr_scan_streamed(mode, self.chunk_tab, self.stage_h, self.slots, self.side, self.blocks, Qr, pr,
+                                  self.s1["tab"], self.s1["L"], self.Wd, half=True, nsplit=nsplit, **kw)
+            self.copied_bytes += int(sum(self._block_bytes(r1 - r0) for r0, r1, _, _ in self.chunks))
+            return
         main = torch.cuda.current_stream()
+        self.side.wait_stream(main)  # the slots' previous contents have been scanned
         done = [None, None]
         for i, (r0, r1, i0, i1) in enumerate(self.chunks):
             slot = i % 2
-            w, s = self.slots[slot]
+            n = r1 - r0
+            nb = self._block_bytes(n)
+            buf = self.slots[slot]
             with torch.cuda.stream(self.side):
                 if done[slot] is not None:
                     self.side.wait_event(done[slot])
                 if self.timing:
                     a = torch.cuda.Event(enable_timing=True)
                     a.record(self.side)
-                w[:r1 - r0].copy_(self.words_h[r0:r1], non_blocking=True)
-                s[:r1 - r0].copy_(self.scale1_h[r0:r1], non_blocking=True)
+                o = self.block_off[i]
+                buf[:nb].copy_(self.stage_h[o:o + nb], non_blocking=True)
                 ready = torch.cuda.Event(enable_timing=self.timing)
                 ready.record(self.side)
                 if self.timing:
-                    self.copy_events.append((a, ready, (r1 - r0) * (4 * self.Wd + 2)))
-            self.copied_bytes += (r1 - r0) * (4 * self.Wd + 2)
+                    self.copy_events.append((a, ready, nb))
+            self.copied_bytes += nb
             main.wait_event(ready)
+            w = buf[:4 * self.Wd * n].view(torch.int32).view(n, self.Wd)
+            s = buf[4 * self.Wd * n:4 * self.Wd * n + 2 * n].view(torch.float16)
             blocks = tuple(b[i0:i1] for b in self.blocks)
             # fp16 operands at every batch size: the reference's host-resident engine always runs
             # search_static (host_resident/space_x.py:15,42)
-            _lib.tr_scan(mode, blocks, Qr, pr, w, s, self.s1["tab"], self.s1["L"], row0=r0, half=True, **kw)
+            _lib.tr_scan(mode, blocks, Qr, pr, w, s, self.s1["tab"], self.s1["L"], row0=r0, half=True, nsplit=nsplit,
+                         **kw)
             ev = torch.cuda.Event()
             ev.record(main)
             done[slot] = ev
@@ -135,13 +179,17 @@ class SpaceX(EngineS):
         scratch = _lib.pairs_scratch(B, NC, dev)
         pr, prn = _lib.pairs2(probe, n1, NC, QM, None, scratch, qadd=QC)
         bm = torch.empty((B, n1, self.MB), dtype=torch.float32, device=dev)
+        self._mark("pair lists")
         self._scan_streamed(0, Qr, pr, bm=bm, MB=self.MB, n1=n1)
+        self._mark("first pass (streamed)")
         cnt = torch.empty((B,), dtype=torch.int32, device=dev)  # zeroed by the threshold kernel
         t0 = _lib.threshold(bm, probe, self.s1["off_t"], n1, self.MB, r, cnt)
         bval = torch.empty((B, M), dtype=torch.float32, device=dev)
         bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
         pr = prn
+        self._mark("threshold")
         self._scan_streamed(1, Qr, pr, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
+        self._mark("emit pass (streamed)")
         pos, est1, ok, _ = _lib.select(bval, bpos, cnt, K, 0, None)
         self._bm, self._t0, self._cnt, self._bval, self._bpos, self._n1, self._M = bm, t0, cnt, bval, bpos, n1, M
         return pos, ok.view(torch.bool)  # the kernel writes 0 / 1 bytes: a view, no conversion kernel
@@ -166,12 +214,26 @@ class SpaceX(EngineS):
         self._est, self._sd = est, sd
         return _lib.refine(est, sd, pos, None, self.Hs, Qb, z, k)
 
+    def _mark(self, name):
+        if self.phase_events is not None:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.phase_events.append((name, ev))
+
     def _run(self, Qb, K, z, nprobe, k, rho_override=None, M_override=None, dense=None):
+        self._mark("start")
         Qr, QC, QM, Zq = dense if dense is not None else self._dense(Qb)
         qadd = QC if self.proj else None
+        self._np = nprobe
         probe = _lib.route_topk_scaled(QM, self.inv_mnorm, nprobe, qadd=qadd)
+        self._mark("dense products and routing")
         pos, ok = self.stage1(Qr, QM, probe, K, rho_override, M_override, QC=qadd)
-        ids, I, scores, reads = self._finish(Qb, QC, Zq, pos, z, k)
+        self._mark("stage 1 (streamed)")
+        est, sd = _lib.tiered_score(pos, QC, Zq, self.code)
+        self._est, self._sd = est, sd
+        self._mark("stage 2 (records zero-copy)")
+        ids, I, scores, reads = _lib.refine(est, sd, pos, None, self.Hs, Qb, z, k)
+        self._mark("refine (rows zero-copy)")
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq)
 
     def search(self, Qb, K, z, nprobe, k, ret_scores=False, sorted_ids=False):

@@ -366,13 +366,35 @@ int fvs_trellis_encode(const float *Zs, const float *nz, int64_t n, int32_t R, c
  *   147,151-152; src/s1small_cell.py:57-59); half = 0 keeps fp32 operands, as its small-batch kernels do
  *   (src/s1small_cell.py:17-21,101). The products of fp16 operands are exact in fp32, so the accumulation
  *   order above is the only rounding left.
+ * nsplit (1 .. 64): each item's queries are split into nsplit consecutive parts, one wave each (the same
+ * results; for launches over few items, such as the host-resident engine's streamed chunks).
  * R must be 256; 2 <= L <= 12.
  */
 int fvs_tr_scan(int32_t mode, int32_t P, const float *Qr, const int32_t *qid, const int32_t *qrank,
                 const int32_t *coff, const int32_t *ccnt, const int32_t *pcell, const int32_t *pblk, const int32_t *ps,
                 const int32_t *pe, const uint32_t *words, int64_t row0, int32_t W, const uint16_t *scale1, const float *tab,
                 int32_t L, int32_t R, int32_t half, const float *qcp, const float *t0, int32_t *cnt, float *bval,
-                int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, void *stream);
+                int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1, int32_t nsplit, void *stream);
+
+/*
+ * The host-resident engine's streamed stage-1 pass (config 5; the reference reads the stage-1 codes
+ * zero-copy, host_resident/space_x.py:17-32; here the code tiles are copied, as the configuration asks):
+ * for each chunk i, one hipMemcpyAsync on `side` copies the chunk's block -- its rows' trellis words
+ * (int32 [n, W]), then their fp16 scales, padded to 16 bytes -- from pinned host memory `stage_h` into
+ * staging slot i % 2 (slot_bytes each), and `stream` runs fvs_tr_scan over the chunk's items once the
+ * copy has landed (words, scale1 = the slot, row0 = the chunk's first row); a slot is refilled only after
+ * the scan that read it, and the first copies wait for the work already queued on `stream`.
+ * chunks: HOST int64 [nchunks][5] = (first row, end row, first item, end item, byte offset of the block in
+ * stage_h). The other arguments are fvs_tr_scan's, with the work list (pcell, pblk, ps, pe) of the whole
+ * index. The ordering events are created once per device and reused: calls on one device must not overlap.
+ */
+int fvs_tr_scan_streamed(int32_t mode, int32_t nchunks, const int64_t *chunks, const uint8_t *stage_h,
+                         uint8_t *slot0, uint8_t *slot1, int64_t slot_bytes, void *side, const float *Qr,
+                         const int32_t *qid, const int32_t *qrank, const int32_t *coff, const int32_t *ccnt,
+                         const int32_t *pcell, const int32_t *pblk, const int32_t *ps, const int32_t *pe, int32_t W,
+                         const float *tab, int32_t L, int32_t R, int32_t half, const float *qcp, const float *t0,
+                         int32_t *cnt, float *bval, int32_t *bpos, float *bm, int32_t CAP, int32_t MB, int32_t n1,
+                         int32_t nsplit, void *stream);
 
 /*
  * Routing on fp32 keys (a7 for the default engine). Replaces route() (src/engine_cell.py:40-42):

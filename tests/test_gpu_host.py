@@ -55,8 +55,8 @@ def test_gpu_bytes_per_vector(env):
     N = E.N
     fixed = sum(t.numel() * t.element_size() for t in (E.means, E.W1, E.code["VP"], E.code["cb"], E.s1["tab"],
                                                        E.s1["off_t"], E.s1["inv_mnorm"], E.s1["c"]))
-    fixed += sum(w.numel() * w.element_size() + s.numel() * s.element_size() for w, s in E.slots)
+    fixed += sum(b.numel() * b.element_size() for b in E.slots)
     per_vector = E.gpu_bytes() - fixed / N
     assert per_vector <= 0.6, per_vector
-    assert E.Hs.is_pinned() and E.words_h.is_pinned() and E.code["rec"].is_pinned()
-    assert not E.Hs.is_cuda and not E.words_h.is_cuda
+    assert E.Hs.is_pinned() and E.stage_h.is_pinned() and E.code["rec"].is_pinned()
+    assert not E.Hs.is_cuda and not E.stage_h.is_cuda

@@ -264,3 +264,41 @@ def test_dense_small_products_accuracy(env, B):
     ref = qh @ m
     tol = bound(qh, m) + ref.abs() * 2.0 ** -11
     assert ((QM.double().cpu() - ref).abs() <= tol + 1e-7).all()
+
+
+@pytest.mark.parametrize("nsplit", [3, 8])
+def test_query_split_matches_one_wave_per_item(env, nsplit):
+    """fvs_tr_scan with each item's queries split over nsplit waves gives the one-wave result bit for bit: the
+    block maxima of the first pass, and the counts and emitted sets of the emit pass."""
+    E, Q = env["E"], env["Q"]
+    s1 = E.s1
+    Qr, QC, QM, Zq = E._dense(Q)
+    probe = _lib.route_topk_scaled(QM, s1["inv_mnorm"], NPROBE)
+    NC = len(s1["off"]) - 1
+    B = Q.shape[0]
+    M, n1, r = E._params(K, NPROBE, B=B)
+    pr, prn = _lib.pairs2(probe, n1, NC, QM, None, _lib.pairs_scratch(B, NC, Q.device))
+    L = int(s1["L"])
+    res = []
+    for ns in (1, nsplit):
+        bm = torch.full((B, n1, E.MB), -7.0, device=Q.device)
+        _lib.tr_scan(0, E.blocks, Qr, pr, s1["words"], s1["scale1"], s1["tab"], L, bm=bm, MB=E.MB, n1=n1, half=True,
+                     nsplit=ns)
+        cnt = torch.empty((B,), dtype=torch.int32, device=Q.device)
+        t0 = _lib.threshold(bm, probe, s1["off_t"], n1, E.MB, r, cnt)
+        bval = torch.empty((B, M), dtype=torch.float32, device=Q.device)
+        bpos = torch.empty((B, M), dtype=torch.int32, device=Q.device)
+        _lib.tr_scan(1, E.blocks, Qr, prn, s1["words"], s1["scale1"], s1["tab"], L, t0=t0, cnt=cnt, bval=bval, bpos=bpos,
+                     CAP=M, half=True, nsplit=ns)
+        torch.cuda.synchronize()
+        res.append((npy(bm), npy(t0), npy(cnt), npy(bval), npy(bpos)))
+    (bm1, t01, c1, v1, p1), (bm2, t02, c2, v2, p2) = res
+    assert np.array_equal(bm1.view(np.uint32), bm2.view(np.uint32))
+    assert np.array_equal(t01.view(np.uint32), t02.view(np.uint32))
+    assert np.array_equal(c1, c2)
+    for q in range(B):
+        n = min(int(c1[q]), M)
+        if c1[q] > M:
+            continue
+        assert sorted(zip(p1[q, :n].tolist(), v1[q, :n].view(np.uint32).tolist())) == \
+            sorted(zip(p2[q, :n].tolist(), v2[q, :n].view(np.uint32).tolist())), q
