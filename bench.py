@@ -702,15 +702,18 @@ def host_mode(args):
     Q = datagen.gen(B, d, args.clusters, 0.7, seed=1, device=dev, dtype=torch.float32)
     GT = datagen.ground_truth(X, Q, args.k).cpu().numpy()
     s1, code = trellis.build_index(X, nlist=args.nlist)
-    E = SpaceX(s1, code, X)
+    engines = {"zero-copy": SpaceX(s1, code, X), "copy": SpaceX(s1, code, X, staging="copy")}
     del s1, code
     X = None
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    log(f"host-resident index ready in {time.time() - t:.1f}s; GPU bytes/vector {E.gpu_bytes():.2f}; "
-        f"{len(E.chunks)} chunks of <= {E.chunk_rows} rows")
+    Ec = engines["copy"]
+    log(f"host-resident index ready in {time.time() - t:.1f}s; GPU bytes/vector "
+        f"{ {k_: round(e.gpu_bytes(), 2) for k_, e in engines.items()} }; copy staging: {len(Ec.chunks)} chunks "
+        f"of <= {Ec.chunk_rows} rows")
     rows = []
-    for p in args.lat_points.split(","):
+    for staging, p in ((st, p) for st in engines for p in args.lat_points.split(",")):
+        E = engines[staging]
         nprobe, K = (int(v) for v in p.split(":"))
         z = 2.0
         I, reads, _ = E.search(Q, K, z, nprobe, args.k)
@@ -736,32 +739,38 @@ def host_mode(args):
             ph[name] = round(ph.get(name, 0.0) + a.elapsed_time(b), 3)
         gpu_ms = sum(sum(v.values()) for v in phases.values())
         phases["host"] = round(dt * 1e3 - gpu_ms, 3)  # flag sync, fallback set-up, ids mapped on the host
-        pass_bytes = sum(E._block_bytes(r1 - r0) for r0, r1, _, _ in E.chunks)
+        if staging == "copy":
+            pass_bytes = sum(E._block_bytes(r1 - r0) for r0, r1, _, _ in E.chunks)
+        else:
+            pass_bytes = E.N * (4 * E.Wd + 2)  # every row's words and scale, read once
         first_ms = phases["main"].get("first pass (streamed)", 0.0)
         E.phase_events = None
-        # the PCIe rate of the streamed copies: a search whose chunk copies are queued one by one between
-        # timing events (the same copies and scans)
-        E.timing, E.copy_events, E.copied_bytes = True, [], 0
-        E.search(Q, K, z, nprobe, args.k)
-        torch.cuda.synchronize()
-        ct = sum(a.elapsed_time(b) for a, b, _ in E.copy_events) * 1e-3
-        cb = sum(x for _, _, x in E.copy_events)
-        per_copy = sorted(x / (a.elapsed_time(b) * 1e-3) / 1e9 for a, b, x in E.copy_events)
-        E.timing = False
-        row = dict(nprobe=nprobe, K=K, z=z, recall=rec, qps=round(B / dt, 1), ms_per_batch=round(dt * 1e3, 3),
-                   reads=round(float(reads.float().mean()), 2), fallback=E.nbad,
+        row = dict(staging=staging, nprobe=nprobe, K=K, z=z, recall=rec, qps=round(B / dt, 1),
+                   ms_per_batch=round(dt * 1e3, 3), reads=round(float(reads.float().mean()), 2), fallback=E.nbad,
                    stage1_MB_per_pass=round(pass_bytes / 1e6, 1),
                    first_pass_GBps=round(pass_bytes / (first_ms * 1e-3) / 1e9, 2) if first_ms else None,
-                   first_pass_pcie_frac=round(pass_bytes / (first_ms * 1e-3) / 1e9 / PCIE_PEAK_GBS, 3) if first_ms else None,
-                   stage1_streamed_MB=round(cb / 1e6, 1), copies=len(per_copy),
-                   copy_GBps_event_timed=round(cb / ct / 1e9, 2),
-                   copy_GBps_median=round(per_copy[len(per_copy) // 2], 2), phases_ms=phases)
+                   first_pass_pcie_frac=round(pass_bytes / (first_ms * 1e-3) / 1e9 / PCIE_PEAK_GBS, 3) if first_ms else None)
+        if staging == "copy":
+            # the PCIe rate of the streamed copies: a search whose chunk copies are queued one by one between
+            # timing events (the same copies and scans)
+            E.timing, E.copy_events, E.copied_bytes = True, [], 0
+            E.search(Q, K, z, nprobe, args.k)
+            torch.cuda.synchronize()
+            ct = sum(a.elapsed_time(b) for a, b, _ in E.copy_events) * 1e-3
+            cb = sum(x for _, _, x in E.copy_events)
+            per_copy = sorted(x / (a.elapsed_time(b) * 1e-3) / 1e9 for a, b, x in E.copy_events)
+            E.timing = False
+            row.update(stage1_streamed_MB=round(cb / 1e6, 1), copies=len(per_copy),
+                       copy_GBps_event_timed=round(cb / ct / 1e9, 2),
+                       copy_GBps_median=round(per_copy[len(per_copy) // 2], 2))
+        row["phases_ms"] = phases
         rows.append(row)
         log(f"host {row}")
     out = {"metric": "QPS of the host-resident engine (< 8 B/vector on the GPU), PCIe GB/s of the streamed stage 1",
            "unit": "queries/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
            "config": {"workload": f"host-resident mode, {n}x{d} fp16 synthetic, batch {B}, k={args.k}",
-                      "gpu_bytes_per_vector": round(E.gpu_bytes(), 2), "pcie_peak_GBps": PCIE_PEAK_GBS},
+                      "gpu_bytes_per_vector": {k_: round(e.gpu_bytes(), 2) for k_, e in engines.items()},
+                      "pcie_peak_GBps": PCIE_PEAK_GBS},
            "rows": rows}
     print(json.dumps(out), flush=True)
 

@@ -157,6 +157,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
                                                  int nsplit) {
   __shared__ float stab[1 << kMaxL];
   __shared__ float4 qbuf[4][kTrR / 4];  // per wave: the query vector of the current step
+  __shared__ uint32_t rows_s[4][32 * 10];  // per wave: the words of its item's rows (W <= 10)
   const int tid = threadIdx.x, lane = tid & 63, w = fvs_wave_id();
   const int S = 1 << L;
   for (int i = tid; i < S; i += 256) stab[i] = half ? fvs_round_h(tab[i]) : tab[i];
@@ -174,13 +175,35 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
   const int h = lane >> 5, li = lane & 31;
   const int r = blk * 32 + li;
   const bool valid = r >= cs && r < ce;
-  const int rr = valid ? r : cs;  // decode a valid row for padding lanes (their results are dropped)
+  // The item's rows r_lo .. r_hi - 1 are one contiguous run of words: the wave reads it with consecutive
+  // lanes on consecutive dwords (every byte fetched once, which matters when the words are read
+  // zero-copy from pinned host memory over PCIe) and stages it in LDS for the per-row decode.
+  const int r_lo = max(blk * 32, cs), r_hi = min(blk * 32 + 32, ce);
+  const int rr = valid ? r : r_lo;  // padding lanes decode a staged row (their results are dropped)
+  {
+    const int nw = max(r_hi - r_lo, 0) * W;  // <= 32 * 10
+    const uint32_t *src = words + ((int64_t)r_lo - row0) * W;
+    uint32_t tmp[5];
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+      const int i = lane + 64 * k;
+      tmp[k] = i < nw ? src[i] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+      const int i = lane + 64 * k;
+      if (i < nw) rows_s[w][i] = tmp[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
   // coordinates [128 h, 128 h + 128) need words 4h .. 4h + 4 of the stream
   uint32_t ww[5];
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     const int i = 4 * h + k;
-    ww[k] = i < W ? words[((int64_t)rr - row0) * W + i] : 0u;
+    ww[k] = i < W ? rows_s[w][(rr - r_lo) * W + i] : 0u;
   }
   float v[128];
   const uint32_t mask = (uint32_t)S - 1u;
@@ -189,7 +212,7 @@ __global__ __launch_bounds__(256) void k_tr_scan(const float *__restrict__ Qr, c
     const uint64_t comb = ((uint64_t)ww[i >> 5] << 32) | (uint64_t)ww[(i >> 5) + 1];
     v[i] = stab[(uint32_t)(comb >> (64 - L - (i & 31))) & mask];
   }
-  const float s1 = fvs_h2f(scale1[(int64_t)rr - row0]);
+  const float s1 = valid ? fvs_h2f(scale1[(int64_t)rr - row0]) : 0.f;
   // The query vectors (kTrR floats = one float4 per lane) are read one step ahead and staged in LDS, so
   // a step waits for one LDS round trip instead of a chain of global ones.
   const float4 *Qr4 = reinterpret_cast<const float4 *>(Qr);

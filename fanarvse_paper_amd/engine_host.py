@@ -4,20 +4,26 @@ Every per-vector array lives in pinned host memory: the trellis words and scales
 records, and the fp16 rows (kept in sorted order, so no id table is needed on the GPU; ids are mapped
 on the host, as the reference's ids_host variant does). The GPU keeps only shared tables: the cell
 means for routing and the pair constants, W1, the stage-2 rotation VP, the trellis table, the cell
-offsets and the static work list, plus two staging slots for stage-1 chunks. The reference's two
+offsets and the static work list (plus two stage-1 staging slots with copy staging). The reference's two
 switches are kept (space_x.py:19-36):
   proj: the means projected on the stage-1 basis, meansR = fp16((m_c - c) @ W1) [NC, R], with
         QM = fp16(Qr) @ meansR.T and the pair term and routing key adding <q, c>. It is exact only when
         the cell means lie in the span of W1 (true of the reference's embeddings, not of isotropic
         cluster centres), so it is off by default;
   vp16: W1 and VP in fp16, with Qr = f32(fp16(Qb) @ W1h) and Zq = f32(fp16(Qb) @ VP16).
-The default (proj off, vp16 on, 16,384-row chunks) stays under 8 B per vector at 1.28M vectors.
+The default (proj off, vp16 on, zero-copy stage 1) stays under 8 B per vector at 1.28M vectors, and so
+does copy staging with its 16,384-row chunks.
 
-Stage 1 streams: the index is cut into cell-aligned chunks of about CHUNK rows, each stored in pinned
-memory as one contiguous block (its rows' trellis words, then their scales, padded to 16 bytes); a side
-stream copies chunk i+1's block into the free staging slot with one hipMemcpyAsync while the main stream
-scans chunk i (fvs_tr_scan with row0 = the chunk's first row). Stage 2 and stage 3 read their records and
-rows zero-copy from pinned memory. Results equal EngineS's with the projected-means routing.
+Stage 1 has two stagings of its trellis words and scales (the same results either way):
+  "zero-copy" (the default, and the reference's placement: space_x.py:23 hands the pinned arrays to the
+        scan): one fvs_tr_scan launch per pass over the whole work list reads the words and scales from
+        pinned memory over PCIe, each item's rows once, with consecutive lanes on consecutive dwords;
+  "copy": the index is cut into cell-aligned chunks of about CHUNK rows, each stored in pinned memory as
+        one contiguous block (its rows' trellis words, then their scales, padded to 16 bytes); a side
+        stream copies chunk i+1's block into the free one of two staging slots with one hipMemcpyAsync
+        while the main stream scans chunk i (fvs_tr_scan_streamed).
+Stage 2 and stage 3 read their records and rows zero-copy from pinned memory. Results equal EngineS's
+with the projected-means routing.
 """
 import numpy as np
 import torch
@@ -35,7 +41,10 @@ def _pin(t):
 class SpaceX(EngineS):
     CHUNK = 16384  # rows per staged stage-1 chunk
 
-    def __init__(self, s1, code, H16, proj=False, vp16=True):
+    def __init__(self, s1, code, H16, proj=False, vp16=True, staging="zero-copy"):
+        if staging not in ("zero-copy", "copy"):
+            raise ValueError("SpaceX: staging is 'zero-copy' or 'copy'")
+        self.staging = staging
         s2lut.prepare_u(code)
         if "VP" not in code:
             raise ValueError("SpaceX needs a Lloyd-Max tiered code (s2lut.encode_lloyd)")
@@ -59,11 +68,15 @@ class SpaceX(EngineS):
         self.H = self.Hs
         self.graphs = {}
         self.nbad = 0
-        self._chunks()
-        self._stage_host(s1["words"], s1["scale1"])
-        self.side = torch.cuda.Stream()
-        self.slots = [torch.empty((self._block_bytes(self.chunk_rows),), dtype=torch.uint8, device=dev)
-                      for _ in range(2)]
+        if staging == "copy":
+            self._chunks()
+            self._stage_host(s1["words"], s1["scale1"])
+            self.side = torch.cuda.Stream()
+            self.slots = [torch.empty((self._block_bytes(self.chunk_rows),), dtype=torch.uint8, device=dev)
+                          for _ in range(2)]
+        else:
+            self.chunks, self.slots = [], []
+            self.words_h, self.scale1_h = _pin(s1["words"]), _pin(s1["scale1"])
         self.copied_bytes = 0
         self.copy_events = []
         self.phase_events = None  # when a list, _run records (name, event) at each stage boundary
@@ -129,9 +142,15 @@ class SpaceX(EngineS):
         return int(max(1, min(8, fill, qpc // 16)))
 
     def _scan_streamed(self, mode, Qr, pr, **kw):
-        """One stage-1 pass over every chunk, copies on the side stream overlapped with the scans: one library
-        call (fvs_tr_scan_streamed) queues every chunk's copy and scan; with `timing` set, the same steps are
+        """One stage-1 pass. Zero-copy staging: one scan over the whole work list reading pinned memory.
+        Copy staging: every chunk copied on the side stream, overlapped with the scans; one library call
+        (fvs_tr_scan_streamed) queues every chunk's copy and scan; with `timing` set, the same steps are
         queued from here with every copy bracketed by timing events."""
+        if self.staging == "zero-copy":
+            _lib.tr_scan(mode, self.blocks, Qr, pr, self.words_h, self.scale1_h, self.s1["tab"], self.s1["L"],
+                         half=True, **kw)
+            self.copied_bytes += self.N * (4 * self.Wd + 2)
+            return
         nsplit = self._nsplit(max(i1 - i0 for _, _, i0, i1 in self.chunks), Qr.shape[0], pr[2].numel())
         if not self.timing:
             _lib.tr_scan_streamed(mode, self.chunk_tab, self.stage_h, self.slots, self.side, self.blocks, Qr, pr,
@@ -236,16 +255,21 @@ class SpaceX(EngineS):
         self._mark("refine (rows zero-copy)")
         return ok, I, reads, ids, scores, (Qr, QC, QM, Zq)
 
+    FALLBACK_M = 1 << 20  # emit buffer of the flagged queries' second pass (host_resident/space_x.py:65)
+
     def search(self, Qb, K, z, nprobe, k, ret_scores=False, sorted_ids=False):
         """(I, reads, cand_ids) (+ scores): ids mapped to the original ids on the host (numpy -> torch CPU
-        tensors), as SpaceX.run does (host_resident/space_x.py:71-78); sorted_ids keeps sorted positions."""
+        tensors), as SpaceX.run does (host_resident/space_x.py:71-78); sorted_ids keeps sorted positions.
+        Flagged queries run the same pass again with a 1 << 20-entry buffer (space_x.py:58-70), which holds
+        every row above the threshold of a query whose count overflowed the main buffer: its top K no longer
+        depends on the order the rows were emitted in."""
         Qb = Qb.float().contiguous()
         ok, I, nr, ids, sc, dense = self._run(Qb, K, z, nprobe, k)
         if not bool(ok.all()):
             bad = torch.nonzero(~ok).flatten()
             self.nbad += len(bad)
             sub = tuple(t[bad].contiguous() for t in dense)
-            _, a, b, c, s, _ = self._run(Qb[bad], K, z, nprobe, k, rho_override=1.0, M_override=65536, dense=sub)
+            _, a, b, c, s, _ = self._run(Qb[bad], K, z, nprobe, k, M_override=self.FALLBACK_M, dense=sub)
             I, nr, ids, sc = I.clone(), nr.clone(), ids.clone(), sc.clone()
             I[bad], nr[bad], ids[bad], sc[bad] = a, b, c, s
         if not sorted_ids:

@@ -578,12 +578,14 @@ def tr_stage1(idx, Qr, QM16, probe, K, M=None, rho_override=None, M_override=Non
 
 
 def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, proj=False, order=True, half=None,
-                fb_half=True):
+                fb_half=True, fb_rho=1.0, fb_M=65536):
     """The default engine's batch (EngineS._gpu + the fallback): Qr = Q @ W1 (f32), QM16 = fp16(Q) @ means16.T
     (fp16), Zq = Q @ VP (f32) are the shared dense products. proj: QM16 = fp16(Qr) @ meansR.T and the pair term
     and routing key add <q, c> (host_resident/space_x.py:33-39). order=False: ids are sorted positions.
     half: fp16 stage-1 operands (None: the reference's choice by batch size, fp16 above 8 queries,
-    src/engine_cell.py:48-53,82-83); fb_half: the same for the fallback pass."""
+    src/engine_cell.py:48-53,82-83); fb_half: the same for the fallback pass. fb_rho / fb_M: the fallback's
+    rho and buffer, (1.0, 65536) for EngineS; the host-resident engine reruns its flagged queries with the
+    main pass's rho and a 1 << 20 buffer (fb_rho=None, fb_M=1 << 20: host_resident/space_x.py:63-70)."""
     Q = _c(Q, np.float32)
     _, _, qc, _ = query_prep(Q, None, idx["c"], Qr)
     qadd = qc if proj else None
@@ -600,8 +602,8 @@ def tr_pipeline(idx, Q, K, z, nprobe, k, Qr, QM16, Zq, M=None, fallback=True, pr
     bad = np.nonzero(s1["ok"] == 0)[0]
     out["bad"] = bad
     if fallback and len(bad):
-        f1 = tr_stage1(idx, np.asarray(Qr)[bad], np.asarray(QM16)[bad], probe[bad], K, M, rho_override=1.0,
-                       M_override=65536, qadd=None if qadd is None else qadd[bad], half=fb_half)
+        f1 = tr_stage1(idx, np.asarray(Qr)[bad], np.asarray(QM16)[bad], probe[bad], K, M, rho_override=fb_rho,
+                       M_override=fb_M, qadd=None if qadd is None else qadd[bad], half=fb_half)
         estf, sdf = tiered_score(f1["pos"], qc[bad], np.asarray(Zq)[bad], idx["rec"], idx["soff"], idx["TS"],
                                  idx["toff"], idx["cb"])
         idsf, If, scf, rf_ = refine(estf, sdf, f1["pos"], ordr, H, Q[bad], z, k)

@@ -267,18 +267,27 @@ def test_config5_host_resident_1_28Mx768(oracle_mod):
     idx = oracle_mod.trellis_index_from_tables(s1, code, X)
     idx["Hs"] = npy(X[s1["order"].long()]).view(np.uint16)
     E = SpaceX(s1, code, X)
+    Ec = SpaceX(s1, code, X, staging="copy")
     del s1, code
     free()
     K, z, nprobe, k = 200, 2.0, 256, 10
     I, reads, ids = E.search(Q, K, z, nprobe, k, sorted_ids=True)
     tr = E.trace(Q, K, z, nprobe, k)
     torch.cuda.synchronize()
+    # the two stagings of stage 1 (zero-copy reads, chunk copies) give the same results on every query
+    Ic, rc, ic = Ec.search(Q, K, z, nprobe, k, sorted_ids=True)
+    trc = Ec.trace(Q, K, z, nprobe, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(npy(Ic), npy(I)) and np.array_equal(npy(rc), npy(reads)) and np.array_equal(npy(ic), npy(ids))
+    assert np.array_equal(npy(trc["t0"]).view(np.uint32), npy(tr["t0"]).view(np.uint32))
+    assert np.array_equal(npy(trc["cnt"]), npy(tr["cnt"]))
+    del Ec, Ic, rc, ic, trc
     rec = metrics.recall(E.order_np[npy(I)], GT, k)
     say(f"config 5: recall@10 {rec:.4f}, {E.nbad} flagged; oracle checks")
     Qr, QC, QM, Zq = (npy(tr[n]) for n in ("Qr", "QC", "QM", "Zq"))
     sample = np.linspace(0, 1999, 32).astype(np.int64)
     out = oracle_mod.tr_pipeline(idx, npy(Q)[sample], K, z, nprobe, k, Qr=Qr[sample], QM16=QM.view(np.uint16)[sample],
-                                 Zq=Zq[sample], proj=E.proj, order=False, half=True)
+                                 Zq=Zq[sample], proj=E.proj, order=False, half=True, fb_rho=None, fb_M=E.FALLBACK_M)
     assert np.array_equal(npy(I)[sample], out["I"])
     assert np.array_equal(npy(reads)[sample], out["reads"])
     assert np.array_equal(npy(ids)[sample], out["cand"])
