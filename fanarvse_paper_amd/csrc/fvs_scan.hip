@@ -1,28 +1,26 @@
-// int8 stage-1 scans on gfx950 MFMA (v_mfma_i32_32x32x32_i8): the first pass (block maxima) and the
-// threshold-and-emit pass.
+// int8 stage-1 scans on gfx950 MFMA: the first pass (block maxima, v_mfma_i32_32x32x32_i8) and the
+// threshold-and-emit pass (v_mfma_i32_16x16x64_i8).
 //
 // Work item = (cell, up to 256 consecutive rows of it from a first row r0); its 32-row blocks start at
 // r0, r0 + 32, ... The first pass needs the reference's global 32-row blocks (its block maxima are per
 // global block), so its items start on a multiple of 32; the emit pass, whose output does not depend on
 // the grouping, takes items that start at the cell's first row (a cell of up to 256 rows is one item,
-// with no block straddling the cell start). A 4-wave workgroup runs an item; wave w keeps blocks 2w and
-// 2w+1 (64 code rows) as MFMA operands in registers for the whole item, so each code byte is read from
-// HBM once per pass. The cell's queries stream through in tiles of 32:
+// with no block straddling the cell start). Each code byte is read from HBM once per pass: a wave keeps
+// its 64 code rows as MFMA operands in registers for the whole item (first pass) or half item (emit),
+// and the cell's queries stream through in tiles:
 //   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the row
-//     scales of its 256 rows are staged in LDS up front (kMeta pairs at a time);
-//   * a tile's fragments (its 32 query codes, 8 KB) are written straight into LDS by the vector memory
-//     unit (global_load_lds, no registers), in MFMA-step order so that every fragment read is one
-//     contiguous 1 KB ds_read_b128 per wave. The buffer is double-buffered and shared by the four waves:
-//     each wave requests a quarter of tile t + 1 while tile t is computed, and one barrier per tile
-//     publishes it.
-// Two blocks per wave halve the fragment reads per MFMA. Both passes are persistent: a workgroup loops
-// over items (grid = resident workgroups), and the next item's pair ids, row scales and code blocks are
-// requested as soon as the current item's tile loop is done.
+//     scales of its rows are staged in LDS up front (kMeta / kMetaE pairs at a time);
+//   * a tile's query fragments are written straight into LDS by the vector memory unit (global_load_lds,
+//     no registers), in MFMA-step order so that every fragment read is one contiguous 1 KB ds_read_b128 per
+//     wave. The buffer is double-buffered and shared by the workgroup's waves: each wave requests its share
+//     of tile t + 1 while tile t is computed, and one barrier per tile publishes it.
+// Both passes are persistent: a workgroup loops over items (grid = resident workgroups), and the next
+// item's pair ids, row scales and code rows are requested as soon as the current item's tile loop is done.
 //
-// Operand layout: lane l holds row/column (l & 31) and, for MFMA step s (k-block of 32 bytes), the
-// 16 bytes at 32*s + 16*(l >> 5); both operands use the same assignment, so the contraction is exact for
-// any internal k order. Accumulator layout (32x32, D = A x B): lane l, element v holds row
-// 8*(v/4) + 4*(l/32) + (v%4) of A and column l%32 of B.
+// The first pass's operand layout (32 x 32 x 32): lane l holds row/column (l & 31) and, for MFMA step s
+// (k-block of 32 bytes), the 16 bytes at 32*s + 16*(l >> 5); both operands use the same assignment, so
+// the contraction is exact for any internal k order. Accumulator layout (D = A x B): lane l, element v
+// holds row 8*(v/4) + 4*(l/32) + (v%4) of A and column l%32 of B.
 //
 // The item's row scales sit in LDS; rows outside the cell get a NaN scale: their estimate is NaN,
 // which never passes `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
@@ -35,9 +33,7 @@ namespace {
 constexpr int kR = 256;
 constexpr int kNB = 2;          // 32-row blocks per wave
 constexpr int kCB = 4 * kNB;    // 32-row blocks per work item
-constexpr int kMeta = 512;      // pairs staged in LDS at a time
-constexpr int kEmitWaves = 4;   // waves per emit workgroup
-constexpr int kCapE = 640;      // LDS candidate slots per wave of the emit pass
+constexpr int kMeta = 512;      // pairs staged in LDS at a time (first pass)
 
 // row of accumulator element v in the 32x32 layout, for lanes of half h = l / 32
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
@@ -50,6 +46,8 @@ struct Meta {  // one (query, cell) pair of the item
 };
 
 // ------------------------------------------------------------------ the first pass (mode 0)
+// A 4-wave workgroup runs an item: wave w keeps blocks 2w and 2w + 1 (two blocks per wave halve the
+// fragment reads per MFMA), and the queries come in tiles of 32 (8 KB), each wave requesting a quarter.
 // The code rows are the A operand and the queries the B operand, so each lane owns one query (column
 // l % 32) and 16 rows of a block; the epilogue needs only per-lane scalars for the query:
 //   bm[(q * n1 + qrank[pair]) * MB + blk - cs/32] = max over the block's rows of
@@ -216,11 +214,22 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 }
 
 // ------------------------------------------------------------------ the emit pass (mode 1)
-// Same items, waves and LDS query tiles as the first pass, with the MFMA operands swapped: the tile's 32
-// queries are the A operand and the wave's code rows the B operand, so lane l holds code row l % 32 of the
-// block and element v the query 8*(v/4) + 4*(l/32) + (v%4) of the tile. A wave ballot of one element then
-// covers two (query, 32-row block) pairs, and since the rows that pass for a query come in clusters, most
-// ballots are empty (about 9 %, against 44 % with one query per lane).
+// The emit pass runs on smaller items than the first pass: a workgroup of two waves takes a cell and up to 128
+// of its rows (64 per wave, as four 16-row blocks), and the cell's queries in tiles of 16, on
+// v_mfma_i32_16x16x64_i8. Cells are skewed (a tenth hold under 16 rows), so 128-row items leave few waves
+// without rows (about 4 % of the wave-steps, against 28 % for four-wave items of 256 rows), and 16-row
+// blocks leave few empty rows in the blocks that are computed. The persistent grid walks the items in list
+// order with a stride of the grid size; the engine's list (index.row_chunks(off, 128)) has about 6.5 items
+// per workgroup at 1M rows, so the busiest workgroup runs 7.
+//
+// MFMA layout (16 x 16 x 64, int8): for step s (64 bytes of the code), lane l holds 16 bytes 64 s + 16 (l >> 4)
+// .. + 15 of A row l & 15 (a query of the tile) and of B column l & 15 (a code row of the block); both use
+// the same assignment, so the contraction is exact for any internal order. Accumulator element i of lane l is
+// D[4 (l >> 4) + i][l & 15]: query 4 (l >> 4) + i of the tile against row l & 15 of the block. A wave ballot
+// of one element covers 16 rows of four queries; passing rows cluster by query, so most ballots are empty.
+// The tile's fragments (16 queries, 4 KB) go straight into LDS by the vector memory unit (global_load_lds),
+// in MFMA-step order [s][lane], double-buffered; each wave requests two of the four steps of tile t + 1
+// while tile t is computed, one barrier per tile.
 //
 // Per element the tile loop evaluates a conservative prefilter instead of the canonical estimate:
 //   g = fmaf((float)acc, z, 2z) >= T[q],  T[q] = (t0 - qcp)/qs - 2^-20 (|t0| + |qcp|)/qs  (f32 ops).
@@ -230,8 +239,9 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 // rounding of T's three operations is far below its 2^-20 margin; so every element whose estimate passes
 // also passes the prefilter. (A query with qs <= 0 or an overflowing T gets T = -inf, a row scale that is
 // negative or infinite the addend +inf: the prefilter then admits every query of the chunk, and the exact
-// test decides; the missing queries of a last partial tile have a NaN threshold, which nothing passes.) Per element that is a convert, an fma and a compare; the tests of four elements of both
-// blocks are made before one branch on the OR of their eight ballots skips the group.
+// test decides; the missing queries of a last partial tile have a NaN threshold, which nothing passes.) Per
+// element that is a convert, an fma and a compare; the tests of two blocks (eight elements) are made before
+// one branch on the OR of their ballots skips the group.
 //
 // The passing elements are staged as (accumulator, tag) in the wave's LDS region. The flush computes the
 // canonical estimate of each, fmaf((float)acc * qs, zs, qcp), drops those below t0 (the few the
@@ -239,18 +249,24 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 // with one global atomic per (item, query) and writes them out. So the emitted set and its estimates are
 // exactly those of the canonical formula; their order in a query's buffer is unspecified.
 //
-// Three workgroups per CU (at most 168 VGPRs, 50 KB of LDS with 640 staging slots per wave): the third
-// resident workgroup hides more of each item's fixed latencies (pair staging, first tile, flush) than
-// overlapping the next tile's MFMAs with the current epilogue inside one wave did at two per CU.
-// The item's pairs are processed in chunks of up to kMeta queries; a chunk whose candidates overflow a
-// wave's region is dropped and scanned again with half as many queries, down to 8 queries, whose
-// 8 x 64 = 512 candidates per wave always fit in its 640 slots.
-template <int NW>
+// Six workgroups (twelve waves) per CU: at most 168 VGPRs and 23 KB of LDS each. An item's pairs are
+// processed in chunks of up to kMetaE queries; a chunk whose candidates overflow a wave's region is dropped
+// and scanned again with half as many queries, down to 8 queries, whose 8 x 64 = 512 candidates per wave
+// always fit in its kCapE = 512 slots.
+constexpr int kEW = 2;         // waves per emit workgroup
+constexpr int kET = 64 * kEW;  // threads per emit workgroup
+constexpr int kERows = 64 * kEW;  // rows of an emit item
+constexpr int kTQ = 16;        // queries per tile
+constexpr int kMetaE = 256;    // pairs staged in LDS at a time
+constexpr int kCapE = 512;     // LDS candidate slots per wave
+constexpr int kEmitWG = 6;     // resident emit workgroups per CU
+static_assert(8 * 64 <= kCapE, "an 8-query chunk must fit a wave's region");
+
 struct EmitStage {
-  int acc[NW][kCapE];       // dot products of the staged elements; the estimate after the exact test
-  uint32_t tag[NW][kCapE];  // row - first row of the item (bits 0-7) | pair index (8-19) | number (20-31)
-  uint32_t lcnt[kMeta];     // candidates of each pair in the item; then the pair's base in its query's buffer
-  int n[NW];
+  int acc[kEW][kCapE];       // dot products of the staged elements; the estimate after the exact test
+  uint32_t tag[kEW][kCapE];  // row - first row of the item (bits 0-7) | pair index (8-19) | number (20-31)
+  uint32_t lcnt[kMetaE];     // candidates of each pair in the item; then the pair's base in its query's buffer
+  int n[kEW];
 };
 
 __device__ __forceinline__ float emit_prefilter_T(float th, float qc, float qsv) {
@@ -262,71 +278,64 @@ __device__ __forceinline__ float emit_prefilter_T(float th, float qc, float qsv)
   return T;
 }
 
-template <int NW>
-__global__ __launch_bounds__(256, 3) void k_i8_emit(
+__global__ __launch_bounds__(kET, 3) void k_i8_emit(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt, const int32_t *__restrict__ pcell,
     const int32_t *__restrict__ prow, const int32_t *__restrict__ ps, const int32_t *__restrict__ pe, int P,
-    const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N, const float *__restrict__ qcp,
+    const int8_t *__restrict__ Z, const float *__restrict__ zs, const float *__restrict__ qcp,
     const float *__restrict__ t0, int32_t *__restrict__ cnt, float *__restrict__ bval, int32_t *__restrict__ bpos,
     int CAP) {
-  constexpr int NT = 64 * NW;     // threads of the workgroup
-  constexpr int kSt = 8 / NW;     // MFMA steps of a query tile each wave requests
-  static_assert(kNB == 2, "the epilogue pairs the ballots of two blocks");
-  static_assert(8 * 64 <= kCapE, "an 8-query chunk must fit a wave's region");
-  static_assert(NW == 4, "an item's 256 rows are one pass of four waves");
-  __shared__ __align__(16) Meta meta[kMeta];
-  __shared__ __align__(16) float Tl[kMeta + 32];
-  __shared__ __align__(16) float zsl[256];
-  __shared__ __align__(16) v4i bsh0[8 * 64];  // query tiles of even index: [step s][half h][query li], 16 B each
-  __shared__ __align__(16) v4i bsh1[8 * 64];  // query tiles of odd index
-  __shared__ EmitStage<NW> S;
+  __shared__ __align__(16) Meta meta[kMetaE];
+  __shared__ __align__(16) float Tl[kMetaE + kTQ];
+  __shared__ __align__(16) float zsl[kERows];
+  __shared__ __align__(16) v4i bsh0[4 * 64];  // query tiles of even index: [step s][lane], 16 B each
+  __shared__ __align__(16) v4i bsh1[4 * 64];  // query tiles of odd index
+  __shared__ EmitStage S;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = fvs_wave_id();
-  const int h = lane >> 5, li = lane & 31;
+  const int g4 = lane >> 4, l16 = lane & 15;
+  // item p: rows [lo, ce) with lo = max(prow, ps) and ce = min(prow + 128, pe), in 16-row blocks from prow;
+  // qn = 0 marks an item without rows or queries
   struct Item {
-    int c, qn, qoff, r0, cs, ce;
+    int qn, qoff, r0, lo, ce;
   };
   auto item_at = [&](int p) {
-    Item it{0, 0, 0, 0, 0, 0};
+    Item u{0, 0, 0, 0, 0};
     if (p < P) {
-      it.c = pcell[p];
-      it.r0 = prow[p];
-      it.cs = ps[p];
-      it.ce = pe[p];
-      it.qn = ccnt[it.c];
-      it.qoff = coff[it.c];
+      const int c = pcell[p];
+      u.r0 = prow[p];
+      u.lo = max(u.r0, ps[p]);
+      u.ce = min(u.r0 + kERows, pe[p]);
+      if (u.lo < u.ce) {
+        u.qn = ccnt[c];
+        u.qoff = coff[c];
+      }
     }
-    return it;
+    return u;
   };
-  int pq[kMeta / NT];  // pair ids of the item's first chunk
-  float zr[256 / NT];  // row scales of the item's rows r0 + tid + NT i (NaN outside the cell)
-  v4i cb[kNB][8];      // this wave's code blocks: the B operands
-  auto load_cb = [&](int r0p, int ce) {
+  int pq[kMetaE / kET];  // pair ids of the item's first chunk
+  float zr;              // this thread's row scale of the item (NaN outside the cell)
+  v4i cb[4][4];          // this wave's code rows: block b (16 rows), MFMA step s (64 bytes)
+  auto prefetch = [&](const Item &u) {
+    if (u.qn == 0) return;
 #pragma unroll
-    for (int u = 0; u < kNB; u++) {
-      const int b0 = r0p + 32 * (kNB * w + u);
-      int64_t zr_ = (int64_t)b0 + li;
-      if (b0 >= ce || zr_ > N - 1) zr_ = N - 1;  // rows past the cell carry a NaN scale
-      const v4i *zp = reinterpret_cast<const v4i *>(Z + zr_ * kR + h * 16);
-#pragma unroll
-      for (int s = 0; s < 8; s++) cb[u][s] = zp[2 * s];
+    for (int i = 0; i < kMetaE / kET; i++) {
+      const int j = tid + kET * i;
+      pq[i] = j < min(kMetaE, u.qn) ? qid[u.qoff + j] : 0;
     }
-  };
-  auto prefetch = [&](const Item &it) {
-    if (it.qn == 0) return;
-#pragma unroll
-    for (int i = 0; i < kMeta / NT; i++) {
-      const int j = tid + NT * i;
-      pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
+    {
+      const int r = u.r0 + tid;
+      zr = (r >= u.lo && r < u.ce) ? zs[r] : __builtin_nanf("");
     }
 #pragma unroll
-    for (int i = 0; i < 256 / NT; i++) {
-      const int r = it.r0 + tid + NT * i;
-      zr[i] = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
+    for (int b = 0; b < 4; b++) {
+      const int r = u.r0 + 64 * w + 16 * b + l16;
+      const int64_t rr = r < u.ce ? r : u.ce - 1;  // rows past the cell carry a NaN scale
+      const v4i *zp = reinterpret_cast<const v4i *>(Z + rr * kR + 16 * g4);
+#pragma unroll
+      for (int s = 0; s < 4; s++) cb[b][s] = zp[4 * s];
     }
-    load_cb(it.r0, it.ce);
   };
 
   const int stride = (int)gridDim.x;
@@ -343,22 +352,23 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
     }
     const int qn = cur.qn, qoff = cur.qoff;
     const int row0 = cur.r0;
-#pragma unroll
-    for (int i = 0; i < 256 / NT; i++) zsl[tid + NT * i] = zr[i];
+    zsl[tid] = zr;
     int ebase = 0;  // wave-uniform: used slots of this wave's region (may exceed kCapE: overflow)
     int nq = 0;     // queries of the current pair chunk
+    const int wrows = cur.ce - row0 - 64 * w;  // rows of this wave's 64 (<= 0: none)
+    const int nact = wrows <= 0 ? 0 : min(4, (wrows + 15) >> 4);  // blocks with rows of the cell
 
     // the tile loop over the current chunk's nq pairs (staged in meta / Tl)
     auto scan = [&]() {
-      const int ntiles = (nq + 31) / 32;
+      const int ntiles = (nq + kTQ - 1) / kTQ;
       // tile t's fragments go to bsh0 (t even) or bsh1 (t odd): global_load_lds, 16 B per lane; wave w
-      // requests kSt of the 8 steps
+      // requests steps 2w and 2w + 1
       auto request = [&](int tile, v4i *buf) {
-        const int8_t *src = q8 + (int64_t)meta[min(tile * 32 + li, nq - 1)].qid * kR + h * 16;
+        const int8_t *src = q8 + (int64_t)meta[min(tile * kTQ + l16, nq - 1)].qid * kR + 16 * g4;
 #pragma unroll
-        for (int k = 0; k < kSt; k++) {
-          const int s = kSt * w + k;
-          __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&buf[s * 64], 16,
+        for (int i = 0; i < 4 / kEW; i++) {
+          const int s = (4 / kEW) * w + i;
+          __builtin_amdgcn_global_load_lds(src + 64 * s, (__attribute__((address_space(3))) void *)&buf[s * 64], 16,
                                            0, 0);
         }
       };
@@ -366,87 +376,84 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       };
-      auto load_qa = [&](v4i (&qa)[8], const v4i *buf) {
+      // this lane's row scale per block and the prefilter's addend; rows outside the cell have a NaN scale
+      // and never pass
+      float zl[4], nd[4];
 #pragma unroll
-        for (int s = 0; s < 8; s++) qa[s] = buf[s * 64 + lane];
-      };
-      {
-        constexpr int rp = 0;  // the item's rows are one pass: 4 waves x 2 blocks x 32 rows = 256
-        const bool any = row0 + 32 * kNB * w < cur.ce;  // the wave has rows of the cell
-        // this lane's row scale per block and the prefilter's addend; rows outside the cell have a NaN
-        // scale and never pass
-        float zl[kNB], nd[kNB];
+      for (int b = 0; b < 4; b++) {
+        const float z = zsl[64 * w + 16 * b + l16];
+        const bool fin = z >= 0.f && z < __builtin_inff();
+        zl[b] = fin || z != z ? z : 0.f;
+        nd[b] = fin || z != z ? z + z : __builtin_inff();
+      }
+      // tile loop of a wave with NB blocks of rows: step t requests tile t + 1 into the other buffer (every
+      // wave has passed the barrier that ended tile t - 1), computes tile t and waits for tile t + 1
+      auto tiles = [&](auto NB_) {
+        constexpr int NB = decltype(NB_)::value;
+        v4i qa[4];
+        for (int t = 0; t < ntiles; t++) {
+          const v4i *cur_t = (t & 1) ? bsh1 : bsh0;
+          if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
 #pragma unroll
-        for (int u = 0; u < kNB; u++) {
-          const float z = zsl[32 * (kNB * w + u) + li];
-          const bool fin = z >= 0.f && z < __builtin_inff();
-          zl[u] = fin || z != z ? z : 0.f;
-          nd[u] = fin || z != z ? z + z : __builtin_inff();
-        }
-        // the epilogue of tile t over its accumulators A
-        auto epilogue = [&](const v16i (&A)[kNB], int t) {
-          const uint32_t tagt = (uint32_t)(32 * t + 4 * h) << 8;
-          // Four elements of both blocks at a time: their eight tests are independent, so they issue back to
-          // back, and one branch on the OR of the eight ballots skips the group (a branch per element would
-          // make every test wait for the previous one's scalar round trip).
+          for (int s = 0; s < 4; s++) qa[s] = cur_t[s * 64 + lane];
+          v4i A[NB];
 #pragma unroll
-          for (int g = 0; g < 4; g++) {
-            bool pass_[4][kNB];
-            uint64_t bal[4][kNB];
+          for (int s = 0; s < 4; s++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const int v = 4 * g + i;
+            for (int b = 0; b < NB; b++)
+              A[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[s], cb[b][s], s == 0 ? (v4i){0, 0, 0, 0} : A[b], 0, 0, 0);
+          const float4 T4 = *reinterpret_cast<const float4 *>(&Tl[kTQ * t + 4 * g4]);
+          const float Tv[4] = {T4.x, T4.y, T4.z, T4.w};
+          const uint32_t tagt = (uint32_t)(kTQ * t + 4 * g4) << 8;
+          // two blocks (eight tests) at a time: their tests issue back to back, and one branch on the OR of
+          // the eight ballots skips the group
 #pragma unroll
-              for (int u = 0; u < kNB; u++) {
-                pass_[i][u] = __builtin_fmaf((float)A[u][v], zl[u], nd[u]) >= Tl[32 * t + 8 * g + 4 * h + i];
-                bal[i][u] = __ballot(pass_[i][u]);
-              }
-            }
-            if ((bal[0][0] | bal[0][1]) | (bal[1][0] | bal[1][1]) | (bal[2][0] | bal[2][1]) | (bal[3][0] | bal[3][1])) {
+          for (int b0 = 0; b0 < NB; b0 += 2) {
+            bool pass_[2][4];
+            uint64_t bal[2][4];
+            uint64_t anyb = 0;
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++)
 #pragma unroll
               for (int i = 0; i < 4; i++) {
+                const int b = b0 + bb < NB ? b0 + bb : b0;
+                pass_[bb][i] = b0 + bb < NB && __builtin_fmaf((float)A[b][i], zl[b], nd[b]) >= Tv[i];
+                bal[bb][i] = __ballot(pass_[bb][i]);
+                anyb |= bal[bb][i];
+              }
+            if (anyb) {
 #pragma unroll
-                for (int u = 0; u < kNB; u++) {
-                  if (bal[i][u]) {
-                    const int ro = rp + 32 * (kNB * w + u) + li;  // the lane's row, relative to the item's first row
-                    const int pop = __popcll(bal[i][u]);
-                    if (ebase + pop <= kCapE && pass_[i][u]) {
-                      const int pre = fvs_lane_prefix(bal[i][u]);
-                      (S.acc[w] + ebase)[pre] = A[u][4 * g + i];
-                      (S.tag[w] + ebase)[pre] = ((uint32_t)ro | tagt) + ((uint32_t)(8 * g + i) << 8);
+              for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                  const int b = b0 + bb < NB ? b0 + bb : b0;
+                  if (bal[bb][i]) {
+                    const int pop = __popcll(bal[bb][i]);
+                    if (ebase + pop <= kCapE && pass_[bb][i]) {
+                      const int pre = fvs_lane_prefix(bal[bb][i]);
+                      (S.acc[w] + ebase)[pre] = A[b][i];
+                      (S.tag[w] + ebase)[pre] = ((uint32_t)(64 * w + 16 * b + l16) | tagt) + ((uint32_t)i << 8);
                     }
                     ebase += pop;
                   }
                 }
-              }
             }
           }
-        };
-        // tile loop: step t requests tile t + 1 into the other buffer (every wave has passed the barrier
-        // that ended tile t - 1), computes tile t and waits for tile t + 1
-        request(0, bsh0);
-        published();
-        if (any) {
-          v16i acc[kNB];
-          v4i qa[8];
-          for (int t = 0; t < ntiles; t++) {
-            const v4i *cur_t = (t & 1) ? bsh1 : bsh0;
-            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
-            load_qa(qa, cur_t);
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-              for (int u = 0; u < kNB; u++)
-                acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], cb[u][s], s == 0 ? (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0} : acc[u], 0, 0, 0);
-            epilogue(acc, t);
-            published();
-          }
-        } else {  // a wave without rows of the cell: the same barriers and requests, no compute
-          for (int t = 0; t < ntiles; t++) {
-            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
-            published();
-          }
+          published();
         }
+      };
+      request(0, bsh0);
+      published();
+      switch (nact) {
+        case 4: tiles(std::integral_constant<int, 4>{}); break;
+        case 3: tiles(std::integral_constant<int, 3>{}); break;
+        case 2: tiles(std::integral_constant<int, 2>{}); break;
+        case 1: tiles(std::integral_constant<int, 1>{}); break;
+        default:  // a wave without rows of the cell: the same barriers and requests, no compute
+          for (int t = 0; t < ntiles; t++) {
+            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
+            published();
+          }
       }
     };
 
@@ -455,43 +462,43 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
     // the query's range, and every candidate goes to base + number
     auto flush = [&]() {
 #pragma unroll
-      for (int ww = 0; ww < NW; ww++) {
+      for (int ww = 0; ww < kEW; ww++) {
         const int nn = S.n[ww];
-        for (int k = tid; k < nn; k += NT) {
-          const uint32_t tg = S.tag[ww][k];
+        for (int e = tid; e < nn; e += kET) {
+          const uint32_t tg = S.tag[ww][e];
           const int j = (int)((tg >> 8) & 0xfffu);
           if (j >= nq) {  // not a pair of the chunk (cannot be staged: its threshold is NaN)
-            S.tag[ww][k] = 0xffffffffu;
+            S.tag[ww][e] = 0xffffffffu;
             continue;
           }
           const Meta m = meta[j];
-          const float est = __builtin_fmaf((float)S.acc[ww][k] * m.qs, zsl[tg & 0xffu], m.qcp);
+          const float est = __builtin_fmaf((float)S.acc[ww][e] * m.qs, zsl[tg & 0xffu], m.qcp);
           if (est >= m.x) {
-            const uint32_t num = atomicAdd(&S.lcnt[j], 1u);  // < 256 rows per item
-            S.acc[ww][k] = __float_as_int(est);
-            S.tag[ww][k] = tg | (num << 20);
+            const uint32_t num = atomicAdd(&S.lcnt[j], 1u);  // < 128 rows per item
+            S.acc[ww][e] = __float_as_int(est);
+            S.tag[ww][e] = tg | (num << 20);
           } else {
-            S.tag[ww][k] = 0xffffffffu;  // admitted by the prefilter only
+            S.tag[ww][e] = 0xffffffffu;  // admitted by the prefilter only
           }
         }
       }
       __syncthreads();
-      for (int j = tid; j < nq; j += NT) {
+      for (int j = tid; j < nq; j += kET) {
         const int c = (int)S.lcnt[j];
         S.lcnt[j] = c ? (uint32_t)atomicAdd(&cnt[meta[j].qid], c) : 0u;
       }
       __syncthreads();
 #pragma unroll
-      for (int ww = 0; ww < NW; ww++) {
+      for (int ww = 0; ww < kEW; ww++) {
         const int nn = S.n[ww];
-        for (int k = tid; k < nn; k += NT) {
-          const uint32_t tg = S.tag[ww][k];
+        for (int e = tid; e < nn; e += kET) {
+          const uint32_t tg = S.tag[ww][e];
           if (tg == 0xffffffffu) continue;
           const int j = (int)((tg >> 8) & 0xfffu);
           const int idx = (int)S.lcnt[j] + (int)(tg >> 20);
           if (idx < CAP) {
             const int64_t q = meta[j].qid;
-            bval[q * CAP + idx] = __int_as_float(S.acc[ww][k]);
+            bval[q * CAP + idx] = __int_as_float(S.acc[ww][e]);
             bpos[q * CAP + idx] = row0 + (int)(tg & 0xffu);
           }
         }
@@ -499,23 +506,23 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
       __syncthreads();  // the flush has read meta and the regions before the next chunk restages them
     };
 
-    // The item's pairs in chunks of csz queries (kMeta at first), each staged, scanned and flushed. A chunk
+    // The item's pairs in chunks of csz queries (kMetaE at first), each staged, scanned and flushed. A chunk
     // whose candidates overflow a wave's region is dropped and scanned again with half as many queries, down
-    // to 8, whose at most 8 x 64 = 512 candidates per wave always fit in kCapE = 640 slots.
-    bool pq_ok = true;  // pq holds the first kMeta pair ids of the item
-    for (int c0 = 0, csz = kMeta;;) {
+    // to 8, whose at most 8 x 64 = 512 candidates per wave always fit in kCapE = 512 slots.
+    bool pq_ok = true;  // pq holds the first kMetaE pair ids of the item
+    for (int c0 = 0, csz = kMetaE;;) {
       nq = min(csz, qn - c0);
       if (!(pq_ok && c0 == 0)) {
 #pragma unroll
-        for (int i = 0; i < kMeta / NT; i++) {
-          const int j = tid + NT * i;
+        for (int i = 0; i < kMetaE / kET; i++) {
+          const int j = tid + kET * i;
           pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
         }
       }
       pq_ok = false;
 #pragma unroll
-      for (int i = 0; i < kMeta / NT; i++) {
-        const int j = tid + NT * i;
+      for (int i = 0; i < kMetaE / kET; i++) {
+        const int j = tid + kET * i;
         if (j < nq) {
           const int pidx = qoff + c0 + j;
           const int q = pq[i];
@@ -531,7 +538,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
       }
       // the last tile's missing queries pass nothing: every compare with NaN is false, also for the +inf
       // prefilter value of a row whose scale is negative or infinite
-      if (tid < 32) Tl[nq + tid] = __builtin_nanf("");
+      if (tid < kTQ) Tl[nq + tid] = __builtin_nanf("");
       ebase = 0;
       __syncthreads();
       scan();
@@ -539,7 +546,7 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
       __syncthreads();
       bool over = false;
 #pragma unroll
-      for (int ww = 0; ww < NW; ww++) over = over || S.n[ww] > kCapE;
+      for (int ww = 0; ww < kEW; ww++) over = over || S.n[ww] > kCapE;
       if (over && csz > 8) {  // the same first pair again, with half the queries
         csz >>= 1;
         pq_ok = false;
@@ -550,16 +557,16 @@ __global__ __launch_bounds__(256, 3) void k_i8_emit(
         // past nq have a NaN threshold). Should it happen, the chunk's staged elements are dropped and bit
         // 30 of each of its queries' counts marks them (a count above any buffer: the query is flagged and
         // recomputed), and the scan goes on instead of halving below 8.
-        for (int j = tid; j < nq; j += NT) atomicOr(&cnt[meta[j].qid], 1 << 30);
+        for (int j = tid; j < nq; j += kET) atomicOr(&cnt[meta[j].qid], 1 << 30);
         __syncthreads();  // every thread has read the region counts
-        if (tid < NW) S.n[tid] = 0;
+        if (tid < kEW) S.n[tid] = 0;
         __syncthreads();
       }
       if (c0 + nq >= qn) break;  // the last chunk is flushed after the next item's loads are issued
       flush();
       c0 += nq;
     }
-    prefetch(nxt);  // the code blocks are no longer needed: the next item's loads run under the flush
+    prefetch(nxt);  // the code rows are no longer needed: the next item's loads run under the flush
     flush();
     cur = nxt;
     p += stride;
@@ -684,15 +691,15 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // persistent grids of three resident workgroups per CU
+  // persistent grids: three first-pass workgroups, six emit workgroups per CU
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_i8_first, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(256), 0, st, q8, qs, qid, qrank,
                        coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, bm, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_emit<kEmitWaves>, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(64 * kEmitWaves), 0, st, q8, qs, qid, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, t0,
-                       cnt, bval, bpos, CAP);
+    hipLaunchKernelGGL(k_i8_emit, dim3((unsigned)min(P, kEmitWG * fvs_cu_count())), dim3(kET), 0, st, q8, qs,
+                       qid, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, qcp, t0, cnt, bval, bpos, CAP);
   }
   return fvs_launch_status();
 }

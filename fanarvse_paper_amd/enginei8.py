@@ -90,7 +90,8 @@ class EngineI8:
     NROUTE = True
     DELTA = 0.07
     LUTH = True
-    CB = 8  # 32-row blocks per stage-1 work item (the kernel stages 4 at a time in LDS)
+    CB = 8  # 32-row blocks per first-pass work item
+    EROWS = 128  # rows per emit work item (the emit kernel's item span)
     NINST = 3  # graph instances per search shape: batches that submit / collect keep in flight
 
     def __init__(self, s1, code, Z, zs, Vr, H=None):
@@ -101,7 +102,7 @@ class EngineI8:
         s2lut.prepare_u(code)
         _, self.MB = index.static_blocks(s1["off_t"], self.BN)
         self.blocks = index.static_chunks(s1["off_t"], self.BN, self.CB)  # first pass: global 32-row blocks
-        self.rchunks = index.row_chunks(s1["off_t"], self.BN * self.CB)   # emit: chunks from each cell's start
+        self.rchunks = index.row_chunks(s1["off_t"], self.EROWS)  # emit: 128-row chunks from each cell's start
         N = Z.shape[0]
         if int(s1["off_t"][-1]) != N or int(self.blocks[3].max()) > N:
             raise ValueError("EngineI8: cell offsets do not match the code rows")

@@ -170,11 +170,11 @@ def static_chunks(off_t, BN=32, CB=8):
     return i32(cell), i32(blk0 * BN), i32(s[cell]), i32(e[cell])
 
 
-def row_chunks(off_t, rows=256):
+def row_chunks(off_t, rows=128):
     """Work items of the emit pass: every non-empty cell's rows in chunks of `rows` from its first row.
     Returns (cell, first row, cell start, cell end) int32 tensors. The emitted set is per row, so any
-    grouping gives the same candidates; starting at the cell's first row leaves no 32-row block that
-    straddles the cell start, and a cell of up to `rows` rows is a single item."""
+    grouping gives the same candidates; starting at the cell's first row leaves no block that straddles
+    the cell start, and a cell of up to `rows` rows is a single item (the emit kernel's items span 128)."""
     off = off_t.long()
     s, e = off[:-1], off[1:]
     nch = (e - s + rows - 1) // rows

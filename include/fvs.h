@@ -174,13 +174,13 @@ int fvs_i8_scan_civf8(int32_t mode, int32_t P, const int8_t *q8, const float *qs
  * int8 stage-1 scan on MFMA (a9, a11), the engine's grouped form of fvs_i8_scan_civf8 (same estimates and
  * emitted sets; throughput/civf8.py:89-91, throughput/ivf8c_kern.py:2-36), plus qrank/n1 so that the first
  * pass writes each query's block maxima straight into its own row.
- *   One workgroup per item p < P: a cell and up to 256 consecutive rows of it (pcell, prow, ps, pe: the
- *   cell, the item's first row, and the cell's first and end row; the item covers rows
- *   [max(prow, ps), min(prow + 256, pe)) as eight 32-row blocks starting at prow). Mode 0: prow is a
- *   multiple of 32 and the items cover each static (cell, global 32-row block) of the reference's work
- *   list (src/s1cell.py:161-168) exactly once. Mode 1: the items cover each row of each cell exactly
- *   once (any grouping; prow = ps + 256 j is the one that wastes least). For every query q of the cell's
- *   pair list:
+ *   Work item p < P: a cell and consecutive rows of it (pcell, prow, ps, pe: the cell, the item's first
+ *   row, and the cell's first and end row). Mode 0: the item covers rows [max(prow, ps), min(prow + 256,
+ *   pe)) as eight 32-row blocks starting at prow; prow is a multiple of 32 and the items cover each static
+ *   (cell, global 32-row block) of the reference's work list (src/s1cell.py:161-168) exactly once.
+ *   Mode 1: the item covers rows [max(prow, ps), min(prow + 128, pe)) (128 rows at most, as eight 16-row
+ *   blocks from prow); the items cover each row of each cell exactly once (any grouping; prow = ps + 128 j,
+ *   index.row_chunks(off, 128), is the one that wastes least). For every query q of the cell's pair list:
  *     acc = sum_j q8[q][j] * Z[n][j] (int32, exact), est = fmaf((float)acc * qs[q], zs[n], qcp[pair]).
  *   mode 0 (first pass): bm[(q*n1 + qrank[pair])*MB + blk - cs/32] = max over the block's rows in the
  *     cell; entries of blocks a cell does not have are left untouched.

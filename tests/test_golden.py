@@ -74,7 +74,9 @@ def test_gpu_reproduces_golden(G):
     bval = torch.empty((B, M), device=dev)
     bpos = torch.empty((B, M), dtype=torch.int32, device=dev)
     pr = _lib.pairs(probe, nprobe, NC, QM, mnorm)
-    _lib.i8_scan(1, blocks, q8, qs, pr, Zc, zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos, CAP=M)
+    # emit items of at most 128 rows on global blocks (four per item): any grouping gives the same sets
+    _lib.i8_scan(1, _index.static_chunks(off_t, 32, 4), q8, qs, pr, Zc, zs, t0=t0, cnt=cnt, bval=bval, bpos=bpos,
+                 CAP=M)
     pos, est1, ok, ncnt = _lib.select(bval, bpos, cnt, K, k - 1, delta)
     pre = _lib.lut_build(Zq, TS, True)
     est, sd = _lib.lut_score(pos, qc, pre, code, ncnt)
