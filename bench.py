@@ -340,7 +340,7 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
                            torch)
     t_emit = _time_launch(lambda: _lib.i8_scan(1, E.rchunks, q8, qs, prn, E.Z, E.zs, t0=t0, cnt=cnt, bval=bval,
                                                bpos=bpos, CAP=M), reps, torch, setup=lambda: _lib.fill_u32(cnt, 0))
-    pre = (tr["L"], tr["qsum"], tr["qn2"])
+    pre = _lib.ZqTables(tr["Zq"], E.LUTF and E.LUTH)  # the engine's scorer: tables built from Zq in the kernel
     ncnt = tr["ncnt"] if E.DELTA is not None else None
     t_lut = _time_launch(lambda: _lib.lut_score(tr["pos"], tr["QC"], pre, E.code, ncnt), reps, torch)
     t_ref = _time_launch(lambda: _lib.refine(tr["est"], tr["sd"], tr["pos"], s1["order"], E.H, Q, args.z, args.k),

@@ -45,6 +45,7 @@ SIGNATURES = {
     "fvs_select": [P, P, P, I64, I32, I32, I32, F32, P, P, P, P, P],
     "fvs_lut_build": [P, I64, I32, I32, P, I32, P, P, P, P],
     "fvs_lut_score": [P, P, P, I32, I32, P, P, P, I64, I32, I32, I32, P, P, P, I32, P, I64, I32, P, P, P],
+    "fvs_lut_score_zq": [P, P, P, I32, I32, P, I64, I32, I32, I32, P, P, P, I32, P, I64, I32, P, P, P],
     "fvs_refine": [P, P, P, P, P, P, I64, I32, I32, F32, I32, P, P, P, P, P],
     "fvs_classify": [P, P, P, P, I64, I32, F32, I32, P, P, P, P, P],
     "fvs_refine_rows": [P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
@@ -339,20 +340,40 @@ def lut_build(Zq, TS, half):
     return L, qsum, qn2
 
 
+class ZqTables:
+    """Stand-in for lut_build's (L, qsum, qn2): the rotated queries Zq, from which fvs_lut_score_zq forms the
+    same tables inside the scoring kernel (no table in memory, no build launch)."""
+
+    def __init__(self, Zq, half):
+        self.Zq, self.half = Zq, bool(half)
+
+
 def lut_score(pos, qc, pre, code, ncnt=None, nt=None):
     """(est, sd) [B, K] of the candidates (throughput/s2lut.py:92-106), from the packed records; nt: the
-    partial estimate over the first nt tiers (score_lut(..., nt=...), throughput/s2lut.py:92-93)."""
-    L, qsum, qn2 = pre
+    partial estimate over the first nt tiers (score_lut(..., nt=...), throughput/s2lut.py:92-93). `pre` is
+    lut_build's (L, qsum, qn2) or a ZqTables (the same results, tables built inside the scorer)."""
     B, K = pos.shape
     TS = code["TS"]
     T = len(TS)
     rec = code["rec"]
     N, RB = rec.shape
-    half = L.dtype == torch.float16
     deltas = (ctypes.c_float * T)(*[float(code["deltas"][b]) for _, _, b in TS])
     toff = (ctypes.c_int32 * T)(*[int(x) for x in code["toff"]])
     est = _empty((B, K), torch.float32, pos.device)
     sd = _empty((B, K), torch.float32, pos.device)
+    if isinstance(pre, ZqTables):
+        Zq = pre.Zq
+        if Zq.dim() != 2 or Zq.shape[0] != B:
+            raise ValueError("lut_score: Zq must be [B, D]")
+        _check(lib().fvs_lut_score_zq(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
+                                      _dev(Zq, torch.float16, "Zq"), Zq.shape[1], int(pre.half),
+                                      _dev(rec, torch.uint8, "rec"), N, RB, int(code["soff"]), T, _tiers_arr(TS), deltas,
+                                      toff, int(nt or 0), _opt(ncnt, torch.int32, "ncnt", (B,)), B, K,
+                                      _dev(est, torch.float32, "est"), _dev(sd, torch.float32, "sd"), _stream()),
+               "fvs_lut_score_zq")
+        return est, sd
+    L, qsum, qn2 = pre
+    half = L.dtype == torch.float16
     _check(lib().fvs_lut_score(_dev(pos, torch.int32, "pos"), _dev(qc, torch.float32, "qc", (B,)),
                                _dev(L, L.dtype, "L"), int(half), L.shape[1], _dev(qsum, torch.float32, "qsum", (T, B)),
                                _dev(qn2, torch.float32, "qn2", (T, B)), _dev(rec, torch.uint8, "rec"), N, RB,

@@ -93,6 +93,7 @@ constexpr int kUD = kUnit * 4;       // dwords per unit
 constexpr int kZeroBytes = 512;      // zero table after the LUT: dwords past the planes look up zeros
 constexpr int kSchedMax = 512;       // record dwords (whole units) the schedule covers: records up to 2 KiB
 constexpr int kSetupVec = 16;        // 16-byte table vectors per thread in the one-pass set-up (LW <= 16384)
+constexpr int kSetupPos = 4;         // FUSED: 4-coordinate table groups per thread (D <= 4096)
 
 // Schedule: one descriptor per record dword, the same for every record and query, built on the host and
 // passed as a kernel argument. Kernel arguments are read through the scalar cache, so a dword's descriptor
@@ -142,12 +143,15 @@ __device__ __forceinline__ void lookup8(const char *lutb, uint32_t x, uint32_t l
   }
 }
 
-template <bool HALF, int TT>
+// FUSED: the kernel builds the query's table and tier sums itself from its rotated query Zq (fp16 [B, D]), with
+// k_lut_build's operations (the same entries, fp16-rounded when HALF, and the same double sums), instead of
+// reading the table L and the sums qsum / qn2 that k_lut_build wrote; the results are the same bits.
+template <bool HALF, int TT, bool FUSED>
 __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     const int32_t *__restrict__ pos, const float *__restrict__ qc, const void *__restrict__ Lin, int LW,
-    const float *__restrict__ qsum, const float *__restrict__ qn2, const uint8_t *__restrict__ rec, int RB, int U,
-    TierArgs ta, ScoreSched sched, const int32_t *__restrict__ ncnt, int64_t N, int64_t B, int K,
-    float *__restrict__ est, float *__restrict__ sdo) {
+    const float *__restrict__ qsum, const float *__restrict__ qn2, const uint16_t *__restrict__ Zq, int D,
+    const uint8_t *__restrict__ rec, int RB, int U, TierArgs ta, ScoreSched sched, const int32_t *__restrict__ ncnt,
+    int64_t N, int64_t B, int K, float *__restrict__ est, float *__restrict__ sdo) {
   // the table comes first in LDS (no static LDS), so a schedule offset is an LDS address as it stands
   extern __shared__ int32_t smem[];
   int32_t *lut = smem;                                                  // [LW] fixed-point tables + zero table
@@ -162,16 +166,24 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   // 1. every global read of the set-up is issued at once: the query's table (one pass, held in registers),
   //    its candidate rows, its tier constants, and the first unit of this lane's first record
   const int nvec = HALF ? LW / 8 : LW / 4;  // 16-byte vectors of the table: 8 halves or 4 floats each
-  const uint4 *L4 = reinterpret_cast<const uint4 *>(Lin) + q * nvec;
-  uint4 lv[kSetupVec];
+  uint4 lv[FUSED ? 1 : kSetupVec];
+  uint2 zv[FUSED ? kSetupPos : 1];  // FUSED: the four query coordinates of each of this thread's table groups
+  if constexpr (FUSED) {
+    const uint2 *Z2 = reinterpret_cast<const uint2 *>(Zq + q * (int64_t)D);
 #pragma unroll
-  for (int c = 0; c < kSetupVec; c++)
-    if (tid + kScoreThreads * c < nvec) lv[c] = L4[tid + kScoreThreads * c];
+    for (int c = 0; c < kSetupPos; c++)
+      if (tid + kScoreThreads * c < D / 4) zv[c] = Z2[tid + kScoreThreads * c];
+  } else {
+    const uint4 *L4 = reinterpret_cast<const uint4 *>(Lin) + q * nvec;
+#pragma unroll
+    for (int c = 0; c < kSetupVec; c++)
+      if (tid + kScoreThreads * c < nvec) lv[c] = L4[tid + kScoreThreads * c];
+  }
   const int lim = ncnt ? min(ncnt[q], K) : K;
   for (int i = tid; i < K; i += kScoreThreads)
     rows[i] = (int32_t)min(max((int64_t)pos[q * (int64_t)K + i], (int64_t)0), N - 1);
   float tq0 = 0.f, tq1 = 0.f;
-  if (tid < T) {
+  if (!FUSED && tid < T) {
     tq0 = qsum[(int64_t)tid * B + q];
     tq1 = qn2[(int64_t)tid * B + q];
   }
@@ -190,12 +202,58 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     return HALF ? fvs_h2f((uint16_t)((u & 1) ? x >> 16 : x & 0xffffu)) : __uint_as_float(x);
   };
   float m = 0.f;
+  float ov[FUSED ? kSetupPos : 1][16];  // FUSED: this thread's table entries (group tid + 256 c, nibble v)
+  if constexpr (FUSED) {
+    // entries as k_lut_build computes them: sum over i of fmaf(z_i, bit (3 - i) of v, .) in i order, then
+    // fp16-rounded when HALF
 #pragma unroll
-  for (int c = 0; c < kSetupVec; c++)
-    if (tid + kScoreThreads * c < nvec) {
+    for (int c = 0; c < kSetupPos; c++) {
+      if (tid + kScoreThreads * c < D / 4) {
+        const float z[4] = {fvs_h2f((uint16_t)(zv[c].x & 0xffffu)), fvs_h2f((uint16_t)(zv[c].x >> 16)),
+                            fvs_h2f((uint16_t)(zv[c].y & 0xffffu)), fvs_h2f((uint16_t)(zv[c].y >> 16))};
 #pragma unroll
-      for (int u = 0; u < kPer; u++) m = fmaxf(m, fabsf(entry(lv[c], u)));
+        for (int v = 0; v < 16; v++) {
+          float a = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++) a = __builtin_fmaf(z[i], (float)((v >> (3 - i)) & 1), a);
+          ov[c][v] = HALF ? fvs_round_h(a) : a;
+          m = fmaxf(m, fabsf(ov[c][v]));
+        }
+      }
     }
+    // the tier sums as k_lut_build forms them: wave t & 3 sums tier t, lane l the coordinates start + l,
+    // start + l + 64, ... in double, then a fixed xor butterfly
+    const int lane = tid & 63, wv = fvs_wave_id();
+    const uint16_t *zr = Zq + q * (int64_t)D;
+#pragma unroll
+    for (int t = 0; t < FVS_MAX_TIERS; t++) {
+      if (t < T && (t & 3) == wv) {
+        const int i0 = ta.loff[t] / 4, i1 = i0 + 8 * ta.kb[t];
+        double s1 = 0.0, s2 = 0.0;
+        for (int i = i0 + lane; i < i1; i += 64) {
+          const double x = (double)fvs_h2f(zr[i]);
+          s1 += x;
+          s2 += x * x;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          s1 += fvs_xor_lane_d(s1, o);
+          s2 += fvs_xor_lane_d(s2, o);
+        }
+        if (lane == 0) {
+          tf[4 * t + 2] = (float)s1;
+          tf[4 * t + 3] = (float)s2;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kSetupVec; c++)
+      if (tid + kScoreThreads * c < nvec) {
+#pragma unroll
+        for (int u = 0; u < kPer; u++) m = fmaxf(m, fabsf(entry(lv[c], u)));
+      }
+  }
   m = fvs_wave_max(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
@@ -208,12 +266,27 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     (void)frexpf(mm, &E);
     s = max(0, E - 3);
   }
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int c = 0; c < kSetupVec; c++) {
-    const int i = tid + kScoreThreads * c;
-    if (i < nvec) {
+    for (int c = 0; c < kSetupPos; c++) {
+      const int n = tid + kScoreThreads * c;
+      if (n < D / 4) {
+        int32_t w[16];
 #pragma unroll
-      for (int u = 0; u < kPer; u++) lut[kPer * i + u] = (int32_t)rintf(ldexpf(entry(lv[c], u), 24 - s));
+        for (int v = 0; v < 16; v++) w[v] = (int32_t)rintf(ldexpf(ov[c][v], 24 - s));
+        int4 *dst = reinterpret_cast<int4 *>(lut + 16 * n);
+#pragma unroll
+        for (int v = 0; v < 4; v++) dst[v] = make_int4(w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kSetupVec; c++) {
+      const int i = tid + kScoreThreads * c;
+      if (i < nvec) {
+#pragma unroll
+        for (int u = 0; u < kPer; u++) lut[kPer * i + u] = (int32_t)rintf(ldexpf(entry(lv[c], u), 24 - s));
+      }
     }
   }
   for (int i = tid; i < kZeroBytes / 4; i += kScoreThreads) lut[LW + i] = 0;
@@ -222,8 +295,10 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     if (t < T && tid == t) {
       tf[4 * t + 0] = ta.delta[t];
       tf[4 * t + 1] = ta.mid[t];
-      tf[4 * t + 2] = tq0;
-      tf[4 * t + 3] = tq1;
+      if (!FUSED) {
+        tf[4 * t + 2] = tq0;
+        tf[4 * t + 3] = tq1;
+      }
     }
   }
   __syncthreads();
@@ -406,11 +481,15 @@ extern "C" int fvs_lut_build(const uint16_t *Zq, int64_t B, int32_t D, int32_t T
   return fvs_launch_status();
 }
 
-extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
-                             const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB,
-                             int32_t soff, int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff,
-                             int32_t nt, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
-                             void *stream) {
+namespace {
+
+// Checks, schedule and launch shared by fvs_lut_score (table L and sums qsum / qn2 from fvs_lut_build) and
+// fvs_lut_score_zq (the kernel builds them from the rotated queries Zq: fused = true).
+int lut_score_impl(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW, const float *qsum,
+                   const float *qn2, const uint16_t *Zq, int32_t D, bool fused, const uint8_t *rec, int64_t N,
+                   int32_t RB, int32_t soff, int32_t T, const int32_t *tiers, const float *deltas,
+                   const int32_t *toff, int32_t nt, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
+                   void *stream) {
   // LW = 16 entries per 4 coordinates, in whole 512-byte table groups (tiers are whole 32-coordinate blocks)
   if (B < 0 || K <= 0 || N <= 0 || LW <= 0 || LW > 16384 || LW % 128 != 0) return FVS_E_ARG;
   if (RB <= 0 || RB % 16 != 0 || soff <= 0 || soff % 4 != 0) return FVS_E_ARG;
@@ -430,7 +509,8 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (nt < 0 || nt > T) return FVS_E_ARG;
   if (nt > 0) ta.T = nt;
   if (B == 0) return FVS_OK;
-  if (!pos || !qc || !L || !qsum || !qn2 || !rec || !est || !sd) return FVS_E_ARG;
+  if (!pos || !qc || !rec || !est || !sd) return FVS_E_ARG;
+  if (fused ? !Zq : (!L || !qsum || !qn2)) return FVS_E_ARG;
   if (K > 4096) return FVS_E_CAPACITY;
   const int units = (soff / 4 + T + kUD - 1) / kUD;
   ScoreSched sched;
@@ -441,26 +521,55 @@ extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L,
   if (shm > 160 * 1024 - 64) return FVS_E_CAPACITY;
   hipStream_t st = (hipStream_t)stream;
   // one instantiation per tier count, so the tier queues have a static size
-  auto launch = [&](auto HALF_, auto TT_) {
-    hipLaunchKernelGGL((k_lut_score<decltype(HALF_)::value, decltype(TT_)::value>), dim3((unsigned)B),
-                       dim3(kScoreThreads), shm, st, pos, qc, L, LW, qsum, qn2, rec, RB, units, ta, sched, ncnt, N, B,
-                       K, est, sd);
+  auto launch = [&](auto HALF_, auto TT_, auto FUSED_) {
+    hipLaunchKernelGGL((k_lut_score<decltype(HALF_)::value, decltype(TT_)::value, decltype(FUSED_)::value>),
+                       dim3((unsigned)B), dim3(kScoreThreads), shm, st, pos, qc, L, LW, qsum, qn2, Zq, D, rec, RB,
+                       units, ta, sched, ncnt, N, B, K, est, sd);
   };
-  auto by_t = [&](auto HALF_) {
+  auto by_t = [&](auto HALF_, auto FUSED_) {
     switch (ta.T) {
-      case 1: launch(HALF_, std::integral_constant<int, 1>{}); break;
-      case 2: launch(HALF_, std::integral_constant<int, 2>{}); break;
-      case 3: launch(HALF_, std::integral_constant<int, 3>{}); break;
-      case 4: launch(HALF_, std::integral_constant<int, 4>{}); break;
-      case 5: launch(HALF_, std::integral_constant<int, 5>{}); break;
-      case 6: launch(HALF_, std::integral_constant<int, 6>{}); break;
-      case 7: launch(HALF_, std::integral_constant<int, 7>{}); break;
-      default: launch(HALF_, std::integral_constant<int, 8>{}); break;
+      case 1: launch(HALF_, std::integral_constant<int, 1>{}, FUSED_); break;
+      case 2: launch(HALF_, std::integral_constant<int, 2>{}, FUSED_); break;
+      case 3: launch(HALF_, std::integral_constant<int, 3>{}, FUSED_); break;
+      case 4: launch(HALF_, std::integral_constant<int, 4>{}, FUSED_); break;
+      case 5: launch(HALF_, std::integral_constant<int, 5>{}, FUSED_); break;
+      case 6: launch(HALF_, std::integral_constant<int, 6>{}, FUSED_); break;
+      case 7: launch(HALF_, std::integral_constant<int, 7>{}, FUSED_); break;
+      default: launch(HALF_, std::integral_constant<int, 8>{}, FUSED_); break;
     }
   };
-  if (half)
-    by_t(std::true_type{});
-  else
-    by_t(std::false_type{});
+  if (fused) {
+    if (half)
+      by_t(std::true_type{}, std::true_type{});
+    else
+      by_t(std::false_type{}, std::true_type{});
+  } else {
+    if (half)
+      by_t(std::true_type{}, std::false_type{});
+    else
+      by_t(std::false_type{}, std::false_type{});
+  }
   return fvs_launch_status();
+}
+
+}  // namespace
+
+extern "C" int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t half, int32_t LW,
+                             const float *qsum, const float *qn2, const uint8_t *rec, int64_t N, int32_t RB,
+                             int32_t soff, int32_t T, const int32_t *tiers, const float *deltas, const int32_t *toff,
+                             int32_t nt, const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd,
+                             void *stream) {
+  return lut_score_impl(pos, qc, L, half, LW, qsum, qn2, nullptr, 0, false, rec, N, RB, soff, T, tiers, deltas, toff,
+                        nt, ncnt, B, K, est, sd, stream);
+}
+
+extern "C" int fvs_lut_score_zq(const int32_t *pos, const float *qc, const uint16_t *Zq, int32_t D, int32_t half,
+                                const uint8_t *rec, int64_t N, int32_t RB, int32_t soff, int32_t T,
+                                const int32_t *tiers, const float *deltas, const int32_t *toff, int32_t nt,
+                                const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream) {
+  // the table covers the D coordinates of the tiers: 16 entries per 4 coordinates; the last tier ends at D
+  if (D <= 0 || D % 32 != 0 || D > 4 * kScoreThreads * kSetupPos) return FVS_E_ARG;
+  if (T <= 0 || T > FVS_MAX_TIERS || !tiers || tiers[3 * (T - 1) + 1] != D) return FVS_E_SHAPE;
+  return lut_score_impl(pos, qc, nullptr, half, D / 4 * 16, nullptr, nullptr, Zq, D, true, rec, N, RB, soff, T,
+                        tiers, deltas, toff, nt, ncnt, B, K, est, sd, stream);
 }

@@ -198,9 +198,10 @@ class EngineI8:
         s1 = self.s1
         qp = _lib.query_prep(Qb, self.Vr, s1["c"])
         q8, qs, QC, Qh, zq = qp
-        # the stage-2 tables depend only on the fp16 queries: a side stream builds them while stage 1 runs.
-        # The routing product is issued before the side branch: it heads the critical path, and a branch
-        # issued ahead of it was measured to hold it back until the branch's first node had finished.
+        # the stage-2 inputs depend only on the fp16 queries: a side stream computes the rotated queries while
+        # stage 1 runs (the LUT scorer builds its tables from them). The routing product is issued before the
+        # side branch: it heads the critical path, and a branch issued ahead of it was measured to hold it back
+        # until the branch's first node had finished.
         main = torch.cuda.current_stream()
         if self._side is None:
             self._side = torch.cuda.Stream(device=Qb.device)
@@ -211,9 +212,8 @@ class EngineI8:
         half = self.LUTF and self.LUTH
         with torch.cuda.stream(self._side):
             Zq = s2lut.rotate(self.code, Qh)
-            pre = _lib.lut_build(Zq, self.code["TS"], half)
-        for t in (Zq, *pre):  # made on the side stream, used on this one
-            t.record_stream(main)
+        Zq.record_stream(main)  # made on the side stream, used on this one
+        pre = _lib.ZqTables(Zq, half)
         QM, probe = self._route(Qh, QC, nprobe, QM0)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)
         main.wait_stream(self._side)
@@ -222,9 +222,10 @@ class EngineI8:
         return ok, I, reads, ids, scores, (zq, QM0, Zq)  # the fallback routes on the plain QM
 
     def _finish(self, Qb, Zq, QC, pos, ok, K, z, k, half, ncnt, pre=None):
-        """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95)."""
+        """LUT stage 2, error bars, exact reads and the final top-k (throughput/enginei8.py:80-95). The LUT scorer
+        forms the tables of luts_fused (throughput/s2lut.py:108-126) from Zq itself (fvs_lut_score_zq)."""
         if pre is None:
-            pre = _lib.lut_build(Zq, self.code["TS"], half)
+            pre = _lib.ZqTables(Zq, half)
         if self.K2 is not None and self.K2 < K:
             # progressive stage 2 (throughput/enginei8.py:82-85): rank all K by the partial estimate over the
             # first NT tiers, keep the K2 best
@@ -391,7 +392,8 @@ class EngineI8:
         half = self.LUTF and self.LUTH
         ncnt = self._ncnt if self.DELTA is not None else None
         Zq = s2lut.rotate(self.code, Qh)
-        pre = _lib.lut_build(Zq, self.code["TS"], half)
+        tables = _lib.lut_build(Zq, self.code["TS"], half)  # returned for inspection; the scorer builds its own
+        pre = _lib.ZqTables(Zq, half)
         pos1 = pos
         if self.K2 is not None and self.K2 < K:
             e_all, _ = s2lut.score_lut(self.code, QC, pos, pre, None, nt=min(self.NT, len(self.code["TS"])))
@@ -403,7 +405,7 @@ class EngineI8:
         ids, I, scores, reads = _lib.refine(est, sd, pos, self.s1["order"], self.H, Qb, z, k)
         return dict(q8=q8, qs=qs, QC=QC, Qh=Qh, z=zq, QM=QM, probe=probe, bm=self._bm, n1=self._n1, M=self._M,
                     t0=self._t0, cnt=self._cnt, bval=self._bval, bpos=self._bpos, pos=pos, pos1=pos1, est1=self._est1, ok=ok,
-                    ncnt=self._ncnt, Zq=Zq, L=pre[0], qsum=pre[1], qn2=pre[2], est=est, sd=sd, ids=ids, I=I,
+                    ncnt=self._ncnt, Zq=Zq, L=tables[0], qsum=tables[1], qn2=tables[2], est=est, sd=sd, ids=ids, I=I,
                     scores=scores, reads=reads)
 
     def gpu_bytes(self):

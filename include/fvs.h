@@ -257,6 +257,19 @@ int fvs_lut_score(const int32_t *pos, const float *qc, const void *L, int32_t ha
                   const int32_t *ncnt, int64_t B, int32_t K, float *est, float *sd, void *stream);
 
 /*
+ * LUT stage 2 fused with its table build (a13 + a15): the same est and sd as fvs_lut_build followed by
+ * fvs_lut_score with the same half, but each query's table and tier sums are formed inside the scoring
+ * kernel from its rotated query (throughput/s2lut.py:108-126 feeding :48-106), so the table never goes
+ * through memory and the separate build launch disappears.
+ *   Zq fp16 [B, D] (as fvs_lut_build); D % 32 == 0, D <= 4096, and the last tier ends at D. The other
+ *   arguments and the canonical arithmetic are fvs_lut_score's (with LW = D / 4 * 16).
+ */
+int fvs_lut_score_zq(const int32_t *pos, const float *qc, const uint16_t *Zq, int32_t D, int32_t half,
+                     const uint8_t *rec, int64_t N, int32_t RB, int32_t soff, int32_t T, const int32_t *tiers,
+                     const float *deltas, const int32_t *toff, int32_t nt, const int32_t *ncnt, int64_t B, int32_t K,
+                     float *est, float *sd, void *stream);
+
+/*
  * Error-bar classification, exact refinement and final top-k (a16, a17, a18). Replaces
  * throughput/enginei8.py:92-95, src/engine3.py:143-146 and src/stage3_zc.py:11-27.
  *   est, sd f32 [B, K]; pos i32 [B, K]; order i32 [N]; H fp16 [n_ids, d] in id order (device memory or a

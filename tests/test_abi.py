@@ -99,6 +99,20 @@ def test_lut_score_layout_checks_need_no_gpu(L):
     assert call(LW=1552, D=388, bits=4, RB=208) == E_ARG      # LW % 128 (tiers are whole 32-coordinate blocks)
     assert call(LW=16384, D=4096, bits=4, RB=2064) == E_CAP   # 513 dwords of planes and pair: past 512
 
+    # the fused form takes the query width D instead of a table: D % 32, D <= 4096, the last tier ending at D
+    def call_zq(D, tier_end, bits, RB):
+        tiers = (ctypes.c_int32 * 3)(0, tier_end, bits)
+        deltas = (ctypes.c_float * 1)(1.0)
+        soff = tier_end * bits // 8
+        toff = (ctypes.c_int32 * 1)(0)
+        return L.fvs_lut_score_zq(p, p, p, D, 1, p, 10, RB, soff, 1, tiers, deltas, toff, 0, None, 1, 10, p, p, None)
+
+    E_SHAPE = -2
+    assert call_zq(D=388, tier_end=388, bits=4, RB=208) == E_ARG     # D % 32
+    assert call_zq(D=4128, tier_end=4128, bits=1, RB=528) == E_ARG   # D > 4096
+    assert call_zq(D=384, tier_end=352, bits=4, RB=192) == E_SHAPE  # the tiers end before D
+    assert call_zq(D=4096, tier_end=4096, bits=4, RB=2064) == E_CAP  # the record's schedule past 512 dwords
+
 
 def test_wrappers_refuse_cpu_tensors(L):
     from fanarvse_paper_amd import _lib

@@ -125,6 +125,28 @@ def test_select_and_stage2_bit_exact(traced):
     assert np.array_equal(npy(tr["sd"])[ok].view(np.uint32), out["sd"][ok].view(np.uint32))
 
 
+def test_fused_lut_scorer_matches_build_then_score(env, traced):
+    """fvs_lut_score_zq (tables and tier sums formed inside the scorer from Zq) gives the bits of
+    fvs_lut_build followed by fvs_lut_score: fp16 and fp32 tables, all tiers or the leading two, with and
+    without the delta-rule counts."""
+    from fanarvse_paper_amd import _lib
+
+    tr, _ = traced
+    code = env["code"]
+    dev = "cuda"
+    pos, QC, Zq = tr["pos"].to(dev), tr["QC"].to(dev), tr["Zq"].to(dev)
+    ncnt = tr["ncnt"].to(dev)
+    for half in (True, False):
+        pre = _lib.lut_build(Zq, code["TS"], half)
+        for nt in (None, 2):
+            for nc in (ncnt, None):
+                a = _lib.lut_score(pos, QC, pre, code, nc, nt)
+                b = _lib.lut_score(pos, QC, _lib.ZqTables(Zq, half), code, nc, nt)
+                torch.cuda.synchronize()
+                for x, y in zip(a, b):
+                    assert np.array_equal(npy(x).view(np.uint32), npy(y).view(np.uint32)), (half, nt, nc is None)
+
+
 def test_refine_and_final_ids_bit_exact(traced):
     tr, out = traced
     ok = out["ok"] == 1
