@@ -28,6 +28,7 @@ SIGNATURES = {
     "fvs_pack_ids": [P, P, I64, I32, P, P],
     "fvs_dense_small": [P, I64, I32, P, I32, P, P, I32, P, P, I32, P, P, P, P],
     "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
+    "fvs_query_code": [P, I64, I32, P, I32, P, P, P, P, P, P, P],
     "fvs_build_codes": [P, P, P, I64, I32, P, P, I32, P, P, P],
     "fvs_route_topk": [P, I64, I32, I32, P, P],
     "fvs_pairs_scratch_bytes": [I64, I32],
@@ -150,18 +151,30 @@ def dense_small(Q, W1T, M16, VPT, c):
     return Qr, QM, Zq, qc
 
 
-def query_prep(Q, Vr, c, z=None):
+def query_prep(Q, Vr, c, z=None, canonical=False):
     """q8 [B,R] int8, qs [B], qc [B], qh [B,d] fp16 and the projection z [B,R] (throughput/enginei8.py:38, :62).
-    z = Q @ Vr is an fp32 BLAS product, as in the reference (pass it to reuse rows of an earlier product);
-    the rest runs in one kernel."""
+    z = Q @ Vr is the fp32 BLAS product, as in the reference, unless given (rows of an earlier projection, or
+    another engine's product); the code, centre term and fp16 copy are derived from it in one launch. With
+    canonical=True (and no z) one launch computes everything, z as a sequential fp32 fmaf chain over d (the
+    index build's order, which the oracle reproduces bit for bit)."""
     B, d = Q.shape
     R = z.shape[1] if z is not None else Vr.shape[1]
     dev = Q.device
-    z = (Q @ Vr).contiguous() if z is None else z.contiguous()
     q8 = _empty((B, R), torch.int8, dev)
     qs = _empty((B,), torch.float32, dev)
     qc = _empty((B,), torch.float32, dev)
     qh = _empty((B, d), torch.float16, dev)
+    if z is None and not canonical:
+        z = Q @ Vr
+    if z is None:
+        z = _empty((B, R), torch.float32, dev)
+        _check(lib().fvs_query_code(_dev(Q, torch.float32, "Q"), B, d, _dev(Vr, torch.float32, "Vr", (d, R)), R,
+                                    _dev(c, torch.float32, "c", (d,)), _dev(z, torch.float32, "z"),
+                                    _dev(q8, torch.int8, "q8"), _dev(qs, torch.float32, "qs"),
+                                    _dev(qc, torch.float32, "qc"), _dev(qh, torch.float16, "qh"), _stream()),
+               "fvs_query_code")
+        return q8, qs, qc, qh, z
+    z = z.contiguous()
     _check(lib().fvs_query_prep(_dev(Q, torch.float32, "Q"), B, d, _dev(z, torch.float32, "z", (B, R)), R,
                                 _dev(c, torch.float32, "c", (d,)), _dev(q8, torch.int8, "q8"), _dev(qs, torch.float32, "qs"),
                                 _dev(qc, torch.float32, "qc"), _dev(qh, torch.float16, "qh"), _stream()),

@@ -34,12 +34,16 @@ __device__ __forceinline__ void stage_rows(float (*xs)[QB], const float *__restr
   }
 }
 
+// RESID: rows are the cell residuals of the base set (index build). Otherwise rows are queries, and the block
+// also writes the projection z itself (zout), qc = <Q, c> and the fp16 copy qh as k_query_code computes them.
 template <int QB, bool RESID>
 __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, const uint16_t *__restrict__ X16,
                                                  const int32_t *__restrict__ order, const int32_t *__restrict__ cell,
                                                  const uint16_t *__restrict__ M16, int64_t nrows, int d,
                                                  const float *__restrict__ Vr, int8_t *__restrict__ out8,
-                                                 float *__restrict__ outs) {
+                                                 float *__restrict__ outs, float *__restrict__ zout,
+                                                 const float *__restrict__ c, float *__restrict__ qc,
+                                                 uint16_t *__restrict__ qh) {
   __shared__ float xs[2][kKC][QB];
   __shared__ float red[QB][4];
   const int j = threadIdx.x;
@@ -103,6 +107,25 @@ __global__ __launch_bounds__(256) void k_project(const float *__restrict__ Q, co
     qv = fminf(fmaxf(qv, -127.0f), 127.0f);
     out8[row * kR + j] = (int8_t)(int)qv;
     if (j == 0) outs[row] = a;
+    if (!RESID) zout[row * kR + j] = acc[rr];
+  }
+  if constexpr (!RESID) {
+    // qc and the fp16 copy, one wave per row: lane l sums the exact double products of coordinates
+    // l, l + 64, ... in order, then the fixed xor butterfly (k_query_code's order)
+    for (int rr = w; rr < QB; rr += 4) {
+      const int64_t row = r0 + rr;
+      if (row >= nrows) continue;
+      const float *qr = Q + row * d;
+      double sacc = 0.0;
+      for (int k = lane; k < d; k += 64) {
+        const float x = qr[k];
+        qh[row * d + k] = fvs_f2h(x);
+        sacc += (double)x * (double)c[k];
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) sacc += fvs_xor_lane_d(sacc, o);
+      if (lane == 0) qc[row] = (float)sacc;
+    }
   }
 }
 
@@ -257,6 +280,19 @@ extern "C" int fvs_build_codes(const uint16_t *X16, const int32_t *order, const 
   constexpr int QB = 64;
   const int64_t nb = (N + QB - 1) / QB;
   hipLaunchKernelGGL((k_project<QB, true>), dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, nullptr, X16,
-                     order, cell, means16, N, d, Vr, Z, zs);
+                     order, cell, means16, N, d, Vr, Z, zs, nullptr, nullptr, nullptr, nullptr);
+  return fvs_launch_status();
+}
+
+extern "C" int fvs_query_code(const float *Q, int64_t B, int32_t d, const float *Vr, int32_t R, const float *c,
+                              float *z, int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream) {
+  if (R != kR) return FVS_E_SHAPE;
+  if (B < 0 || d <= 0 || d % 8 != 0) return FVS_E_ARG;
+  if (B == 0) return FVS_OK;
+  if (!Q || !Vr || !c || !z || !q8 || !qs || !qc || !qh) return FVS_E_ARG;
+  constexpr int QB = 8;  // 250 workgroups for a batch of 2000
+  const int64_t nb = (B + QB - 1) / QB;
+  hipLaunchKernelGGL((k_project<QB, false>), dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, Q, nullptr,
+                     nullptr, nullptr, nullptr, B, d, Vr, q8, qs, z, c, qc, qh);
   return fvs_launch_status();
 }

@@ -93,6 +93,10 @@ class EngineI8:
     CB = 8  # 32-row blocks per first-pass work item
     EROWS = 128  # rows per emit work item (the emit kernel's item span)
     NINST = 3  # graph instances per search shape: batches that submit / collect keep in flight
+    # the projection z = Qb @ Vr of the query code: False, the fp32 library GEMM (as the reference's cuBLAS
+    # product); True, fvs_query_code's sequential fmaf chain, which the oracle reproduces bit for bit (its VALU
+    # work costs about 3.5 % of the pipelined throughput against the matrix-core GEMM)
+    CANON_Z = False
 
     def __init__(self, s1, code, Z, zs, Vr, H=None):
         if self.BN != 32:
@@ -118,7 +122,7 @@ class EngineI8:
     def _knobs(self):
         """The knob values captured work depends on: a search after a change captures new graphs."""
         return (self.MSZ, self.BETA, self.RHO, self.DELTA, self.LUTF, self.LUTH, self.NROUTE, self.ROUTE16,
-                self.PROJ, self.UNSORTED, self.SORTROUTE, self.K2, self.NT)
+                self.PROJ, self.UNSORTED, self.SORTROUTE, self.K2, self.NT, self.CANON_Z)
 
     def _check_knobs(self):
         if self.PROJ and not self.NROUTE and "W1" not in self.s1:
@@ -145,7 +149,7 @@ class EngineI8:
         s1 = self.s1
         NC = len(s1["off"]) - 1
         B = Qb.shape[0]
-        q8, qs = (qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"]))[:2]
+        q8, qs = (qp if qp is not None else _lib.query_prep(Qb, self.Vr, s1["c"], canonical=self.CANON_Z))[:2]
         M, n1, r = self._params(K, probe.shape[1], rho_override, M_override)
         scratch = _lib.pairs_scratch(B, NC, Qb.device)
         # NROUTE: QM holds normalised-mean scores, the pair constants scale them back by |m_c|
@@ -196,7 +200,7 @@ class EngineI8:
         if self.H is None:
             raise RuntimeError("EngineI8.H (fp16 vectors in id order) must be set before searching")
         s1 = self.s1
-        qp = _lib.query_prep(Qb, self.Vr, s1["c"])
+        qp = _lib.query_prep(Qb, self.Vr, s1["c"], canonical=self.CANON_Z)
         q8, qs, QC, Qh, zq = qp
         # the stage-2 inputs depend only on the fp16 queries: a side stream computes the rotated queries while
         # stage 1 runs (the LUT scorer builds its tables from them). The routing product is issued before the
@@ -385,7 +389,7 @@ class EngineI8:
         """Eager run of one batch that returns every intermediate (for parity tests and profiling)."""
         self._check_knobs()
         Qb = Qb.float().contiguous()
-        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"])
+        qp = _lib.query_prep(Qb, self.Vr, self.s1["c"], canonical=self.CANON_Z)
         q8, qs, QC, Qh, zq = qp
         QM, probe = self._route(Qh, QC, nprobe)
         pos, ok = self.stage1_i8(Qb, QM, probe, K, qp=qp, delta=self.DELTA, kd=k - 1)

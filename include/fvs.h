@@ -84,6 +84,17 @@ int fvs_query_prep(const float *Q, int64_t B, int32_t d, const float *z, int32_t
                    int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream);
 
 /*
+ * fvs_query_prep with the projection computed by the library: z f32 [B, R] = Q @ Vr (Vr f32 [d, R],
+ * row-major), each output a sequential fmaf chain over k = 0 .. d - 1 from +0 (the order of fvs_build_codes'
+ * projection, so the oracle reproduces z bit for bit), written to z; then q8, qs, qc and qh exactly as
+ * fvs_query_prep computes them from that z. Replaces the fp32 BLAS product Qb @ Vr of
+ * throughput/enginei8.py:38 together with the code, the centre term (:62) and the casts (:67).
+ * R must be 256; d must be a multiple of 8.
+ */
+int fvs_query_code(const float *Q, int64_t B, int32_t d, const float *Vr, int32_t R, const float *c, float *z,
+                   int8_t *q8, float *qs, float *qc, uint16_t *qh, void *stream);
+
+/*
  * int8 cell-residual codes of the base set (a3). Replaces build_codes, throughput/enginei8.py:19-27.
  *   X16 fp16 [n_ids, d] in id order; order i32 [N] (sorted position -> id);
  *   cell i32 [N] (cell of each sorted position); means16 fp16 [NC, d]; Vr f32 [d, R]

@@ -57,8 +57,8 @@ static double butterfly64_d(double *lane) {
   return lane[0];
 }
 
-/* z = Q @ Vr with one sequential fmaf chain per output (the CPU baseline's own product; the GPU uses
- * its BLAS, and parity tests hand the GPU's z to or_query_prep). */
+/* z = Q @ Vr with one sequential fmaf chain per output: the order of fvs_query_code's projection (the GPU's
+ * query path) and of fvs_build_codes' residual projection, so the parity tests compare z bit for bit. */
 void or_project(const float *Q, int64_t B, int d, const float *Vr, int R, float *z) {
 #pragma omp parallel for schedule(static)
   for (int64_t q = 0; q < B; q++) project_row(Q + q * d, d, Vr, R, z + q * R);

@@ -397,8 +397,9 @@ def route(idx, QM16, nprobe, knobs):
 
 
 def pipeline(idx, Q, K, z, nprobe, k, knobs=None, QM16=None, Zq16=None, zq=None, fallback=True, QMfb16=None):
-    """Every intermediate of one batch (EngineI8._gpu + _fallback). zq (f32), QM16 / Zq16 (fp16 as uint16)
-    are the three BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs,
+    """Every intermediate of one batch (EngineI8._gpu + _fallback). zq (f32) is the projection, computed here
+    in the library's order (one sequential fmaf chain per output) unless given; QM16 / Zq16 (fp16 as uint16)
+    are the two BLAS products; when given (e.g. read back from the GPU) they are used as shared inputs,
     otherwise computed here with sequential fp32 accumulation."""
     knobs = dict(knobs or {})
     delta = knobs.get("DELTA", 0.07)

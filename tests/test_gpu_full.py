@@ -94,6 +94,11 @@ def check_i8_config(E, idx, Q, GT, oracle_mod, K, z, nprobe, k, min_recall, zs_m
     torch.cuda.synchronize()
     say(f"search done: recall@{k} {rec:.4f}, {E.nbad} flagged; oracle checks")
     q8, qs, probe, QM = npy(tr["q8"]), npy(tr["qs"]), npy(tr["probe"]), u16(tr["QM"])
+    # the canonical projection (fvs_query_code, EngineI8.CANON_Z) at this batch's full size, against the oracle
+    zc = _lib.query_prep(Q, E.Vr, E.s1["c"], canonical=True)[4]
+    torch.cuda.synchronize()
+    assert np.array_equal(npy(zc).view(np.uint32), oracle_mod.project(npy(Q), idx["Vr"]).view(np.uint32))
+    del zc
     M, n1 = tr["M"], tr["n1"]
     MB = oracle_mod.static_blocks(idx["off"])[4]
     # stage 1 on every query: block maxima, threshold, counts and the emitted sets

@@ -41,12 +41,18 @@ def env(oracle_mod):
 
 @pytest.fixture(scope="module")
 def traced(env, oracle_mod):
+    """The eager trace of one batch with the canonical projection (CANON_Z): the oracle computes z itself, so
+    everything but the two fp16 library products (QM, Zq) is checked end to end."""
     E, Q = env["E"], env["Q"]
-    tr = E.trace(Q, K, Z_, NPROBE, KK)
-    torch.cuda.synchronize()
+    E.CANON_Z = True
+    try:
+        tr = E.trace(Q, K, Z_, NPROBE, KK)
+        torch.cuda.synchronize()
+    finally:
+        E.CANON_Z = False
     tr = {k: (v.detach().cpu() if torch.is_tensor(v) else v) for k, v in tr.items()}
     out = oracle_mod.pipeline(env["idx"], npy(Q), K, Z_, NPROBE, KK, QM16=u16(tr["QM"]), Zq16=u16(tr["Zq"]),
-                              zq=npy(tr["z"]), fallback=False)
+                              fallback=False)
     return tr, out
 
 
@@ -66,12 +72,28 @@ def test_query_code_bit_exact(traced):
     assert np.array_equal(u16(tr["Qh"]), out["qh"])
 
 
-def test_blas_products_accuracy(env, traced):
-    """z: fp32 GEMM, within fp32 accumulation error of float64. QM and Zq: fp16 outputs of fp16 GEMMs,
-    within one fp16 rounding (+ fp32 accumulation) of float64."""
+def test_projection_bit_exact(env, oracle_mod, traced):
+    """With CANON_Z, z = Q @ Vr is a sequential fp32 fmaf chain over d (fvs_query_code): the oracle's
+    or_project gives the same bits. The default library GEMM's z is within fp32 accumulation error of float64,
+    and the query code derived from it matches the oracle's given that z."""
     tr, _ = traced
-    z64 = npy(env["Q"]).astype(np.float64) @ npy(env["Vr"]).astype(np.float64)
+    Q, Vr = npy(env["Q"]), npy(env["Vr"])
+    assert np.array_equal(npy(tr["z"]).view(np.uint32), oracle_mod.project(Q, Vr).view(np.uint32))
+    z64 = Q.astype(np.float64) @ Vr.astype(np.float64)
     assert np.all(np.abs(npy(tr["z"]) - z64) <= 1e-5 * np.abs(z64).max(1, keepdims=True))
+    from fanarvse_paper_amd import _lib
+
+    q8, qs, qc, qh, zb = _lib.query_prep(env["Q"], env["Vr"], env["s1"]["c"])  # the engine's default path
+    torch.cuda.synchronize()
+    assert np.all(np.abs(npy(zb) - z64) <= 1e-5 * np.abs(z64).max(1, keepdims=True))
+    o8, oqs, oqc, oqh = oracle_mod.query_prep(Q, Vr, npy(env["s1"]["c"]), npy(zb))
+    assert np.array_equal(npy(q8), o8) and np.array_equal(npy(qs).view(np.uint32), oqs.view(np.uint32))
+    assert np.array_equal(npy(qc).view(np.uint32), oqc.view(np.uint32)) and np.array_equal(u16(qh), oqh)
+
+
+def test_blas_products_accuracy(env, traced):
+    """QM and Zq: fp16 outputs of fp16 GEMMs, within one fp16 rounding (+ fp32 accumulation) of float64."""
+    tr, _ = traced
     Qh = npy(tr["Qh"]).astype(np.float64)
     E = env["E"]
     QM64 = Qh @ npy(E.meansN).astype(np.float64).T
@@ -157,17 +179,22 @@ def test_refine_and_final_ids_bit_exact(traced):
 
 
 def test_search_graph_replays_match_eager(env, traced):
+    """The captured search (with the trace's canonical projection) replayed three times gives the eager ids."""
     tr, _ = traced
     E, Q = env["E"], env["Q"]
     ok = npy(tr["ok"]).astype(bool)
-    for rep in range(3):
-        I, reads, ids = E.search(Q, K, Z_, NPROBE, KK)
-        x = torch.randn(1000, device="cuda").sum()  # eager work between replays
-        torch.cuda.synchronize()
-        assert np.array_equal(npy(I)[ok], npy(tr["I"])[ok]), f"replay {rep}"
-        assert np.array_equal(npy(reads)[ok], npy(tr["reads"])[ok])
-        assert np.array_equal(npy(ids)[ok], npy(tr["ids"])[ok])
-        del x
+    E.CANON_Z = True
+    try:
+        for rep in range(3):
+            I, reads, ids = E.search(Q, K, Z_, NPROBE, KK)
+            x = torch.randn(1000, device="cuda").sum()  # eager work between replays
+            torch.cuda.synchronize()
+            assert np.array_equal(npy(I)[ok], npy(tr["I"])[ok]), f"replay {rep}"
+            assert np.array_equal(npy(reads)[ok], npy(tr["reads"])[ok])
+            assert np.array_equal(npy(ids)[ok], npy(tr["ids"])[ok])
+            del x
+    finally:
+        E.CANON_Z = False
 
 
 def test_fallback_matches_oracle(env, oracle_mod):
