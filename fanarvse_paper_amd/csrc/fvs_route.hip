@@ -15,9 +15,10 @@
 // Pairs: instead of a global counting sort (atomics on popular cells serialise), the probe lists are
 // transposed into a cell-major rank matrix rank[c][q] (int16, -1 = not probed) in caller scratch.
 // The same pass copies each query's routing scores into a cell-major score matrix, so that the pair
-// constants are read row-wise. One wave per cell then reads its rank row once to count and its rank
-// and score rows once to compact its queries in ascending order -- the order of the reference's
-// stable sort -- with no atomics, no per-cell sort and no column gathers. The first-pass list (the
+// constants are read row-wise, and adds each tile's per-cell counts to the cell totals (one integer
+// atomic per tile and cell). After a one-block scan of the totals, one wave per cell reads its rank and
+// score rows once to compact its queries in ascending order -- the order of the reference's stable
+// sort -- with no per-pair atomics, no per-cell sort and no column gathers. The first-pass list (the
 // first n1 probe columns) and the full list come out of one matrix (fvs_pairs2).
 #include <mutex>
 
@@ -563,7 +564,8 @@ __global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__
 // c; score[c * Bp + q] = QM[q][c] (fp16 bits). One block per (64 queries, kTileC cells): the block's
 // probe entries inside its cell range are scattered into an LDS rank tile and its scores are read
 // row-wise into an LDS score tile (rows padded to 33 dwords, so neither the transposed writes nor the
-// row reads conflict on banks); both tiles are then written out as whole 128-byte rows. Probe entries
+// row reads conflict on banks); both tiles are then written out as whole 128-byte rows, and the tile's
+// number of ranks below na (nb) per cell is added to ccnt_a (ccnt_b), which start at zero. Probe entries
 // outside [0, NC) are ignored.
 constexpr int kTileQ = 64;
 constexpr int kTileC = 256;
@@ -571,7 +573,9 @@ constexpr int kTileRow = kTileQ / 2 + 1;  // dwords per padded tile row
 
 __global__ __launch_bounds__(512) void k_rank_build(const int32_t *__restrict__ probe, const uint16_t *__restrict__ QM,
                                                     int64_t B, int npr, int n, int NC, int64_t Bp,
-                                                    uint16_t *__restrict__ rank, uint16_t *__restrict__ score) {
+                                                    uint16_t *__restrict__ rank, uint16_t *__restrict__ score,
+                                                    uint32_t na, uint32_t nb, int32_t *__restrict__ ccnt_a,
+                                                    int32_t *__restrict__ ccnt_b) {
   __shared__ uint32_t rt[kTileC * kTileRow];
   __shared__ uint32_t st[kTileC * kTileRow];
   const int64_t q0 = (int64_t)blockIdx.y * kTileQ;
@@ -621,6 +625,19 @@ __global__ __launch_bounds__(512) void k_rank_build(const int32_t *__restrict__ 
     }
   }
   __syncthreads();
+  // the tile's share of each cell's counts: thread t < kTileC sums the ranks below na (and nb) in row t (the
+  // odd row pitch keeps the 64 lanes' reads on distinct banks); one atomic per cell and list adds it to the
+  // zeroed totals (integer sums: the result does not depend on their order)
+  if (tid < kTileC && c0 + tid < NC) {
+    int ma = 0, mb = 0;
+    for (int j = 0; j < kTileRow - 1; j++) {
+      const uint32_t v = rt[tid * kTileRow + j];
+      ma += ((v & 0xffffu) < na) + ((v >> 16) < na);
+      mb += ((v & 0xffffu) < nb) + ((v >> 16) < nb);
+    }
+    if (ma) atomicAdd(&ccnt_a[c0 + tid], ma);
+    if (ccnt_b && mb) atomicAdd(&ccnt_b[c0 + tid], mb);
+  }
   // out: 32 dwords per cell row, one row per 32 threads
   for (int i = tid; i < kTileC * 32; i += 512) {
     const int cc = i >> 5, j = i & 31;
@@ -643,27 +660,11 @@ __device__ __forceinline__ int below8(const uint4 v, uint32_t n) {
 
 constexpr int kCellWaves = 4;  // cells per block in the count and emit kernels (one wave per cell)
 
-// ccnt_a[c] = number of queries probing cell c within their first na columns (and ccnt_b for nb).
-template <bool TWO>
-__global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_count(const uint16_t *__restrict__ rank, int NC,
-                                                                      int64_t Bp, uint32_t na, uint32_t nb,
-                                                                      int32_t *__restrict__ ccnt_a,
-                                                                      int32_t *__restrict__ ccnt_b) {
-  const int lane = threadIdx.x & (FVS_WAVE - 1);
-  const int c = blockIdx.x * kCellWaves + fvs_wave_id();
-  if (c >= NC) return;
-  const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
-  int ma = 0, mb = 0;
-  for (int64_t i = lane; i < Bp / 8; i += FVS_WAVE) {
-    const uint4 v = rr[i];
-    ma += below8(v, na);
-    if (TWO) mb += below8(v, nb);
-  }
-  ma = wave_sum_i32(ma);
-  if (TWO) mb = wave_sum_i32(mb);
-  if (lane == 0) {
-    ccnt_a[c] = ma;
-    if (TWO) ccnt_b[c] = mb;
+// ccnt_a[0, NC) = 0 (and ccnt_b): the totals k_rank_build adds its tiles' counts to.
+__global__ __launch_bounds__(256) void k_cell_zero(int32_t *__restrict__ ccnt_a, int32_t *__restrict__ ccnt_b, int NC) {
+  for (int c = blockIdx.x * 256 + threadIdx.x; c < NC; c += gridDim.x * 256) {
+    ccnt_a[c] = 0;
+    if (ccnt_b) ccnt_b[c] = 0;
   }
 }
 
@@ -866,23 +867,23 @@ int pairs_impl(const int32_t *probe, int64_t B, int npr, int NC, const uint16_t 
   uint16_t *score = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(scratch) + matrix_bytes(B, NC));
   const int n = (int)max(la.n, lb ? lb->n : 0u);
   int e;
+  hipLaunchKernelGGL(k_cell_zero, dim3((unsigned)((NC + 255) / 256)), dim3(256), 0, st, ccnt_a, lb ? ccnt_b : nullptr,
+                     NC);
+  if ((e = fvs_launch_status())) return e;
   if (B > 0) {
     const dim3 grid((unsigned)((NC + kTileC - 1) / kTileC), (unsigned)(Bp / kTileQ));
-    hipLaunchKernelGGL(k_rank_build, grid, dim3(512), 0, st, probe, QM, B, npr, n, NC, Bp, rank, score);
+    hipLaunchKernelGGL(k_rank_build, grid, dim3(512), 0, st, probe, QM, B, npr, n, NC, Bp, rank, score, la.n,
+                       lb ? lb->n : 0u, ccnt_a, lb ? ccnt_b : nullptr);
     if ((e = fvs_launch_status())) return e;
   }
   const unsigned cg = (unsigned)((NC + kCellWaves - 1) / kCellWaves);
   const dim3 cb(kCellWaves * FVS_WAVE);
   if (lb) {
-    hipLaunchKernelGGL(k_cell_count<true>, dim3(cg), cb, 0, st, rank, NC, Bp, la.n, lb->n, ccnt_a, ccnt_b);
-    if ((e = fvs_launch_status())) return e;
     hipLaunchKernelGGL(k_cell_scan, dim3(2), dim3(1024), 0, st, ccnt_a, const_cast<int32_t *>(la.coff), ccnt_b,
                        const_cast<int32_t *>(lb->coff), NC);
     if ((e = fvs_launch_status())) return e;
     hipLaunchKernelGGL(k_cell_emit<true>, dim3(cg), cb, 0, st, rank, score, Bp, mnorm, qadd, NC, la, *lb);
   } else {
-    hipLaunchKernelGGL(k_cell_count<false>, dim3(cg), cb, 0, st, rank, NC, Bp, la.n, 0u, ccnt_a, ccnt_a);
-    if ((e = fvs_launch_status())) return e;
     hipLaunchKernelGGL(k_cell_scan, dim3(1), dim3(1024), 0, st, ccnt_a, const_cast<int32_t *>(la.coff), ccnt_a,
                        const_cast<int32_t *>(la.coff), NC);
     if ((e = fvs_launch_status())) return e;
