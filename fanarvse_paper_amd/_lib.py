@@ -282,8 +282,8 @@ def pairs2(probe, n1, NC, QM, mnorm, scratch=None, qadd=None):
 def i8_scan(mode, blocks, q8, qs, pr, Z, zs, t0=None, cnt=None, bval=None, bpos=None, bm=None, CAP=1, MB=1, n1=1):
     """First pass (mode 0) or emit (mode 1) over the stage-1 work items (throughput/civf8.py:89-91).
 
-    `blocks` = (cell, first row, cell start, cell end): index.static_chunks for mode 0 (items of eight global
-    32-row blocks), items of at most 128 rows for mode 1 (index.row_chunks(off, 128), or static_chunks with
+    `blocks` = (cell, first row, cell start, cell end): index.static_chunks(off, 32, 4) for mode 0 (items of four
+    global 32-row blocks), items of at most 128 rows for mode 1 (index.row_chunks(off, 128), or static_chunks with
     CB = 4), over the same index as Z (its rows lie
     inside Z); no host synchronisation happens here, so the call can be captured in a graph."""
     pcell, prow, ps, pe = blocks

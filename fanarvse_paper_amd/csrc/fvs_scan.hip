@@ -1,15 +1,15 @@
-// int8 stage-1 scans on gfx950 MFMA: the first pass (block maxima, v_mfma_i32_32x32x32_i8) and the
-// threshold-and-emit pass (v_mfma_i32_16x16x64_i8).
+// int8 stage-1 scans on gfx950 MFMA (v_mfma_i32_16x16x64_i8): the first pass (block maxima) and the
+// threshold-and-emit pass.
 //
-// Work item = (cell, up to 256 consecutive rows of it from a first row r0); its 32-row blocks start at
-// r0, r0 + 32, ... The first pass needs the reference's global 32-row blocks (its block maxima are per
-// global block), so its items start on a multiple of 32; the emit pass, whose output does not depend on
-// the grouping, takes items that start at the cell's first row (a cell of up to 256 rows is one item,
-// with no block straddling the cell start). Each code byte is read from HBM once per pass: a wave keeps
-// its 64 code rows as MFMA operands in registers for the whole item (first pass) or half item (emit),
-// and the cell's queries stream through in tiles:
+// Work item = (cell, up to 128 consecutive rows of it from a first row r0), run by a workgroup of two waves,
+// each wave holding 64 of the rows as four 16-row blocks. The first pass needs the reference's global
+// 32-row blocks (its block maxima are per global block), so its items start on a multiple of 32; the emit
+// pass, whose output does not depend on the grouping, takes items that start at the cell's first row (a
+// cell of up to 128 rows is one item, with no block straddling the cell start). Each code byte is read from
+// HBM once per pass: a wave keeps its code rows as MFMA operands in registers for the whole item, and the
+// cell's queries stream through in tiles of 16:
 //   * the item's pair list (query id, query scale, centre term, threshold or probe rank) and the row
-//     scales of its rows are staged in LDS up front (kMeta / kMetaE pairs at a time);
+//     scales of its rows are staged in LDS up front (kFMeta / kMetaE pairs at a time);
 //   * a tile's query fragments are written straight into LDS by the vector memory unit (global_load_lds,
 //     no registers), in MFMA-step order so that every fragment read is one contiguous 1 KB ds_read_b128 per
 //     wave. The buffer is double-buffered and shared by the workgroup's waves: each wave requests its share
@@ -17,13 +17,15 @@
 // Both passes are persistent: a workgroup loops over items (grid = resident workgroups), and the next
 // item's pair ids, row scales and code rows are requested as soon as the current item's tile loop is done.
 //
-// The first pass's operand layout (32 x 32 x 32): lane l holds row/column (l & 31) and, for MFMA step s
-// (k-block of 32 bytes), the 16 bytes at 32*s + 16*(l >> 5); both operands use the same assignment, so
-// the contraction is exact for any internal k order. Accumulator layout (D = A x B): lane l, element v
-// holds row 8*(v/4) + 4*(l/32) + (v%4) of A and column l%32 of B.
+// Operand layout (16 x 16 x 64): for MFMA step s (64 bytes of the code), lane l holds the 16 bytes at
+// 64 s + 16 (l >> 4) of row / column l & 15; both operands use the same assignment, so the contraction is
+// exact for any internal k order. Accumulator element i of lane l is D[4 (l >> 4) + i][l & 15].
 //
 // The item's row scales sit in LDS; rows outside the cell get a NaN scale: their estimate is NaN,
 // which never passes `est >= t0` and is ignored by fmaxf, so no per-element row mask is needed.
+//
+// The reference-signature seam (fvs_i8_scan_civf8, k_i8_civf8 at the end of this file) keeps its own
+// one-block items on v_mfma_i32_32x32x32_i8.
 #include <type_traits>
 
 #include "fvs_common.h"
@@ -31,9 +33,6 @@
 namespace {
 
 constexpr int kR = 256;
-constexpr int kNB = 2;          // 32-row blocks per wave
-constexpr int kCB = 4 * kNB;    // 32-row blocks per work item
-constexpr int kMeta = 512;      // pairs staged in LDS at a time (first pass)
 
 // row of accumulator element v in the 32x32 layout, for lanes of half h = l / 32
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
@@ -46,64 +45,73 @@ struct Meta {  // one (query, cell) pair of the item
 };
 
 // ------------------------------------------------------------------ the first pass (mode 0)
-// A 4-wave workgroup runs an item: wave w keeps blocks 2w and 2w + 1 (two blocks per wave halve the
-// fragment reads per MFMA), and the queries come in tiles of 32 (8 KB), each wave requesting a quarter.
-// The code rows are the A operand and the queries the B operand, so each lane owns one query (column
-// l % 32) and 16 rows of a block; the epilogue needs only per-lane scalars for the query:
-//   bm[(q * n1 + qrank[pair]) * MB + blk - cs/32] = max over the block's rows of
-//   fmaf((float)acc * qs, zs, qcp).
-// Three workgroups per CU (at most 168 VGPRs, 25 KB of LDS).
-__global__ __launch_bounds__(256, 3) void k_i8_first(
+// A two-wave workgroup runs an item of up to four global 32-row blocks (128 rows from a multiple of 32):
+// wave w keeps global blocks 2w and 2w + 1 as four 16-row blocks of v_mfma_i32_16x16x64_i8 A operands (the
+// code rows; 64 VGPRs), and the cell's queries are the B operand, in tiles of 16 (4 KB, each wave requesting
+// two of the four MFMA steps). Accumulator element i of lane l is row 4 (l >> 4) + i of the 16-row block
+// against query l & 15 of the tile, so a lane reduces the 8 rows it holds of a global block in registers and
+// two xor exchanges (lanes 16 and 32 apart) finish the block maximum of its query:
+//   bm[(q * n1 + qrank[pair]) * MB + blk - cs/32] = max over the block's rows of fmaf((float)acc * qs, zs, qcp).
+// Eight workgroups (sixteen waves) per CU: at most 128 VGPRs and 12.5 KB of LDS each. Against four-wave
+// workgroups on 256-row items (three per CU) the scan has twice as many waves in flight to hide each item's
+// dependent loads (its pair ids, their query scales, the first query tile), which is what bounds it.
+constexpr int kFW = 2;            // waves per first-pass workgroup
+constexpr int kFT = 64 * kFW;     // threads per first-pass workgroup
+constexpr int kFRows = 64 * kFW;  // rows of a first-pass item
+constexpr int kFMeta = 256;       // pairs staged in LDS at a time
+constexpr int kFirstWG = 8;       // resident first-pass workgroups per CU
+
+__global__ __launch_bounds__(kFT, 4) void k_i8_first(
     const int8_t *__restrict__ q8, const float *__restrict__ qs, const int32_t *__restrict__ qid,
     const int32_t *__restrict__ qrank, const int32_t *__restrict__ coff, const int32_t *__restrict__ ccnt,
     const int32_t *__restrict__ pcell, const int32_t *__restrict__ prow, const int32_t *__restrict__ ps,
-    const int32_t *__restrict__ pe, int P, const int8_t *__restrict__ Z, const float *__restrict__ zs, int64_t N,
+    const int32_t *__restrict__ pe, int P, const int8_t *__restrict__ Z, const float *__restrict__ zs,
     const float *__restrict__ qcp, float *__restrict__ bm, int MB, int n1) {
-  __shared__ __align__(16) Meta meta[kMeta];
-  __shared__ __align__(16) float zsl[32 * kCB];
-  __shared__ __align__(16) v4i bsh[2][8 * 64];  // query tiles, double-buffered: [step s][half h][query li], 16 B each
+  __shared__ __align__(16) Meta meta[kFMeta];
+  __shared__ __align__(16) float zsl[kFRows];
+  __shared__ __align__(16) v4i bsh[2][4 * 64];  // query tiles: [step s][lane], 16 B each
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = fvs_wave_id();
-  const int h = lane >> 5, li = lane & 31;
-
+  const int g4 = lane >> 4, l16 = lane & 15;
   struct Item {
-    int c, qn, qoff, r0, cs, ce;  // r0: first row of the item
+    int qn, qoff, r0, cs, ce;
   };
   auto item_at = [&](int p) {
-    Item it{0, 0, 0, 0, 0, 0};
+    Item u{0, 0, 0, 0, 0};
     if (p < P) {
-      it.c = pcell[p];
-      it.r0 = prow[p];
-      it.cs = ps[p];
-      it.ce = pe[p];
-      it.qn = ccnt[it.c];
-      it.qoff = coff[it.c];
+      const int c = pcell[p];
+      u.r0 = prow[p];
+      u.cs = ps[p];
+      u.ce = min(u.r0 + kFRows, pe[p]);
+      if (u.r0 < u.ce) {
+        u.qn = ccnt[c];
+        u.qoff = coff[c];
+      }
     }
-    return it;
+    return u;
   };
-  int pq[kMeta / 256];  // pair ids of the item's first chunk
-  float zr = 0.f;       // this thread's row scale of the item
-  v4i a[kNB][8];        // this wave's blocks: the A operands
-  auto prefetch = [&](const Item &it) {
-    if (it.qn == 0) return;
+  int pq[kFMeta / kFT];
+  float zr;
+  v4i cb[4][4];  // this wave's code rows: 16-row block b, MFMA step s
+  auto prefetch = [&](const Item &u) {
+    if (u.qn == 0) return;
 #pragma unroll
-    for (int i = 0; i < kMeta / 256; i++) {
-      const int j = tid + 256 * i;
-      pq[i] = j < min(kMeta, it.qn) ? qid[it.qoff + j] : 0;
+    for (int i = 0; i < kFMeta / kFT; i++) {
+      const int j = tid + kFT * i;
+      pq[i] = j < min(kFMeta, u.qn) ? qid[u.qoff + j] : 0;
     }
     {
-      const int r = it.r0 + tid;
-      zr = (r >= it.cs && r < it.ce) ? zs[r] : __builtin_nanf("");
+      const int r = u.r0 + tid;
+      zr = (r >= u.cs && r < u.ce) ? zs[r] : __builtin_nanf("");
     }
 #pragma unroll
-    for (int u = 0; u < kNB; u++) {
-      const int b0 = it.r0 + 32 * (kNB * w + u);  // first row of the block
-      int64_t zr_ = (int64_t)b0 + li;
-      if (b0 >= it.ce || zr_ > N - 1) zr_ = N - 1;  // rows past the cell carry a NaN scale
-      const v4i *zp = reinterpret_cast<const v4i *>(Z + zr_ * kR + h * 16);
+    for (int b = 0; b < 4; b++) {
+      const int r = u.r0 + 64 * w + 16 * b + l16;
+      const int64_t rr = r < u.ce ? r : u.ce - 1;  // rows past the cell carry a NaN scale
+      const v4i *zp = reinterpret_cast<const v4i *>(Z + rr * kR + 16 * g4);
 #pragma unroll
-      for (int s = 0; s < 8; s++) a[u][s] = zp[2 * s];
+      for (int s = 0; s < 4; s++) cb[b][s] = zp[4 * s];
     }
   };
 
@@ -119,25 +127,22 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
       p += stride;
       continue;
     }
-    const int qn = cur.qn, qoff = cur.qoff, cs = cur.cs;
-    const int row0 = cur.r0;  // first row of the item
+    const int qn = cur.qn, qoff = cur.qoff, cs = cur.cs, row0 = cur.r0;
     zsl[tid] = zr;
-    bool act[kNB];
-#pragma unroll
-    for (int u = 0; u < kNB; u++) act[u] = row0 + 32 * (kNB * w + u) < cur.ce;
-    const bool any = act[0];
-    for (int c0 = 0; c0 < qn; c0 += kMeta) {
-      const int nq = min(kMeta, qn - c0);
+    const int wrows = cur.ce - row0 - 64 * w;
+    const int nact = wrows <= 0 ? 0 : min(4, (wrows + 15) >> 4);  // 16-row blocks with rows of the cell
+    for (int c0 = 0; c0 < qn; c0 += kFMeta) {
+      const int nq = min(kFMeta, qn - c0);
       if (c0 > 0) {
 #pragma unroll
-        for (int i = 0; i < kMeta / 256; i++) {
-          const int j = tid + 256 * i;
+        for (int i = 0; i < kFMeta / kFT; i++) {
+          const int j = tid + kFT * i;
           pq[i] = j < nq ? qid[qoff + c0 + j] : 0;
         }
       }
 #pragma unroll
-      for (int i = 0; i < kMeta / 256; i++) {
-        const int j = tid + 256 * i;
+      for (int i = 0; i < kFMeta / kFT; i++) {
+        const int j = tid + kFT * i;
         if (j < nq) {
           const int pidx = qoff + c0 + j;
           const int q = pq[i];
@@ -150,62 +155,71 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
         }
       }
       __syncthreads();
-      const int ntiles = (nq + 31) / 32;
-      // tile t: the fragments of its 32 queries in MFMA step order, written straight into LDS; wave w
-      // requests steps 2w and 2w + 1 of tile t + 1 while tile t is computed
+      const int ntiles = (nq + 15) / 16;
       auto request = [&](int tile) {
-        const int jr = min(tile * 32 + li, nq - 1);
-        const int8_t *src = q8 + (int64_t)meta[jr].qid * kR + h * 16;
+        const int8_t *src = q8 + (int64_t)meta[min(tile * 16 + l16, nq - 1)].qid * kR + 16 * g4;
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-          const int s = 2 * w + k;
-          __builtin_amdgcn_global_load_lds(src + 32 * s, (__attribute__((address_space(3))) void *)&bsh[tile & 1][s * 64],
+        for (int i = 0; i < 4 / kFW; i++) {
+          const int s = (4 / kFW) * w + i;
+          __builtin_amdgcn_global_load_lds(src + 64 * s, (__attribute__((address_space(3))) void *)&bsh[tile & 1][s * 64],
                                            16, 0, 0);
         }
       };
       auto published = [&]() {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's requests have landed in LDS
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       };
-      auto compute = [&](int t) {
-        v4i b[8];
+      auto tiles = [&](auto NB_) {
+        constexpr int NB = decltype(NB_)::value;
+        for (int t = 0; t < ntiles; t++) {
+          if (t + 1 < ntiles) request(t + 1);
+          v4i qb[4];
 #pragma unroll
-        for (int s = 0; s < 8; s++) b[s] = bsh[t & 1][s * 64 + lane];
-        v16i acc[kNB];
+          for (int s = 0; s < 4; s++) qb[s] = bsh[t & 1][s * 64 + lane];
+          v4i A[NB];
 #pragma unroll
-        for (int u = 0; u < kNB; u++) {
-          acc[u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-          if (act[u]) {
+          for (int s = 0; s < 4; s++)
 #pragma unroll
-            for (int s = 0; s < 8; s++) acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u][s], b[s], acc[u], 0, 0, 0);
+            for (int b = 0; b < NB; b++)
+              A[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cb[b][s], qb[s], s == 0 ? (v4i){0, 0, 0, 0} : A[b], 0, 0, 0);
+          const int jl = t * 16 + l16;
+          const bool valid = jl < nq;
+          const Meta m = meta[valid ? jl : nq - 1];
+#pragma unroll
+          for (int gb = 0; gb < (NB + 1) / 2; gb++) {
+            float mx = -1e30f;
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++) {
+              const int b = 2 * gb + bb;
+              if (b < NB) {
+                const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[64 * w + 16 * b + 4 * g4]);
+                const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_fmaf((float)A[b][i] * m.qs, zz[i], m.qcp));
+              }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, FVS_WAVE));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
+            if (g4 == 0 && valid)
+              bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + 2 * w + gb - (cs >> 5))] = mx;
           }
-        }
-        const int jl = t * 32 + li;  // pair index inside the chunk
-        const bool valid = jl < nq;
-        const Meta m = meta[valid ? jl : nq - 1];
-#pragma unroll
-        for (int u = 0; u < kNB; u++) {
-          if (!act[u]) continue;
-          float mx = -1e30f;
-#pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const float4 z4 = *reinterpret_cast<const float4 *>(&zsl[32 * (kNB * w + u) + 8 * g + 4 * h]);
-            const float zz[4] = {z4.x, z4.y, z4.z, z4.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_fmaf((float)acc[u][4 * g + i] * m.qs, zz[i], m.qcp));
-          }
-          mx = fmaxf(mx, __shfl_xor(mx, 32, FVS_WAVE));
-          if (h == 0 && valid)
-            bm[((int64_t)m.qid * n1 + __float_as_int(m.x)) * MB + ((row0 >> 5) + kNB * w + u - (cs >> 5))] = mx;
+          published();
         }
       };
       request(0);
       published();
-      for (int t = 0; t < ntiles; t++) {
-        if (t + 1 < ntiles) request(t + 1);  // the other buffer: every wave has left tile t - 1
-        if (any) compute(t);
-        published();
+      switch (nact) {
+        case 4: tiles(std::integral_constant<int, 4>{}); break;
+        case 3: tiles(std::integral_constant<int, 3>{}); break;
+        case 2: tiles(std::integral_constant<int, 2>{}); break;
+        case 1: tiles(std::integral_constant<int, 1>{}); break;
+        default:
+          for (int t = 0; t < ntiles; t++) {
+            if (t + 1 < ntiles) request(t + 1);
+            published();
+          }
       }
+      __syncthreads();  // every wave is past meta before the next chunk restages it
     }
     prefetch(nxt);
     cur = nxt;
@@ -214,8 +228,8 @@ __global__ __launch_bounds__(256, 3) void k_i8_first(
 }
 
 // ------------------------------------------------------------------ the emit pass (mode 1)
-// The emit pass runs on smaller items than the first pass: a workgroup of two waves takes a cell and up to 128
-// of its rows (64 per wave, as four 16-row blocks), and the cell's queries in tiles of 16, on
+// The emit pass has the first pass's shape with the operands swapped: a workgroup of two waves takes a cell
+// and up to 128 of its rows (64 per wave, as four 16-row blocks), and the cell's queries in tiles of 16, on
 // v_mfma_i32_16x16x64_i8. Cells are skewed (a tenth hold under 16 rows), so 128-row items leave few waves
 // without rows (about 4 % of the wave-steps, against 28 % for four-wave items of 256 rows), and 16-row
 // blocks leave few empty rows in the blocks that are computed. The persistent grid walks the items in list
@@ -691,11 +705,11 @@ extern "C" int fvs_i8_scan(int32_t mode, int32_t P, const int8_t *q8, const floa
   if (P == 0) return FVS_OK;
   if (!q8 || !qs || !qid || !coff || !ccnt || !pcell || !prow || !ps || !pe || !Z || !zs || !qcp) return FVS_E_ARG;
   hipStream_t st = (hipStream_t)stream;
-  // persistent grids: three first-pass workgroups, six emit workgroups per CU
+  // persistent grids: eight first-pass workgroups, six emit workgroups per CU
   if (mode == 0) {
     if (!qrank || !bm || MB <= 0 || n1 <= 0) return FVS_E_ARG;
-    hipLaunchKernelGGL(k_i8_first, dim3((unsigned)min(P, 3 * fvs_cu_count())), dim3(256), 0, st, q8, qs, qid, qrank,
-                       coff, ccnt, pcell, prow, ps, pe, P, Z, zs, N, qcp, bm, MB, n1);
+    hipLaunchKernelGGL(k_i8_first, dim3((unsigned)min(P, kFirstWG * fvs_cu_count())), dim3(kFT), 0, st, q8, qs, qid,
+                       qrank, coff, ccnt, pcell, prow, ps, pe, P, Z, zs, qcp, bm, MB, n1);
   } else {
     if (!t0 || !cnt || !bval || !bpos || CAP <= 0) return FVS_E_ARG;
     hipLaunchKernelGGL(k_i8_emit, dim3((unsigned)min(P, kEmitWG * fvs_cu_count())), dim3(kET), 0, st, q8, qs,

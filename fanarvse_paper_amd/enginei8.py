@@ -90,7 +90,7 @@ class EngineI8:
     NROUTE = True
     DELTA = 0.07
     LUTH = True
-    CB = 8  # 32-row blocks per first-pass work item
+    CB = 4  # 32-row blocks per first-pass work item (the first-pass kernel's item span)
     EROWS = 128  # rows per emit work item (the emit kernel's item span)
     NINST = 3  # graph instances per search shape: batches that submit / collect keep in flight
     # the projection z = Qb @ Vr of the query code: False, the fp32 library GEMM (as the reference's cuBLAS

@@ -155,9 +155,9 @@ def static_blocks(off_t, BN=32):
     return (i32(cell), i32(blk), i32(s[cell]), i32(e[cell])), MB
 
 
-def static_chunks(off_t, BN=32, CB=8):
+def static_chunks(off_t, BN=32, CB=4):
     """Work items of the first pass: every cell's static blocks (static_blocks) grouped into chunks of up
-    to CB consecutive global blocks. Returns (cell, first row = BN * first global block, cell start, cell
+    to CB consecutive global blocks (the first-pass kernel's items span four). Returns (cell, first row = BN * first global block, cell start, cell
     end) int32 tensors; each item covers blocks [blk0, min(blk0 + CB, last block of the cell + 1))."""
     off = off_t.long()
     s, e = off[:-1], off[1:]

@@ -186,9 +186,10 @@ int fvs_i8_scan_civf8(int32_t mode, int32_t P, const int8_t *q8, const float *qs
  * emitted sets; throughput/civf8.py:89-91, throughput/ivf8c_kern.py:2-36), plus qrank/n1 so that the first
  * pass writes each query's block maxima straight into its own row.
  *   Work item p < P: a cell and consecutive rows of it (pcell, prow, ps, pe: the cell, the item's first
- *   row, and the cell's first and end row). Mode 0: the item covers rows [max(prow, ps), min(prow + 256,
- *   pe)) as eight 32-row blocks starting at prow; prow is a multiple of 32 and the items cover each static
- *   (cell, global 32-row block) of the reference's work list (src/s1cell.py:161-168) exactly once.
+ *   row, and the cell's first and end row). Mode 0: the item covers rows [max(prow, ps), min(prow + 128,
+ *   pe)) as four 32-row blocks starting at prow; prow is a multiple of 32 and the items cover each static
+ *   (cell, global 32-row block) of the reference's work list (src/s1cell.py:161-168) exactly once
+ *   (index.static_chunks(off, 32, 4)).
  *   Mode 1: the item covers rows [max(prow, ps), min(prow + 128, pe)) (128 rows at most, as eight 16-row
  *   blocks from prow); the items cover each row of each cell exactly once (any grouping; prow = ps + 128 j,
  *   index.row_chunks(off, 128), is the one that wastes least). For every query q of the cell's pair list:
