@@ -568,7 +568,7 @@ __global__ __launch_bounds__(256) void k_route_topk(const uint16_t *__restrict__
 // number of ranks below na (nb) per cell is added to ccnt_a (ccnt_b), which start at zero. Probe entries
 // outside [0, NC) are ignored.
 constexpr int kTileQ = 64;
-constexpr int kTileC = 256;
+constexpr int kTileC = 128;  // 33 KB of LDS per block, so blocks fit beside the scans of other batches
 constexpr int kTileRow = kTileQ / 2 + 1;  // dwords per padded tile row
 
 __global__ __launch_bounds__(512) void k_rank_build(const int32_t *__restrict__ probe, const uint16_t *__restrict__ QM,
