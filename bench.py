@@ -349,6 +349,11 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
     cal2 = torch.empty_like(cal)
     t_copy = _time_launch(lambda: cal2.copy_(cal), reps, torch)
     del cal, cal2
+    # the achievable int8 matrix-core rate: four waves per SIMD of register-only MFMA chains
+    mf_blocks, mf_iters = 4 * torch.cuda.get_device_properties(Q.device).multi_processor_count, 2048
+    mf_out = torch.empty(4 * mf_blocks, dtype=torch.int32, device=Q.device)
+    t_mfma = _time_launch(lambda: _lib.calib_mfma(mf_out, mf_iters), reps, torch)
+    mfma_tops = 4.0 * mf_blocks * mf_iters * 16 * (2 * 16 * 16 * 64) / (t_mfma * 1e-3) / 1e12
     # algorithmic work
     off = s1["off_t"].long()
     sizes = (off[1:] - off[:-1])
@@ -378,6 +383,9 @@ def kernel_roofline(E, Q, K, args, nprobe, torch, np, _lib):
                    "hbm_frac": round(gbs(ref_bytes, t_ref) / HBM_PEAK_GBS, 4)},
         "copy_calibration": {"ms": round(t_copy, 4), "bytes": 2.0 * CAL_BYTES,
                              "GBps": round(gbs(2.0 * CAL_BYTES, t_copy), 1)},
+        "mfma_calibration": {"ms": round(t_mfma, 4), "int8_TOPS": round(mfma_tops, 1),
+                             "frac_of_peak": round(mfma_tops / INT8_PEAK_TOPS, 4),
+                             "emit_frac_of_measured": round(emit_tops / mfma_tops, 4)},
     }
     # the binding roofline of the emit scan: the larger of its MFMA and HBM time floors
     if ops_emit / (INT8_PEAK_TOPS * 1e12) >= code_bytes_emit / (HBM_PEAK_GBS * 1e9):

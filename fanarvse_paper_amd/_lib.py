@@ -25,6 +25,7 @@ SIGNATURES = {
     "fvs_abi_version": [],
     "fvs_error_string": [ctypes.c_int],
     "fvs_fill_u32": [P, I64, U32, P],
+    "fvs_calib_mfma": [I32, I32, P, P],
     "fvs_pack_ids": [P, P, I64, I32, P, P],
     "fvs_dense_small": [P, I64, I32, P, I32, P, P, I32, P, P, I32, P, P, P, P],
     "fvs_query_prep": [P, I64, I32, P, I32, P, P, P, P, P, P],
@@ -119,6 +120,15 @@ def fill_u32(t, value):
     if t.element_size() != 4:
         raise TypeError("fill_u32: 32-bit tensor expected")
     _check(lib().fvs_fill_u32(_dev(t, t.dtype, "dst"), t.numel(), U32(value), _stream()), "fvs_fill_u32")
+
+
+def calib_mfma(out, iters):
+    """The matrix-core calibration kernel: len(out) / 4 workgroups, `iters` rounds of sixteen MFMAs (four 4-step
+    chains) per wave (2 * 16 * 16 * 16 * 64 int8 ops per wave and round); out int32 [4 * workgroups] receives the
+    checksums."""
+    if out.numel() % 4 != 0:
+        raise ValueError("calib_mfma: out holds four checksums per workgroup")
+    _check(lib().fvs_calib_mfma(out.numel() // 4, iters, _dev(out, torch.int32, "out"), _stream()), "fvs_calib_mfma")
 
 
 def pack_ids(ok, I, out):

@@ -46,6 +46,12 @@ const char *fvs_error_string(int code);
 /* Fill n 32-bit words with `value` (graph-capturable replacement for hipMemsetAsync). */
 int fvs_fill_u32(void *dst, int64_t n, uint32_t value, void *stream);
 
+/* Matrix-core calibration (no reference counterpart: the achievable-peak measurement that bench.py reports
+ * beside the published one). `blocks` workgroups of 256 threads; every wave runs `iters` rounds of four
+ * independent 4-step v_mfma_i32_16x16x64_i8 chains on register operands (2 * 16 * 16 * 16 * 64 int8 ops per
+ * round) and writes one checksum to out[wave] (out holds blocks * 4 int32). */
+int fvs_calib_mfma(int32_t blocks, int32_t iters, int32_t *out, void *stream);
+
 /*
  * The latency path's host result in one launch: out i64 [B, k+1] = [ok[q] | I[q][0..k)] (ok u8 [B],
  * I i32 [B, k]). out may be pinned host memory: the launch writes it directly, and the values are

@@ -79,6 +79,9 @@ def test_argument_checks_need_no_gpu(L):
     assert L.fvs_dense_threshold(n, 4, 10, 11, n, n, n) == E_ARG                                 # r > n
     assert L.fvs_dense_threshold(n, 4, 10, 0, n, n, n) == E_ARG                                  # r = 0
     assert L.fvs_quantize_i8(n, 4, 0, n, n, n, n) == E_ARG                                       # R = 0
+    assert L.fvs_calib_mfma(0, 16, n, n) == E_ARG                                                # no workgroups
+    assert L.fvs_calib_mfma(4, 0, n, n) == E_ARG                                                 # no rounds
+    assert L.fvs_calib_mfma(4, 16, n, n) == E_ARG                                                # no output
 
 
 def test_lut_score_layout_checks_need_no_gpu(L):
