@@ -165,7 +165,7 @@ def main():
 
     # ---- the same point over distinct batches (no batch is replayed, so no cross-step cache reuse of its
     # candidates' refine rows); throughput/e_dup.py:7-13 measures the duplicate-batch effect the same way
-    ndist = 30
+    ndist = 100  # enough that the three-deep pipeline's fill and drain weigh about 2 %
     distinct = [datagen.gen(args.batch, args.d, args.clusters, 0.7, seed=100 + i, device=dev, dtype=torch.float32)
                 for i in range(ndist)]
     # the fallback graphs of 1..64 flagged rows are captured ahead (a capture takes tens of ms, as a serving
