@@ -1,4 +1,4 @@
-"""SpaceX on MI355X: the host-resident default engine (host_resident/space_x.py:13-78, SURVEY config 5).
+"""SpaceX on MI355X: the host-resident default engine (host_resident/space_x.py:13-78, benchmark config 5).
 
 Every per-vector array lives in pinned host memory: the trellis words and scales, the packed stage-2
 records, and the fp16 rows (kept in sorted order, so no id table is needed on the GPU; ids are mapped

@@ -1,4 +1,4 @@
-"""Bitshift-trellis cell-residual codes of the default engine (latency mode, SURVEY config 3).
+"""Bitshift-trellis cell-residual codes of the default engine (latency mode, benchmark config 3).
 
 A vector's stage-1 code is the Viterbi path of its normalised cell residual through a 2^L-state
 bitshift trellis with one bit per coordinate: the stream holds the L bits of the first state and then
