@@ -377,8 +377,11 @@ __global__ __launch_bounds__(kET, 3) void k_i8_emit(
       const int ntiles = (nq + kTQ - 1) / kTQ;
       // tile t's fragments go to bsh0 (t even) or bsh1 (t odd): global_load_lds, 16 B per lane; wave w
       // requests steps 2w and 2w + 1
-      auto request = [&](int tile, v4i *buf) {
-        const int8_t *src = q8 + (int64_t)meta[min(tile * kTQ + l16, nq - 1)].qid * kR + 16 * g4;
+      // this lane's query in a tile; the tile loop reads it from LDS one tile ahead of the request, so the
+      // LDS read is off the critical path of the request
+      auto tile_q = [&](int tile) { return meta[min(tile * kTQ + l16, nq - 1)].qid; };
+      auto request = [&](int q, v4i *buf) {
+        const int8_t *src = q8 + (int64_t)q * kR + 16 * g4;
 #pragma unroll
         for (int i = 0; i < 4 / kEW; i++) {
           const int s = (4 / kEW) * w + i;
@@ -405,9 +408,11 @@ __global__ __launch_bounds__(kET, 3) void k_i8_emit(
       auto tiles = [&](auto NB_) {
         constexpr int NB = decltype(NB_)::value;
         v4i qa[4];
+        int qn1 = tile_q(1);  // this lane's query of tile t + 1
         for (int t = 0; t < ntiles; t++) {
           const v4i *cur_t = (t & 1) ? bsh1 : bsh0;
-          if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
+          if (t + 1 < ntiles) request(qn1, (t & 1) ? bsh0 : bsh1);
+          qn1 = tile_q(t + 2);
 #pragma unroll
           for (int s = 0; s < 4; s++) qa[s] = cur_t[s * 64 + lane];
           v4i A[NB];
@@ -456,7 +461,7 @@ __global__ __launch_bounds__(kET, 3) void k_i8_emit(
           published();
         }
       };
-      request(0, bsh0);
+      request(tile_q(0), bsh0);
       published();
       switch (nact) {
         case 4: tiles(std::integral_constant<int, 4>{}); break;
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(kET, 3) void k_i8_emit(
         case 1: tiles(std::integral_constant<int, 1>{}); break;
         default:  // a wave without rows of the cell: the same barriers and requests, no compute
           for (int t = 0; t < ntiles; t++) {
-            if (t + 1 < ntiles) request(t + 1, (t & 1) ? bsh0 : bsh1);
+            if (t + 1 < ntiles) request(tile_q(t + 1), (t & 1) ? bsh0 : bsh1);
             published();
           }
       }
