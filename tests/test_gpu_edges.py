@@ -130,8 +130,9 @@ def coarse(oracle_mod):
 
 
 def test_cells_beyond_staged_query_limit(coarse, oracle_mod):
-    """1,500 queries probing 16 of 32 cells: the hottest cells are probed by more than the 1,024 queries
-    the staged emit holds, so they take the direct path (one global atomic per candidate)."""
+    """1,500 queries probing 16 of 32 cells: the hottest cells are probed by more than 1,024 queries, so both
+    passes stage their pairs in several chunks (256 at a time), and n1 covers every probe here, so the first
+    pass's chunk loop runs too."""
     print("\n[gpu edges] hot cells: B=1500 nprobe=16", flush=True)
     Q = datagen.gen(1500, 768, 8, 0.7, seed=13, device="cuda", dtype=torch.float32)
     E = coarse["E"]
