@@ -1,5 +1,5 @@
 """Edge cases of both engines against the CPU oracle, bit for bit: the throughput engine at batch sizes
-that leave partial 32-query tiles or a single query (1, 3, 33, 257); an index with many empty and tiny
+that leave partial query tiles or a single query (1, 3, 33, 257); an index with many empty and tiny
 cells (3,000 vectors over 512 cells, so most probed cells hold a few rows or none); and a dimension
 (d = 384) other than the configurations'. The three dense products come from the GPU's BLAS and are
 shared inputs of the oracle, as in the other parity tests."""
@@ -144,8 +144,9 @@ def test_cells_beyond_staged_query_limit(coarse, oracle_mod):
 
 def test_emit_region_overflow(coarse, oracle_mod):
     """K = 4,000 of the 10,000 probed rows: t0 is low, each wave emits thousands of candidates per item,
-    far beyond its LDS region, and every item is redone on the direct path. A 65,536-entry candidate
-    buffer on both sides holds every candidate, so the emitted sets are compared whole."""
+    far beyond its LDS region, and its chunks are scanned again with fewer queries (down to 8, whose
+    candidates always fit). A 65,536-entry candidate buffer on both sides holds every candidate, so the
+    emitted sets are compared whole."""
     print("\n[gpu edges] emit region overflow: B=600 K=4000", flush=True)
     Q = datagen.gen(600, 768, 8, 0.7, seed=14, device="cuda", dtype=torch.float32)
     E = coarse["E"]
@@ -181,7 +182,7 @@ def test_index_build_is_deterministic():
 def test_emit_degenerate_row_scales(i8env, oracle_mod):
     """Rows whose code scale is +inf, negative or zero, in the cell the batch probes most. The emit scan's
     prefilter admits such a row for every query of a chunk (the exact test then decides), and a batch of
-    33 queries leaves partial 32-query tiles whose missing slots must admit nothing; the emitted sets, the
+    33 queries leaves partial 16-query tiles whose missing slots must admit nothing; the emitted sets, the
     counts and the final results must equal the oracle's canonical ones."""
     print("\n[gpu edges] planted +inf / negative / zero row scales, B=33", flush=True)
     E0 = i8env["E"]
