@@ -6,10 +6,10 @@
 // it streams the candidate's packed record in 128-byte units (the next unit in flight while one is
 // summed), looks up two LUT entries per code byte, and folds the per-tier integer sums into the f32
 // estimate in tier order. All lanes of a wave process the same record dword at the same time, so the
-// per-dword descriptor (LUT base, plane weight, end-of-tier and pair flags) is wave-uniform: the host
+// per-dword descriptor (LUT base, end-of-plane, end-of-tier and pair flags) is wave-uniform: the host
 // builds these descriptors once per record layout and passes them as a kernel argument, so they reach
 // scalar registers through the scalar cache; the lookups of one dword hit one 64-byte table (no LDS
-// bank conflicts), and the only branch, at a tier's end or a pair, is uniform.
+// bank conflicts), and the only branches, at a plane's or tier's end or a pair, are uniform.
 #include <type_traits>
 
 #include "fvs_common.h"
@@ -98,11 +98,14 @@ constexpr int kSetupPos = 4;         // FUSED: 4-coordinate table groups per thr
 // Schedule: one descriptor per record dword, the same for every record and query, built on the host and
 // passed as a kernel argument. Kernel arguments are read through the scalar cache, so a dword's descriptor
 // arrives in a scalar register with no vector instruction.
-//   bits 0-2   plane weight (shift); bits 3-5 are zero, so the word itself is a 64-bit shift amount
-//   bit 6      the dword ends a tier or is a (scale, sigma) pair: the one flag the summing loop tests
+//   bit 0      ends a plane that is not its tier's last: the tier sum is doubled after this dword
+//   bit 6      the dword ends a plane or tier or is a (scale, sigma) pair: the one flag the summing loop tests
 //   bit 7      ends a tier
 //   bit 8      is the (scale, sigma) pair of the next tier in order
 //   bits 9-16  byte offset of the dword's 512-byte table group in LDS (the zero table past the planes)
+// A tier's planes come most significant first, so its sum sum_p 2^(b-1-p) S_p is formed by Horner's rule:
+// every dword adds its entries unshifted and the sum doubles at each plane end but the last.
+constexpr uint32_t kSchedDouble = 1u << 0;
 constexpr uint32_t kSchedSpecial = 1u << 6;
 constexpr uint32_t kSchedLast = 1u << 7;
 constexpr uint32_t kSchedPair = 1u << 8;
@@ -338,6 +341,11 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
     // wave-uniform: skip waves whose lanes are all past the candidate list
     if (kScoreThreads * i + (tid & ~(FVS_WAVE - 1)) < lim) {
       int32_t va[8], vb[8];
+      // an even dword that is not special (no plane, tier or pair end) shares its plane with the next
+      // dword: its entries are carried in `pk` and added to the tier sum with the next dword's, so the
+      // 64-bit add happens once per pair. |entry| < 2^27 (the fixed-point exponent), so 16 entries fit
+      // in 32 bits.
+      int32_t pk = 0;
       lookup8(lutb, unit_word(cur, 0), sd[0] & kSchedBase, va);
 #pragma unroll
       for (int k = 0; k < kUD; k++) {
@@ -345,9 +353,12 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
         int32_t(&vn)[8] = (k & 1) ? va : vb;
         if (k + 1 < kUD) lookup8(lutb, unit_word(cur, k + 1), sd[k + 1] & kSchedBase, vn);
         const uint32_t dk = sd[k];
-        const int32_t part = vc[0] + vc[1] + vc[2] + vc[3] + vc[4] + vc[5] + vc[6] + vc[7];
-        acc += (int64_t)part << (dk & 63u);
+        const int32_t part = vc[0] + vc[1] + vc[2] + vc[3] + vc[4] + vc[5] + vc[6] + vc[7] + ((k & 1) ? pk : 0);
+        if ((k & 1) == 0) pk = part;
+        if ((k & 1) || (dk & kSchedSpecial)) acc += (int64_t)part;
         if (dk & kSchedSpecial) {
+          if ((k & 1) == 0) pk = 0;
+          if (dk & kSchedDouble) acc <<= 1;
           if (dk & kSchedLast) {
 #pragma unroll
             for (int t = TT - 1; t > 0; t--) tsum[t] = tsum[t - 1];
@@ -413,9 +424,9 @@ __global__ __launch_bounds__(kScoreThreads) void k_lut_score(
   }
 }
 
-// The schedule of a record layout (see ScoreSched): plane dwords look up their tier's tables with the
-// plane's weight, the T (scale, sigma) dwords after the planes and the padding up to whole units look up
-// the zero table with weight 1.
+// The schedule of a record layout (see ScoreSched): plane dwords look up their tier's tables and mark the
+// ends of planes and tiers; the T (scale, sigma) dwords after the planes and the padding up to whole units
+// look up the zero table.
 int build_sched(const TierArgs &ta, int nw, int U, int LW, ScoreSched *sc) {
   if (U * kUD > kSchedMax) return FVS_E_CAPACITY;
   const uint32_t zero = (uint32_t)LW * 4u;
@@ -433,8 +444,9 @@ int build_sched(const TierArgs &ta, int nw, int U, int LW, ScoreSched *sc) {
           const int j0 = rel - p * ta.kb[t];
           const uint32_t base = (uint32_t)(ta.loff[t] + 32 * j0) * 4u;  // byte offset of the dword's table group
           if ((base & ~kSchedBase) != 0) return FVS_E_SHAPE;
-          d = base | (uint32_t)(ta.bits[t] - 1 - p);
+          d = base;
           if (byte + 4 == ta.toff[t] + len) d |= kSchedSpecial | kSchedLast;
+          else if (j0 + 4 == ta.kb[t]) d |= kSchedSpecial | kSchedDouble;
         }
       }
     }
