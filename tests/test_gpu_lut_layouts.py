@@ -7,7 +7,8 @@ pairs whose entry sums are added together, the pairs that straddle a plane end, 
 dwords after the planes. Each layout runs with fp16 and fp32 tables (fvs_lut_build then fvs_lut_score)
 and with the tables formed inside the scorer (fvs_lut_score_zq), over all tiers and the leading ones, with
 delta-rule counts that leave some queries no candidate and others all of them. The records are random
-bytes with finite (scale, sigma) pairs; K = 300 takes two rounds of the scorer's 256 lanes."""
+bytes with finite (scale, sigma) pairs; K = 300 takes two rounds of the scorer's 256 lanes, and a second test
+runs K = 1, 63, 257 and 1000 (one to four rounds) with a delta-rule count above K."""
 import numpy as np
 import pytest
 import torch
@@ -77,3 +78,25 @@ def test_lut_scorer_layouts_match_oracle(name, oracle_mod):
                     tag = (name, form, half, nt, nc is None)
                     assert np.array_equal(npy(e).view(np.uint32), want_e.view(np.uint32)), tag
                     assert np.array_equal(npy(s).view(np.uint32), want_s.view(np.uint32)), tag
+
+
+@pytest.mark.parametrize("K", [1, 63, 257, 1000])
+def test_lut_scorer_candidate_counts_match_oracle(K, oracle_mod):
+    """Candidate counts that leave one lane, part of a wave, one lane of a second round and four rounds per
+    query, with delta-rule counts above K (clamped to K) among them: fused fp16 tables as the engine runs them."""
+    TS = LAYOUTS["planes_1_2_4_1"]
+    c = make_case(TS, seed=100 + K, N=3000, B=24, K=K)
+    c["ncnt"][2] = K + 5
+    dev = "cuda"
+    code = {"TS": TS, "rec": torch.from_numpy(c["rec"]).to(dev), "soff": c["soff"], "toff": c["toff"],
+            "deltas": c["deltas_by_bits"]}
+    deltas = np.asarray([c["deltas_by_bits"][b] for _, _, b in TS], np.float32)
+    L, qsum, qn2 = oracle_mod.lut_build(c["Zq"].view(np.uint16), TS, True)
+    want_e, want_s = oracle_mod.lut_score(c["pos"], c["qc"], L, True, qsum, qn2, c["rec"], c["soff"], TS, deltas,
+                                          np.asarray(c["toff"], np.int32), c["ncnt"])
+    e, s = _lib.lut_score(torch.from_numpy(c["pos"]).to(dev), torch.from_numpy(c["qc"]).to(dev),
+                          _lib.ZqTables(torch.from_numpy(c["Zq"]).to(dev), True), code,
+                          torch.from_numpy(c["ncnt"]).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(npy(e).view(np.uint32), want_e.view(np.uint32)), K
+    assert np.array_equal(npy(s).view(np.uint32), want_s.view(np.uint32)), K
