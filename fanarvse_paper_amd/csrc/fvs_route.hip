@@ -701,22 +701,38 @@ struct PairList {
 };
 
 // One wave per cell: its queries in ascending order, their probe ranks and pair constants, for one or
-// two lists. The rank and score rows are read kEmitU 16-byte pieces per lane at a time (2048 queries),
-// then wave prefix sums place each lane's pairs.
+// two lists. The rank and score rows are read kEmitU 16-byte pieces per lane at a time (2048 queries).
+// For each round of one piece per lane (512 queries), wave prefix sums place each lane's pairs in the
+// wave's LDS staging area in query order, and the wave then writes the round's pairs of each list out
+// with consecutive lanes on consecutive slots (whole-line stores instead of one scattered store per
+// pair and lane).
 constexpr int kEmitU = 4;
 
 template <bool TWO>
 __global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_emit(
     const uint16_t *__restrict__ rank, const uint16_t *__restrict__ score, int64_t Bp, const float *__restrict__ mnorm,
     const float *__restrict__ qadd, int NC, PairList la, PairList lb) {
+  // a piece round's pairs of each list, in order: (query, rank << 16 | score bits)
+  __shared__ uint2 stg[TWO ? 2 : 1][kCellWaves][8 * FVS_WAVE];
   const int lane = threadIdx.x & (FVS_WAVE - 1);
-  const int c = blockIdx.x * kCellWaves + fvs_wave_id();
+  const int wv = fvs_wave_id();
+  const int c = blockIdx.x * kCellWaves + wv;
   if (c >= NC) return;
   const uint4 *rr = reinterpret_cast<const uint4 *>(rank + (int64_t)c * Bp);
   const uint4 *ss = reinterpret_cast<const uint4 *>(score + (int64_t)c * Bp);
   const float sc = mnorm ? mnorm[c] : 1.0f;
   const int64_t nv = Bp / 8;
   int runa = la.coff[c], runb = TWO ? lb.coff[c] : 0;
+  auto flush = [&](const uint2 *st, int cnt, const PairList &l, int run) {
+    for (int j = lane; j < cnt; j += FVS_WAVE) {
+      const uint2 p = st[j];
+      float x = fvs_h2f((uint16_t)(p.y & 0xffffu)) * sc;
+      if (qadd) x = x + qadd[p.x];
+      l.qid[run + j] = (int32_t)p.x;
+      l.qrank[run + j] = (int32_t)(p.y >> 16);
+      l.qcp[run + j] = x;
+    }
+  };
   for (int64_t base = 0; base < nv; base += kEmitU * FVS_WAVE) {
     uint4 v[kEmitU], sv[kEmitU];
 #pragma unroll
@@ -725,47 +741,36 @@ __global__ __launch_bounds__(kCellWaves * FVS_WAVE) void k_cell_emit(
       v[u] = i < nv ? rr[i] : make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
       sv[u] = i < nv ? ss[i] : make_uint4(0, 0, 0, 0);
     }
-    int oa[kEmitU], ob[kEmitU];
 #pragma unroll
     for (int u = 0; u < kEmitU; u++) {
       const int ma = below8(v[u], la.n);
       const int ia = wave_incl_scan_i32(ma, lane);
-      oa[u] = runa + ia - ma;
-      runa += __builtin_amdgcn_readlane(ia, FVS_WAVE - 1);
+      const int ta = __builtin_amdgcn_readlane(ia, FVS_WAVE - 1);
+      int oa = ia - ma, ob = 0, tb = 0;
       if (TWO) {
         const int mb = below8(v[u], lb.n);
         const int ib = wave_incl_scan_i32(mb, lane);
-        ob[u] = runb + ib - mb;
-        runb += __builtin_amdgcn_readlane(ib, FVS_WAVE - 1);
+        tb = __builtin_amdgcn_readlane(ib, FVS_WAVE - 1);
+        ob = ib - mb;
       }
-    }
-#pragma unroll
-    for (int u = 0; u < kEmitU; u++) {
       const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
       const uint32_t hw[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const uint32_t r = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
-        const bool ina = r < la.n, inb = TWO && r < lb.n;
-        if (ina || inb) {
-          const int64_t q = (base + u * FVS_WAVE + lane) * 8 + e;
-          const uint32_t h = (e & 1) ? (hw[e >> 1] >> 16) : (hw[e >> 1] & 0xffffu);
-          float x = fvs_h2f((uint16_t)h) * sc;
-          if (qadd) x = x + qadd[q];
-          if (ina) {
-            la.qid[oa[u]] = (int32_t)q;
-            la.qrank[oa[u]] = (int32_t)r;
-            la.qcp[oa[u]] = x;
-            oa[u]++;
-          }
-          if (inb) {
-            lb.qid[ob[u]] = (int32_t)q;
-            lb.qrank[ob[u]] = (int32_t)r;
-            lb.qcp[ob[u]] = x;
-            ob[u]++;
-          }
-        }
+        const uint32_t h = (e & 1) ? (hw[e >> 1] >> 16) : (hw[e >> 1] & 0xffffu);
+        const uint32_t q = (uint32_t)((base + u * FVS_WAVE + lane) * 8 + e);
+        if (r < la.n) stg[0][wv][oa++] = make_uint2(q, (r << 16) | h);
+        if (TWO && r < lb.n) stg[TWO ? 1 : 0][wv][ob++] = make_uint2(q, (r << 16) | h);
       }
+      wave_lds_sync();
+      flush(stg[0][wv], ta, la, runa);
+      runa += ta;
+      if (TWO) {
+        flush(stg[TWO ? 1 : 0][wv], tb, lb, runb);
+        runb += tb;
+      }
+      wave_lds_sync();
     }
   }
 }
